@@ -1,0 +1,430 @@
+/*
+ * dfssm_oracle.c -- CPU restatement of the DF-SSM per-token decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker for the HIP path; only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The product path never
+ * links or calls it.
+ *
+ * Two families of functions:
+ *
+ *  or_*    the GPU-reference numerics: the dataflow and fp16 rounding points of
+ *          inference/gpu/df_ssm_inference.py:141-224 and the conv/SSM arithmetic of
+ *          inference/gpu/df_ssm_kernels.cu:27-103, with two deliberate changes the benchmark
+ *          configuration asks for: the SSM state is fp32 (reference: fp16) and the SSM head
+ *          dimension is d_inner/nheads (reference: hard-coded 32). Activations are fp16 bit
+ *          patterns (uint16_t); weights are passed exactly as stored in the .dfssm file.
+ *
+ *  or_c_*  the CPU-reference numerics of inference/cpu/cpu_inference.c (fp32 activations,
+ *          asymmetric uint8 activation quantizer with a popcount row-sum correction). These
+ *          exist so that the restated dataflow can be compared with the compiled reference
+ *          layer_forward (cpu_inference.c:303-376) built with HEADDIM=64.
+ *
+ * Sums over a vector are accumulated in double and rounded once to fp32; the reference sums in
+ * fp32 in an order that no reference test fixes, so sums carry a tolerance, not bit-exactness.
+ * Integer work (bit unpack, scaffold accumulators, quantized values) is exact.
+ *
+ * fp32 -> fp16 conversion is round-to-nearest-even with IEEE overflow to inf, the behaviour
+ * of __float2half and of torch's Half conversion; it is checked exhaustively against numpy.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define LORA_R 16
+
+/* ---------------------------------------------------------------- fp16 <-> fp32 ------------ */
+
+float or_h2f(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
+  if (e == 0) {
+    float f = (float)m * 5.9604644775390625e-8f; /* m * 2^-24, exact */
+    memcpy(&bits, &f, 4);
+    bits |= sign;
+  } else if (e == 31) {
+    bits = sign | 0x7f800000u | (m << 13);
+  } else {
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t or_f2h(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);          /* NaN */
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);         /* >= 65520 -> inf */
+  if (ax < 0x38800000u) {                                            /* below 2^-14 */
+    float af;
+    memcpy(&af, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)rintf(af * 16777216.0f));     /* units of 2^-24, RNE */
+  }
+  uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
+  uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+  return (uint16_t)(sign | h);
+}
+
+static inline uint16_t r16(double v) { return or_f2h((float)v); }
+static inline float hf(uint16_t h) { return or_h2f(h); }
+
+void or_f2h_array(const float* in, uint16_t* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_f2h(in[i]); }
+void or_h2f_array(const uint16_t* in, float* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_h2f(in[i]); }
+
+/* ---------------------------------------------------------------- bits (row a2) ------------ */
+
+/* Word j, bit b of row n is column 32j+b; bit 1 -> +1, bit 0 -> -1.
+ * export_dfssm.py:34-42 (pack), df_ssm_inference.py:23-29 (unpack), cpu_inference.c:126-128. */
+void or_unpack_bits(const uint32_t* packed, int rows, int kwords, int8_t* out) {
+  for (long r = 0; r < rows; ++r)
+    for (int j = 0; j < kwords; ++j) {
+      uint32_t w = packed[r * kwords + j];
+      for (int b = 0; b < 32; ++b) out[r * kwords * 32 + j * 32 + b] = ((w >> b) & 1u) ? 1 : -1;
+    }
+}
+
+/* ---------------------------------------------------------------- scaffold (row a5) -------- */
+
+/* acc[m][n] = sum_k q[m][k] * w[n][k], exact int32 (torch._int_mm, df_ssm_inference.py:157). */
+void or_scaffold_acc(const uint32_t* bits, const int8_t* q, int M, int N, int K, int32_t* acc) {
+  const int kw = K / 32;
+#pragma omp parallel
+  {
+    int8_t* w = (int8_t*)malloc((size_t)K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      or_unpack_bits(bits + (size_t)n * kw, 1, kw, w);
+      for (int m = 0; m < M; ++m) {
+        const int8_t* qm = q + (size_t)m * K;
+        int32_t s = 0;
+        for (int k = 0; k < K; ++k) s += (int32_t)qm[k] * (int32_t)w[k];
+        acc[(size_t)m * N + n] = s;
+      }
+    }
+    free(w);
+  }
+}
+
+/* ---------------------------------------------------------------- norms (rows a3, a9) ------ */
+
+/* out = fp16((fp32(x) * r) * w), r = 1/sqrt(sum(x^2) * (1/K) + 1e-5) in fp32.
+ * _rms_norm, df_ssm_inference.py:141-145, followed by copy_ into an fp16 buffer (:165,196,210).
+ * The mean is sum * (1/K) as ATen's mean reduction computes it. */
+void or_rmsnorm(const uint16_t* x, const float* w, int M, int K, uint16_t* out) {
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* xm = x + (size_t)m * K;
+    double ss = 0.0;
+    for (int k = 0; k < K; ++k) { double v = hf(xm[k]); ss += v * v; }
+    float var = (float)ss * (1.0f / (float)K);
+    float r = 1.0f / sqrtf(var + 1e-5f);
+    for (int k = 0; k < K; ++k) out[(size_t)m * K + k] = or_f2h((hf(xm[k]) * r) * w[k]);
+  }
+}
+
+/* ---------------------------------------------------------------- quantizer (row a4) ------- */
+
+/* _quantize_to_int8, df_ssm_inference.py:147-152:
+ *   s = fp16(fp16(max(amax|x|, 1e-4)) * (1/127))   (ATen divides a tensor by a CPU scalar
+ *                                                     by multiplying with its fp32 reciprocal)
+ *   q = clamp(rne(fp16(x / s)), -128, 127)          (tensor/tensor division is IEEE fp32) */
+void or_quantize(const uint16_t* xn, int M, int K, int8_t* q, uint16_t* s) {
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* xm = xn + (size_t)m * K;
+    float amax = 0.0f;
+    for (int k = 0; k < K; ++k) { float a = fabsf(hf(xm[k])); if (a > amax) amax = a; }
+    float c = hf(or_f2h(amax > 1e-4f ? amax : 1e-4f));
+    uint16_t sh = or_f2h(c * (1.0f / 127.0f));
+    s[m] = sh;
+    float sf = hf(sh);
+    for (int k = 0; k < K; ++k) {
+      float t = rintf(hf(or_f2h(hf(xm[k]) / sf)));
+      if (t > 127.0f) t = 127.0f;
+      if (t < -128.0f) t = -128.0f;
+      q[(size_t)m * K + k] = (int8_t)t;
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- LoRA + dequant (a5, a6) -- */
+
+/* h16[m][r] = fp16(sum_k xn[m][k] * B16[r][k]) with B16 = fp16(B_i8 * B_s[r]) (the load-time
+ * dequant of df_ssm_inference.py:83, then the fp16 GEMM x_norm @ lora_B.T of :173). */
+void or_lora_h(const uint16_t* xn, const int8_t* lB, const uint16_t* lBs, int M, int K, uint16_t* h16) {
+  for (int m = 0; m < M; ++m)
+    for (int r = 0; r < LORA_R; ++r) {
+      float bs = hf(lBs[r]);
+      double s = 0.0;
+      for (int k = 0; k < K; ++k) {
+        float b16 = hf(or_f2h((float)lB[(size_t)r * K + k] * bs));
+        s += (double)hf(xn[(size_t)m * K + k]) * (double)b16;
+      }
+      h16[m * LORA_R + r] = r16(s);
+    }
+}
+
+/* out[m][n] = fp16(y + sum_r h16[m][r] * A16[n][r]) where
+ *   y   = fp16(fp16(fp16(acc) * xs[m]) * ws[n])   (_scaffold_matmul, df_ssm_inference.py:158)
+ *   A16 = fp16(A_i8 * A_s[n])                       (load-time dequant, :82)
+ * and the sum is the fp32 addmm_ of :173 / :204. */
+void or_dequant_lora(const int32_t* acc, const uint16_t* xs, const uint16_t* ws, const uint16_t* h16,
+                     const int8_t* lA, const uint16_t* lAs, int M, int N, uint16_t* out) {
+  for (int m = 0; m < M; ++m)
+    for (int n = 0; n < N; ++n) {
+      float a16 = hf(or_f2h((float)acc[(size_t)m * N + n]));
+      float y = hf(or_f2h(hf(or_f2h(a16 * hf(xs[m]))) * hf(ws[n])));
+      float as = hf(lAs[n]);
+      double s = 0.0;
+      for (int r = 0; r < LORA_R; ++r) {
+        float a = hf(or_f2h((float)lA[(size_t)n * LORA_R + r] * as));
+        s += (double)hf(h16[m * LORA_R + r]) * (double)a;
+      }
+      out[(size_t)m * N + n] = or_f2h((float)s + y);
+    }
+}
+
+/* ---------------------------------------------------------------- conv (row a7) ------------ */
+
+/* conv_step_kernel, df_ssm_kernels.cu:27-47: out = s0*w0 + s1*w1 + s2*w2 + x*w3 + b (fp32,
+ * left to right), state <- (s1, s2, x), x <- fp16(out * 1/(1+exp(-out))). Products of two fp16
+ * values are exact in fp32, so the order of additions is the only rounding choice. */
+void or_conv_step(uint16_t* state, uint16_t* xbc, int ld, const uint16_t* w, const uint16_t* b, int M, int C) {
+  for (int m = 0; m < M; ++m)
+    for (int ch = 0; ch < C; ++ch) {
+      uint16_t* cs = state + ((size_t)m * C + ch) * 3;
+      uint16_t* xp = xbc + (size_t)m * ld + ch;
+      float s0 = hf(cs[0]), s1 = hf(cs[1]), s2 = hf(cs[2]), xv = hf(*xp);
+      cs[0] = cs[1];
+      cs[1] = cs[2];
+      cs[2] = *xp;
+      const uint16_t* wc = w + (size_t)ch * 4;
+      float o = s0 * hf(wc[0]);
+      o = o + s1 * hf(wc[1]);
+      o = o + s2 * hf(wc[2]);
+      o = o + xv * hf(wc[3]);
+      o = o + hf(b[ch]);
+      float sig = 1.0f / (1.0f + expf(-o));
+      *xp = or_f2h(o * sig);
+    }
+}
+
+/* ---------------------------------------------------------------- SSM (row a8) ------------- */
+
+/* ssm_step_kernel, df_ssm_kernels.cu:53-103, with an fp32 state and P = d_inner/nheads:
+ *   dt = log1p(exp(dt_raw + dt_bias)); Abar = exp(dt * -exp(A_log))
+ *   h[p][n] = fma(Abar, h[p][n], (x_p * dt) * B_n)
+ *   y_p = fp16(sum_n C_n * h[p][n] + x_p * D)
+ * x = xbc[0:DI], B = xbc[DI:DI+N], C = xbc[DI+N:DI+2N] (ngroups = 1: B and C shared by all heads,
+ * df_ssm_inference.py:185-187). */
+void or_ssm_step(float* h, const uint16_t* xbc, int ld_xbc, const uint16_t* dt_raw, int ld_dt,
+                 const float* dt_bias, const float* A_log, const float* Dp,
+                 int M, int H, int P, int N, uint16_t* y) {
+  const int DI = H * P;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int m = 0; m < M; ++m)
+    for (int hd = 0; hd < H; ++hd) {
+      const uint16_t* xr = xbc + (size_t)m * ld_xbc;
+      float dt = log1pf(expf(hf(dt_raw[(size_t)m * ld_dt + hd]) + dt_bias[hd]));
+      float abar = expf(dt * -expf(A_log[hd]));
+      for (int p = 0; p < P; ++p) {
+        float xv = hf(xr[hd * P + p]);
+        float X = xv * dt;
+        float* hp = h + (((size_t)m * H + hd) * P + p) * N;
+        double acc = 0.0;
+        for (int n = 0; n < N; ++n) {
+          float hn = fmaf(abar, hp[n], X * hf(xr[DI + n]));
+          hp[n] = hn;
+          acc += (double)hf(xr[DI + N + n]) * (double)hn;
+        }
+        y[(size_t)m * DI + hd * P + p] = or_f2h((float)acc + xv * Dp[hd]);
+      }
+    }
+}
+
+/* ---------------------------------------------------------------- gate (row a9) ------------ */
+
+/* g = fp16(y * fp16(z * fp16(sigmoid(z)))) -- the three fp16 tensor ops of
+ * df_ssm_inference.py:194-195; the gated RMSNorm is or_rmsnorm on g. */
+void or_gate(const uint16_t* y, const uint16_t* z, int ld_z, int M, int DI, uint16_t* g) {
+  for (int m = 0; m < M; ++m)
+    for (int k = 0; k < DI; ++k) {
+      float zv = hf(z[(size_t)m * ld_z + k]);
+      float sg = hf(or_f2h(1.0f / (1.0f + expf(-zv))));
+      float sz = hf(or_f2h(zv * sg));
+      g[(size_t)m * DI + k] = or_f2h(hf(y[(size_t)m * DI + k]) * sz);
+    }
+}
+
+/* ---------------------------------------------------------------- residual (row a10) ------- */
+
+void or_residual(uint16_t* x, const uint16_t* o, int M, int D) {
+  for (long i = 0; i < (long)M * D; ++i) x[i] = or_f2h(hf(x[i]) + hf(o[i]));
+}
+
+/* ---------------------------------------------------------------- embedding, head (a11) ---- */
+
+/* x0 = E16[tok] with E16 = fp16(E_i8 * s_E) for the int8 table (emb_code 1) or the stored fp16
+ * table (emb_code 0); df_ssm_inference.py:220. */
+void or_embed(const int8_t* E8, const uint16_t* sE, const uint16_t* E16, int emb_code,
+              const int64_t* tok, int M, int D, uint16_t* x) {
+  for (int m = 0; m < M; ++m) {
+    long t = (long)tok[m];
+    for (int k = 0; k < D; ++k)
+      x[(size_t)m * D + k] = emb_code ? or_f2h((float)E8[t * D + k] * hf(sE[t])) : E16[t * D + k];
+  }
+}
+
+/* logits[m][v] = fp16(sum_k xf[m][k] * E[v][k]) (tied head, df_ssm_inference.py:224). For the
+ * int8 table the row scale is applied after the dot product: fp16(fp32(dot) * s_E[v]).
+ * next[m] = first index of the maximum fp16 logit (torch.argmax, :236). */
+void or_lm_head(const uint16_t* xf, const int8_t* E8, const uint16_t* sE, const uint16_t* E16, int emb_code,
+                int M, int V, int D, uint16_t* logits, int64_t* next) {
+#pragma omp parallel for schedule(static)
+  for (int v = 0; v < V; ++v)
+    for (int m = 0; m < M; ++m) {
+      double s = 0.0;
+      const uint16_t* xm = xf + (size_t)m * D;
+      if (emb_code) {
+        const int8_t* e = E8 + (size_t)v * D;
+        for (int k = 0; k < D; ++k) s += (double)hf(xm[k]) * (double)e[k];
+        logits[(size_t)m * V + v] = or_f2h((float)s * hf(sE[v]));
+      } else {
+        const uint16_t* e = E16 + (size_t)v * D;
+        for (int k = 0; k < D; ++k) s += (double)hf(xm[k]) * (double)hf(e[k]);
+        logits[(size_t)m * V + v] = r16(s);
+      }
+    }
+  for (int m = 0; m < M; ++m) {
+    int64_t best = 0;
+    float bv = hf(logits[(size_t)m * V]);
+    for (int v = 1; v < V; ++v) {
+      float lv = hf(logits[(size_t)m * V + v]);
+      if (lv > bv) { bv = lv; best = v; }
+    }
+    next[m] = best;
+  }
+}
+
+/* ================================================================ CPU-reference numerics ==== */
+
+/* rms_norm, cpu_inference.c:34-52: out = (x * w) * (1/sqrt(ss/dim + 1e-5)). */
+void or_c_rms_norm(const float* x, const float* w, float* out, int M, int dim) {
+  for (int m = 0; m < M; ++m) {
+    const float* xm = x + (size_t)m * dim;
+    double ss = 0.0;
+    for (int i = 0; i < dim; ++i) ss += (double)xm[i] * xm[i];
+    float inv = 1.0f / sqrtf((float)ss / dim + 1e-5f);
+    for (int i = 0; i < dim; ++i) out[(size_t)m * dim + i] = xm[i] * w[i] * inv;
+  }
+}
+
+/* quantize_input_uint8, cpu_inference.c:65-97: s = 255/(2 max(amax, 1e-8)),
+ * q = rne(clamp(x*s + 128, 0, 255)), x_scale = 1/s. */
+void or_c_quantize_u8(const float* x, int K, uint8_t* q, float* x_scale) {
+  float amax = 0.0f;
+  for (int i = 0; i < K; ++i) { float a = fabsf(x[i]); if (a > amax) amax = a; }
+  if (amax < 1e-8f) amax = 1e-8f;
+  float s = 255.0f / (2.0f * amax);
+  *x_scale = 1.0f / s;
+  for (int i = 0; i < K; ++i) {
+    float v = x[i] * s + 128.0f;
+    if (v < 0.0f) v = 0.0f;
+    if (v > 255.0f) v = 255.0f;
+    q[i] = (uint8_t)rintf(v);
+  }
+}
+
+/* scaffold_matvec_avx512, cpu_inference.c:99-151, with precompute_row_sums (:286-299):
+ * out = fp32(dot(u8, +-1) - 128 * rowsum) * x_scale * scale. */
+void or_c_scaffold(const uint32_t* bits, const float* x, const float* scale, int M, int N, int K, float* out) {
+  const int kw = K / 32;
+  uint8_t* q = (uint8_t*)malloc((size_t)K);
+  for (int m = 0; m < M; ++m) {
+    float xs;
+    or_c_quantize_u8(x + (size_t)m * K, K, q, &xs);
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      const uint32_t* row = bits + (size_t)n * kw;
+      int32_t dot = 0, pop = 0;
+      for (int j = 0; j < kw; ++j) {
+        pop += __builtin_popcount(row[j]);
+        for (int b = 0; b < 32; ++b) dot += ((row[j] >> b) & 1u) ? (int32_t)q[j * 32 + b] : -(int32_t)q[j * 32 + b];
+      }
+      int32_t rowsum = 2 * pop - K;
+      out[(size_t)m * N + n] = (float)(dot - 128 * rowsum) * xs * scale[n];
+    }
+  }
+  free(q);
+}
+
+/* lora_matvec, cpu_inference.c:155-194: h[r] = (B[r].x) * Bs[r]; out[n] += (A[n].h) * As[n]. */
+void or_c_lora(const int8_t* A, const float* As, const int8_t* B, const float* Bs, const float* x,
+               float* out, int M, int N, int K) {
+  for (int m = 0; m < M; ++m) {
+    float hr[LORA_R];
+    for (int r = 0; r < LORA_R; ++r) {
+      double s = 0.0;
+      for (int k = 0; k < K; ++k) s += (double)B[(size_t)r * K + k] * x[(size_t)m * K + k];
+      hr[r] = (float)s * Bs[r];
+    }
+    for (int n = 0; n < N; ++n) {
+      float s = 0.0f;
+      for (int r = 0; r < LORA_R; ++r) s += (float)A[(size_t)n * LORA_R + r] * hr[r];
+      out[(size_t)m * N + n] += s * As[n];
+    }
+  }
+}
+
+/* conv_step, cpu_inference.c:204-227 (fp32 state). */
+void or_c_conv(float* state, float* xbc, int ld, const float* w, const float* b, int M, int C) {
+  for (int m = 0; m < M; ++m)
+    for (int ch = 0; ch < C; ++ch) {
+      float* cs = state + ((size_t)m * C + ch) * 3;
+      float* xp = xbc + (size_t)m * ld + ch;
+      float s0 = cs[0], s1 = cs[1], s2 = cs[2], xv = *xp;
+      cs[0] = s1; cs[1] = s2; cs[2] = xv;
+      float o = s0 * w[ch * 4 + 0] + s1 * w[ch * 4 + 1] + s2 * w[ch * 4 + 2] + xv * w[ch * 4 + 3] + b[ch];
+      *xp = o / (1.0f + expf(-o));
+    }
+}
+
+/* softplus in layer_forward (cpu_inference.c:352-355) + ssm_step (:231-262). */
+void or_c_ssm(float* h, const float* xbc, int ld, const float* dt_raw, int ld_dt, const float* dt_bias,
+              const float* A_log, const float* Dp, int M, int H, int P, int N, float* y) {
+  const int DI = H * P;
+  for (int m = 0; m < M; ++m)
+    for (int hd = 0; hd < H; ++hd) {
+      const float* xr = xbc + (size_t)m * ld;
+      float dt = log1pf(expf(dt_raw[(size_t)m * ld_dt + hd] + dt_bias[hd]));
+      float abar = expf(dt * -expf(A_log[hd]));
+      for (int p = 0; p < P; ++p) {
+        float xv = xr[hd * P + p], X = xv * dt;
+        float* hp = h + (((size_t)m * H + hd) * P + p) * N;
+        double acc = 0.0;
+        for (int n = 0; n < N; ++n) {
+          float hn = abar * hp[n] + X * xr[DI + n];
+          hp[n] = hn;
+          acc += (double)xr[DI + N + n] * hn;
+        }
+        y[(size_t)m * DI + hd * P + p] = (float)acc + xv * Dp[hd];
+      }
+    }
+}
+
+/* gate_norm, cpu_inference.c:266-278: g = y * silu(z); out = g * inv_rms * w. */
+void or_c_gate_norm(const float* y, const float* z, int ld_z, const float* w, float* out, int M, int DI) {
+  for (int m = 0; m < M; ++m) {
+    double ss = 0.0;
+    for (int i = 0; i < DI; ++i) {
+      float zv = z[(size_t)m * ld_z + i];
+      float g = y[(size_t)m * DI + i] * (zv / (1.0f + expf(-zv)));
+      out[(size_t)m * DI + i] = g;
+      ss += (double)g * g;
+    }
+    float inv = 1.0f / sqrtf((float)ss / DI + 1e-5f);
+    for (int i = 0; i < DI; ++i) out[(size_t)m * DI + i] = out[(size_t)m * DI + i] * inv * w[i];
+  }
+}
