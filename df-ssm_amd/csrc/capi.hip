@@ -1,0 +1,299 @@
+// C ABI of libdfssm_hip.so: argument validation, workspace layout and launch sequencing.
+// Declarations and conventions: include/dfssm.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dfssm.h"
+#include "dfssm_kernels.h"
+
+using namespace dfssm;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+struct Derived {
+  int B, L, D, DI, N, H, P, V, IPO, C, n_slots, head_groups;
+};
+
+Derived derive(const dfssm_dims* d) {
+  Derived r;
+  r.B = d->batch; r.L = d->n_layer; r.D = d->d_model; r.DI = d->d_inner; r.N = d->d_state;
+  r.H = d->nheads; r.P = d->nheads > 0 ? d->d_inner / d->nheads : 0; r.V = d->vocab_size;
+  r.C = r.DI + 2 * d->ngroups * r.N;
+  r.IPO = 2 * r.DI + 2 * d->ngroups * r.N + r.H;
+  r.n_slots = r.P > 0 ? r.H * (r.P / 16) : 0;
+  r.head_groups = (r.V + 63) / 64;
+  return r;
+}
+
+struct WsLayout {
+  size_t proj, g, slots, part_val, part_idx, ticket, err, total;
+};
+
+WsLayout ws_layout(const dfssm_dims* d) {
+  const Derived r = derive(d);
+  WsLayout w;
+  size_t off = 0;
+  w.proj = off;     off = align_up(off + (size_t)r.B * r.IPO * 2);
+  w.g = off;        off = align_up(off + (size_t)r.B * r.DI * 2);
+  w.slots = off;    off = align_up(off + (size_t)r.B * r.n_slots * 8);
+  w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
+  w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
+  w.ticket = off;   off = align_up(off + 4);
+  w.err = off;      off = align_up(off + 4);
+  w.total = off;
+  return w;
+}
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool kdim_ok(int k) { return k > 0 && k % 512 == 0 && k <= 8192; }
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dfssm_version(void) { return DFSSM_ABI_VERSION; }
+
+const char* dfssm_error_string(int code) {
+  switch (code) {
+    case DFSSM_OK: return "ok";
+    case DFSSM_E_NULL: return "required pointer is NULL";
+    case DFSSM_E_DIMS: return "model dimensions not supported by the kernels";
+    case DFSSM_E_BATCH: return "batch size not supported (1..4)";
+    case DFSSM_E_ALIGN: return "pointer or leading dimension misaligned (16-byte rows required)";
+    case DFSSM_E_RANGE: return "index out of range";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}
+
+int dfssm_check_dims(const dfssm_dims* d) {
+  if (!d) return DFSSM_E_NULL;
+  if (d->n_layer <= 0 || d->vocab_size <= 0 || d->nheads <= 0) return DFSSM_E_DIMS;
+  if (!kdim_ok(d->d_model) || !kdim_ok(d->d_inner)) return DFSSM_E_DIMS;
+  if (d->d_state != 128 || d->ngroups != 1 || d->emb_code != 1) return DFSSM_E_DIMS;
+  if (d->d_inner % d->nheads) return DFSSM_E_DIMS;
+  const int P = d->d_inner / d->nheads;
+  if (P % 16 || d->nheads % 8) return DFSSM_E_DIMS;
+  if (d->batch < 1 || d->batch > 4) return DFSSM_E_BATCH;
+  return DFSSM_OK;
+}
+
+size_t dfssm_tiled_bits_bytes(int rows, int k) {
+  if (rows <= 0 || k <= 0) return 0;
+  return (size_t)((rows + 63) / 64 * 64) * (size_t)(k / 32) * 4;
+}
+
+size_t dfssm_tiled_emb_bytes(int vocab, int d_model) {
+  if (vocab <= 0 || d_model <= 0) return 0;
+  return (size_t)((vocab + 63) / 64 * 64) * (size_t)d_model;
+}
+
+int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* stream) {
+  if (!src || !dst) return DFSSM_E_NULL;
+  if (rows <= 0 || !kdim_ok(k)) return DFSSM_E_DIMS;
+  return hip_status(launch_tile_bits(src, dst, rows, k / 32, as_stream(stream)));
+}
+
+int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream) {
+  if (!src || !dst) return DFSSM_E_NULL;
+  if (vocab <= 0 || d_model <= 0 || d_model % 64) return DFSSM_E_DIMS;
+  if (((uintptr_t)src & 3u) || !aligned16(dst)) return DFSSM_E_ALIGN;
+  return hip_status(launch_tile_emb(src, dst, vocab, d_model, as_stream(stream)));
+}
+
+int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
+                        const uint16_t* wscale, int M, int N, int K, int32_t* acc_out,
+                        uint16_t* y_out, void* stream) {
+  if (!tiled_bits || !q || (!acc_out && !y_out)) return DFSSM_E_NULL;
+  if (y_out && (!xscale || !wscale)) return DFSSM_E_NULL;
+  if (M < 1 || M > 4) return DFSSM_E_BATCH;
+  if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
+  if (!aligned16(tiled_bits)) return DFSSM_E_ALIGN;
+  ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, N, K};
+  return hip_status(launch_scaffold(a, M, as_stream(stream)));
+}
+
+int dfssm_rmsnorm_quantize(const uint16_t* x, const float* w, int M, int K, uint16_t* xn_out,
+                           int8_t* q_out, uint16_t* s_out, void* stream) {
+  if (!x || !w || !xn_out || !q_out || !s_out) return DFSSM_E_NULL;
+  if (M < 1 || !kdim_ok(K)) return DFSSM_E_DIMS;
+  ProjArgs a{};
+  a.act = x;
+  a.ld_act = K;
+  a.norm_w = w;
+  a.K = K;
+  return hip_status(launch_prologue(a, M, xn_out, q_out, s_out, as_stream(stream)));
+}
+
+int dfssm_conv_step(uint16_t* conv_state, uint16_t* xbc, int ld_xbc, const uint16_t* conv_w,
+                    const uint16_t* conv_b, int batch, int channels, void* stream) {
+  if (!conv_state || !xbc || !conv_w || !conv_b) return DFSSM_E_NULL;
+  if (batch < 1 || channels < 1 || ld_xbc < channels) return DFSSM_E_DIMS;
+  ConvArgs a{conv_state, xbc, conv_w, conv_b, ld_xbc, channels};
+  return hip_status(launch_conv(a, batch, as_stream(stream)));
+}
+
+int dfssm_ssm_step(float* h_state, const uint16_t* xbc, int ld_xbc, const uint16_t* dt, int ld_dt,
+                   const float* dt_bias, const float* A_log, const float* D, uint16_t* y_out,
+                   int ld_y, int batch, int nheads, int headdim, int d_state, void* stream) {
+  if (!h_state || !xbc || !dt || !dt_bias || !A_log || !D || !y_out) return DFSSM_E_NULL;
+  if (batch < 1 || nheads < 1 || headdim < 16 || headdim % 16 || d_state != 128) return DFSSM_E_DIMS;
+  const int DI = nheads * headdim;
+  if (ld_xbc < DI + 2 * d_state || ld_dt < nheads || ld_y < DI) return DFSSM_E_DIMS;
+  if (!aligned16(h_state) || !aligned16(xbc) || (ld_xbc % 8) || (DI % 8)) return DFSSM_E_ALIGN;
+  SsmArgs a{};
+  a.h = h_state;
+  a.xbc = xbc; a.ld_xbc = ld_xbc;
+  a.dt = dt; a.ld_dt = ld_dt;
+  a.z = nullptr; a.ld_z = 0;
+  a.dt_bias = dt_bias; a.A_log = A_log; a.D = D;
+  a.y_out = y_out; a.ld_y = ld_y;
+  a.sumsq_slots = nullptr; a.n_slots = 0;
+  a.H = nheads; a.P = headdim; a.N = d_state;
+  return hip_status(launch_ssm(a, batch, as_stream(stream)));
+}
+
+size_t dfssm_workspace_bytes(const dfssm_dims* dims) {
+  if (!dims || dfssm_check_dims(dims) != DFSSM_OK) return 0;
+  return ws_layout(dims).total;
+}
+
+int dfssm_workspace_init(const dfssm_dims* dims, void* workspace, void* stream) {
+  if (!dims || !workspace) return DFSSM_E_NULL;
+  int rc = dfssm_check_dims(dims);
+  if (rc) return rc;
+  const WsLayout w = ws_layout(dims);
+  // ticket and error flag are adjacent 256-byte slots; clear both with a fill kernel
+  uint32_t* p = (uint32_t*)((char*)workspace + w.ticket);
+  const int n = (int)((w.total - w.ticket) / 4);
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, as_stream(stream), p, n);
+  return hip_status(hipGetLastError());
+}
+
+int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace) {
+  if (!dims || !workspace || dfssm_check_dims(dims) != DFSSM_OK) return nullptr;
+  return (int*)((char*)workspace + ws_layout(dims).err);
+}
+
+static int check_model(const dfssm_model* model) {
+  if (!model || !model->layers || !model->emb || !model->emb_scale || !model->norm_f) return DFSSM_E_NULL;
+  int rc = dfssm_check_dims(&model->dims);
+  if (rc) return rc;
+  if (!aligned16(model->emb)) return DFSSM_E_ALIGN;
+  return DFSSM_OK;
+}
+
+int dfssm_embed(const dfssm_model* model, const int64_t* tokens, uint16_t* x, void* workspace,
+                void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!tokens || !x || !workspace) return DFSSM_E_NULL;
+  const Derived r = derive(&model->dims);
+  EmbedArgs a{tokens, model->emb, model->emb_scale, x,
+              (int*)((char*)workspace + ws_layout(&model->dims).err), r.V, r.D};
+  return hip_status(launch_embed(a, r.B, as_stream(stream)));
+}
+
+int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                     void* workspace, void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!x || !state || !state->h || !state->conv || !workspace) return DFSSM_E_NULL;
+  const Derived r = derive(&model->dims);
+  if (layer < 0 || layer >= r.L) return DFSSM_E_RANGE;
+  const dfssm_layer& Lw = model->layers[layer];
+  if (!Lw.in_bits || !Lw.in_scale || !Lw.in_lA || !Lw.in_lA_s || !Lw.in_lB || !Lw.in_lB_s ||
+      !Lw.out_bits || !Lw.out_scale || !Lw.out_lA || !Lw.out_lA_s || !Lw.out_lB || !Lw.out_lB_s ||
+      !Lw.conv_w || !Lw.conv_b || !Lw.A_log || !Lw.D || !Lw.dt_bias || !Lw.norm_w || !Lw.ln_w)
+    return DFSSM_E_NULL;
+  if (!aligned16(Lw.in_bits) || !aligned16(Lw.out_bits) || !aligned16(Lw.in_lA) ||
+      !aligned16(Lw.out_lA) || !aligned16(state->h) || ((uintptr_t)Lw.in_lB & 3u) ||
+      ((uintptr_t)Lw.out_lB & 3u) || !aligned16(workspace))
+    return DFSSM_E_ALIGN;
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  uint16_t* proj = (uint16_t*)(ws + w.proj);
+  uint16_t* g = (uint16_t*)(ws + w.g);
+  double* slots = (double*)(ws + w.slots);
+  hipStream_t s = as_stream(stream);
+  float* h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
+  uint16_t* conv = state->conv + (size_t)layer * r.B * r.C * 3;
+
+  ProjArgs ai{};
+  ai.bits = Lw.in_bits; ai.wscale = Lw.in_scale; ai.lA = Lw.in_lA; ai.lAs = Lw.in_lA_s;
+  ai.lB = Lw.in_lB; ai.lBs = Lw.in_lB_s;
+  ai.act = x; ai.ld_act = r.D; ai.norm_w = Lw.ln_w;
+  ai.out = proj; ai.ld_out = r.IPO;
+  ai.conv_state = conv; ai.conv_w = Lw.conv_w; ai.conv_b = Lw.conv_b;
+  ai.conv_lo = r.DI; ai.conv_c = r.C;
+  ai.N = r.IPO; ai.K = r.D;
+  rc = hip_status(launch_proj(ai, r.B, DFSSM_MODE_IN, s));
+  if (rc) return rc;
+
+  SsmArgs as{};
+  as.h = h;
+  as.xbc = proj + r.DI; as.ld_xbc = r.IPO;
+  as.dt = proj + r.DI + r.C; as.ld_dt = r.IPO;
+  as.z = proj; as.ld_z = r.IPO;
+  as.dt_bias = Lw.dt_bias; as.A_log = Lw.A_log; as.D = Lw.D;
+  as.y_out = g; as.ld_y = r.DI;
+  as.sumsq_slots = slots; as.n_slots = r.n_slots;
+  as.H = r.H; as.P = r.P; as.N = r.N;
+  rc = hip_status(launch_ssm(as, r.B, s));
+  if (rc) return rc;
+
+  ProjArgs ao{};
+  ao.bits = Lw.out_bits; ao.wscale = Lw.out_scale; ao.lA = Lw.out_lA; ao.lAs = Lw.out_lA_s;
+  ao.lB = Lw.out_lB; ao.lBs = Lw.out_lB_s;
+  ao.act = g; ao.ld_act = r.DI; ao.norm_w = Lw.norm_w;
+  ao.sumsq_slots = slots; ao.n_slots = r.n_slots;
+  ao.out = x; ao.ld_out = r.D;
+  ao.N = r.D; ao.K = r.DI;
+  return hip_status(launch_proj(ao, r.B, DFSSM_MODE_OUT, s));
+}
+
+int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* workspace,
+                        uint16_t* logits, int64_t* next, uint16_t* x_next, void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!x || !workspace || !next) return DFSSM_E_NULL;
+  const Derived r = derive(&model->dims);
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  HeadArgs a{};
+  a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
+  a.V = r.V; a.D = r.D; a.logits = logits;
+  a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
+  a.ticket = (unsigned*)(ws + w.ticket);
+  a.next = next; a.x_next = x_next;
+  return hip_status(launch_head(a, r.B, as_stream(stream)));
+}
+
+int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
+                      const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
+                      int fuse_next_embed, void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!x || !state || !workspace || !next) return DFSSM_E_NULL;
+  if (tokens) {
+    rc = dfssm_embed(model, tokens, x, workspace, stream);
+    if (rc) return rc;
+  }
+  for (int l = 0; l < model->dims.n_layer; ++l) {
+    rc = dfssm_layer_step(model, l, x, state, workspace, stream);
+    if (rc) return rc;
+  }
+  return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
+}
+
+}  // extern "C"

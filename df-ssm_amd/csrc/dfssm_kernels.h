@@ -1,0 +1,103 @@
+// Internal kernel argument blocks and launchers (not part of the C-ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DFSSM_MODE_IN 0
+#define DFSSM_MODE_OUT 1
+
+namespace dfssm {
+
+struct ProjArgs {
+  const uint32_t* bits;      // tiled sign bits [N_pad/64][K/128][64][4]
+  const uint16_t* wscale;    // (N) fp16 per-row scale
+  const int8_t* lA;          // (N, 16) LoRA A, int8
+  const uint16_t* lAs;       // (N) fp16
+  const int8_t* lB;          // (16, K) LoRA B, int8
+  const uint16_t* lBs;       // (16) fp16
+  const uint16_t* act;       // activation rows (M, ld_act) fp16: x (IN) or gated g (OUT)
+  int ld_act;
+  const float* norm_w;       // (K) fp32 RMSNorm weight: ln_w (IN) or norm_w (OUT)
+  const double* sumsq_slots; // OUT: (M, n_slots) per-block sum(g^2) from the SSM kernel
+  int n_slots;
+  uint16_t* out;             // IN: proj (M, ld_out); OUT: residual x (M, ld_out), updated in place
+  int ld_out;
+  int32_t* acc_out;          // optional (M, N) int32 scaffold accumulators
+  // IN only: conv1d applied to rows [conv_lo, conv_lo + conv_c)
+  uint16_t* conv_state;      // (M, conv_c, 3) fp16
+  const uint16_t* conv_w;    // (conv_c, 4) fp16
+  const uint16_t* conv_b;    // (conv_c) fp16
+  int conv_lo, conv_c;
+  int N, K;
+};
+
+struct ScaffoldArgs {
+  const uint32_t* bits;      // tiled sign bits
+  const int8_t* q;           // (M, K) int8 activations
+  const uint16_t* xscale;    // (M) fp16 (needed only with y_out)
+  const uint16_t* wscale;    // (N) fp16 (needed only with y_out)
+  int32_t* acc_out;          // (M, N) or null
+  uint16_t* y_out;           // (M, N) fp16(fp16(fp16(acc) * xs) * ws) or null
+  int N, K;
+};
+
+struct SsmArgs {
+  float* h;                  // (M, H, P, N) fp32 state, updated in place
+  const uint16_t* xbc;       // (M, ld_xbc) fp16 rows x | B | C (after the conv)
+  int ld_xbc;
+  const uint16_t* dt;        // (M, ld_dt) fp16 raw dt
+  int ld_dt;
+  const uint16_t* z;         // (M, ld_z) fp16 gate input, or null for plain y
+  int ld_z;
+  const float* dt_bias;
+  const float* A_log;
+  const float* D;
+  uint16_t* y_out;           // (M, ld_y) fp16: g (gated) or y
+  int ld_y;
+  double* sumsq_slots;       // (M, n_slots) per-block sum(g^2), or null
+  int n_slots;
+  int H, P, N;
+};
+
+struct ConvArgs {
+  uint16_t* state;           // (M, C, 3) fp16
+  uint16_t* x;               // (M, ld) fp16, in place
+  const uint16_t* w;         // (C, 4)
+  const uint16_t* b;         // (C)
+  int ld, C;
+};
+
+struct HeadArgs {
+  const uint16_t* x;         // (M, D) fp16 residual
+  const float* norm_f;       // (D) fp32
+  const int8_t* emb;         // tiled int8 table
+  const uint16_t* emb_scale; // (V) fp16
+  int V, D;
+  uint16_t* logits;          // (M, V) fp16 or null
+  float* part_val;           // (M, n_groups)
+  int* part_idx;             // (M, n_groups)
+  unsigned* ticket;          // zero before the first launch; left zero by every launch
+  int64_t* next;             // (M) greedy tokens
+  uint16_t* x_next;          // optional (M, D): embedding of the greedy tokens
+};
+
+struct EmbedArgs {
+  const int64_t* tokens;     // (M)
+  const int8_t* emb;         // tiled int8 table
+  const uint16_t* emb_scale; // (V)
+  uint16_t* x;               // (M, D)
+  int* err_flag;             // set to 1 if a token is out of range
+  int V, D;
+};
+
+hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);
+hipError_t launch_prologue(const ProjArgs& a, int M, uint16_t* xn, int8_t* q, uint16_t* s, hipStream_t st);
+hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s);
+hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s);
+hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);
+hipError_t launch_conv(const ConvArgs& a, int M, hipStream_t s);
+hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
+hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
+hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStream_t s);
+
+}  // namespace dfssm

@@ -1,0 +1,207 @@
+// Embedding gather, final RMSNorm + tied int8 LM head + greedy argmax (gfx950).
+//
+// The int8 table is stored re-tiled at load time as [V_pad/64][D/16][64 lanes][16 B]: lane l of
+// a wave owns vocabulary row 64*g + l and each wave-wide 16-byte load is one contiguous 1 KiB
+// transaction. Wave w of the 256-thread workgroup covers a quarter of D.
+//
+// Logits (df_ssm_inference.py:210,224 with an int8 table): xf = fp16(RMSNorm(x) * norm_f),
+// logit_v = fp16(fp32(sum_k xf_k * E_i8[v,k]) * s_E[v]). The dot product is accumulated in fp64,
+// where every partial sum of fp16 x int8 products is exact, so the result does not depend on
+// the summation order. Greedy token = first index of the maximum fp16 logit (torch.argmax, :236):
+// every workgroup writes its (max, first index) pair; the last workgroup to finish (ticket
+// counter, reset by that workgroup) reduces the pairs and may write the next token's embedding.
+#include "common.h"
+#include "dfssm_kernels.h"
+
+namespace dfssm {
+
+template <int M>
+__global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
+  extern __shared__ double xf[];  // [M][D] final-normed activations as fp64
+  __shared__ double part[4][M][64];
+  __shared__ double red_d[4];
+  __shared__ bool is_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x;
+  const int D = a.D, CH = D / 16, CPW = CH / 4;
+  const uint4* E = (const uint4*)a.emb + ((size_t)g * CH + wave * CPW) * 64 + lane;
+
+  u32x4 pre[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) if (c < CPW) pre[c] = ld_nt(E + (size_t)c * 64);
+
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* xm = a.x + (size_t)m * D;
+    double ps = 0.0;
+    for (int k = tid; k < D; k += 256) { double v = (double)h2f(xm[k]); ps += v * v; }
+    const double ss = block_sum_f64<256>(ps, red_d);
+    const float var = (float)ss * (1.0f / (float)D);
+    const float r = 1.0f / sqrtf(var + 1e-5f);
+    for (int k = tid; k < D; k += 256) xf[m * D + k] = (double)r16((h2f(xm[k]) * r) * a.norm_f[k]);
+  }
+  __syncthreads();
+
+  double acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0;
+  for (int c = 0; c < CPW; ++c) {
+    u32x4 e4;
+    if (c < 4) {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) if (cc == c) e4 = pre[cc];
+    } else {
+      e4 = ld_nt(E + (size_t)c * 64);
+    }
+    const uint32_t ev[4] = {e4.x, e4.y, e4.z, e4.w};
+    const int k0 = (wave * CPW + c) * 16;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const double e = (double)(int)(int8_t)(ev[j >> 2] >> (8 * (j & 3)));
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[m] = __builtin_fma(xf[m * D + k0 + j], e, acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) part[wave][m][lane] = acc[m];
+  __syncthreads();
+
+  if (wave < M) {
+    const int m = wave;
+    const int v = g * 64 + lane;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    if (v < a.V) {
+      const double s = part[0][m][lane] + part[1][m][lane] + part[2][m][lane] + part[3][m][lane];
+      const uint16_t lh = f2h((float)s * h2f(a.emb_scale[v]));
+      if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
+      best = h2f(lh);
+      bidx = v;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bidx, o, 64);
+      if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+    }
+    if (lane == 0) {
+      a.part_val[(size_t)m * gridDim.x + g] = best;
+      a.part_idx[(size_t)m * gridDim.x + g] = bidx;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const unsigned t = atomicAdd(a.ticket, 1u);
+    is_last = (t == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  __shared__ int next_tok[M];
+  if (wave < M) {
+    const int m = wave;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (int j = lane; j < (int)gridDim.x; j += 64) {
+      const float vv = __hip_atomic_load(a.part_val + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (vv > best || (vv == best && ii < bidx)) { best = vv; bidx = ii; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bidx, o, 64);
+      if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+    }
+    if (lane == 0) {
+      // no comparable logit (all NaN): report token 0 rather than an index outside the table
+      if (bidx < 0 || bidx >= a.V) bidx = 0;
+      a.next[m] = (int64_t)bidx;
+      next_tok[m] = bidx;
+    }
+  }
+  if (tid == 0) *a.ticket = 0u;
+  __syncthreads();
+  if (a.x_next) {
+    for (int m = 0; m < M; ++m) {
+      const int t = next_tok[m];
+      const int tg = t >> 6, tl = t & 63;
+      const float sc = h2f(a.emb_scale[t]);
+      for (int k = tid; k < D; k += 256) {
+        const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
+        a.x_next[(size_t)m * D + k] = f2h((float)row[k & 15] * sc);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  const int m = blockIdx.x;
+  const int64_t t64 = a.tokens[m];
+  const int t = (t64 < 0 || t64 >= a.V) ? 0 : (int)t64;
+  if (t64 < 0 || t64 >= a.V) {
+    if (threadIdx.x == 0) atomicOr(a.err_flag, 1);
+  }
+  const int CH = a.D / 16, tg = t >> 6, tl = t & 63;
+  const float sc = h2f(a.emb_scale[t]);
+  for (int k = threadIdx.x; k < a.D; k += 256) {
+    const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
+    a.x[(size_t)m * a.D + k] = f2h((float)row[k & 15] * sc);
+  }
+}
+
+// Re-tile a row-major (V, D) int8 table into [V_pad/64][D/16][64][16].
+__global__ void tile_emb_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int V, int D, int v_pad) {
+  const size_t total = (size_t)v_pad * D / 4;  // in 4-byte units
+  const int CH = D / 16;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int w = (int)(i & 3);              // which 4-byte word of the 16-byte chunk
+    const int lane = (int)((i >> 2) & 63);
+    const size_t rest = i >> 8;              // g * CH + c
+    const int c = (int)(rest % CH);
+    const int g = (int)(rest / CH);
+    const int row = g * 64 + lane;
+    uint32_t v = 0;
+    if (row < V) v = *(const uint32_t*)(src + (size_t)row * D + c * 16 + w * 4);
+    ((uint32_t*)dst)[i] = v;
+  }
+}
+
+template <int M>
+static hipError_t launch_head_m(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
+  // dynamic LDS above 64 KiB needs an explicit opt-in (gfx950 has 160 KiB per workgroup)
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<M>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(head_kernel<M>, dim3(groups), dim3(256), shm, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
+  const int groups = (a.V + 63) / 64;
+  const size_t shm = (size_t)M * a.D * sizeof(double);
+  if (shm > 120 * 1024) return hipErrorInvalidValue;
+  switch (M) {
+    case 1: return launch_head_m<1>(a, groups, shm, s);
+    case 2: return launch_head_m<2>(a, groups, shm, s);
+    case 3: return launch_head_m<3>(a, groups, shm, s);
+    case 4: return launch_head_m<4>(a, groups, shm, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStream_t s) {
+  const int v_pad = (V + 63) / 64 * 64;
+  const size_t total = (size_t)v_pad * D / 4;
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(tile_emb_kernel, dim3(blocks), dim3(256), 0, s, src, dst, V, D, v_pad);
+  return hipGetLastError();
+}
+
+}  // namespace dfssm

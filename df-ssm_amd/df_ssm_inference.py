@@ -1,0 +1,296 @@
+"""
+DF-SSM decode on MI355X: the drop-in for the reference's inference/gpu/df_ssm_inference.py.
+
+Same surface as the reference (df_ssm_inference.py:47-252):
+    DFSSMModel(path, device="cuda", batch_size=1)
+    .reset_state()
+    .forward(token_ids) -> fp16 logits (batch, vocab)     (advances the state by one token)
+    .generate(n_tokens=128)                              (prints timing like the reference)
+    python df_ssm_inference.py model.dfssm --batch_size B --n_tokens N
+
+What runs underneath is different: the scaffold stays 1 bit per weight in HBM (re-tiled, not
+unpacked to int8), every layer is three hand-written gfx950 kernels behind the C ABI of
+libdfssm_hip.so (include/dfssm.h), the SSM state is fp32, the tied head is the int8 table with
+a fused greedy argmax, and a whole decode step (embedding, all layers, head) is one HIP graph.
+Compatible extensions: generate(n_tokens, prompt=None, return_tokens=False, verbose=True) ingests
+a (batch, T) prompt step by step and does not leave warm-up state behind (the reference's warm-up
+forward advances the state, df_ssm_inference.py:230; the CPU driver resets after it,
+cpu_inference_driver.py:191-192).
+"""
+from __future__ import annotations
+
+import os
+import sys
+import time
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+from dfssm import _C  # noqa: E402
+from dfssm.format import DFSSMWeights, EMB_I8, LORA_RANK, read_dfssm  # noqa: E402
+
+
+class LayerWeights:
+    """Device tensors of one layer. Names follow the reference's LayerWeights
+    (df_ssm_inference.py:32-44) where the meaning is the same; the scaffold is kept as tiled sign
+    bits (in_bits / out_bits) and the LoRA factors stay int8 with their fp16 row scales."""
+    __slots__ = (
+        "in_bits", "in_scale", "out_bits", "out_scale",
+        "in_lora_A", "in_lora_A_scale", "in_lora_B", "in_lora_B_scale",
+        "out_lora_A", "out_lora_A_scale", "out_lora_B", "out_lora_B_scale",
+        "conv_weight", "conv_bias", "A_log", "D", "dt_bias",
+        "norm_weight", "layer_norm_weight",
+    )
+
+
+def _require_gpu(device) -> torch.device:
+    dev = torch.device(device)
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        raise RuntimeError("DFSSMModel runs only on an MI355X GPU (torch.cuda / HIP device); "
+                           f"got device={device!r}, cuda available={torch.cuda.is_available()}")
+    _C.lib()  # fail loudly if the HIP library is missing
+    return dev
+
+
+def _dev(a: np.ndarray, dev) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    elif a.dtype == np.float16:
+        return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.float16)
+    return torch.from_numpy(a).to(dev)
+
+
+class DFSSMModel:
+    def __init__(self, path, device="cuda", batch_size=1, weights: Optional[DFSSMWeights] = None):
+        self.device = _require_gpu(device)
+        self.batch_size = int(batch_size)
+        self.layers: List[LayerWeights] = []
+        w = weights if weights is not None else read_dfssm(path)
+        self.cfg = w.cfg
+        self._load(w)
+        self._alloc_state()
+        self._graph = None       # forward(): one decode step reading self._tok
+        self._gen_graphs = {}    # generation: S fused steps per replay
+        self._pos = 0
+
+    @classmethod
+    def from_weights(cls, weights: DFSSMWeights, device="cuda", batch_size=1):
+        return cls(None, device=device, batch_size=batch_size, weights=weights)
+
+    # ------------------------------------------------------------------ load
+    def _tile_bits(self, packed: np.ndarray, rows: int, k: int) -> torch.Tensor:
+        src = _dev(packed, self.device)
+        nbytes = _C.lib().dfssm_tiled_bits_bytes(rows, k)
+        dst = torch.empty(nbytes // 4, dtype=torch.int32, device=self.device)
+        _C.check(_C.lib().dfssm_tile_bits(src.data_ptr(), dst.data_ptr(), rows, k, _C.stream()), "tile_bits")
+        return dst
+
+    def _load(self, w: DFSSMWeights):
+        c = self.cfg
+        dims = _C.Dims(c.n_layer, c.d_model, c.d_inner, c.d_state, c.nheads, c.p, c.ngroups,
+                       c.vocab_size, self.batch_size, c.emb_code)
+        rc = _C.lib().dfssm_check_dims(dims)
+        if rc != 0:
+            raise _C.DFSSMError(f"model {c} / batch {self.batch_size} not supported: "
+                                f"{_C.lib().dfssm_error_string(rc).decode()}")
+        if c.emb_code != EMB_I8:
+            raise NotImplementedError("the GPU path implements the int8 tied embedding (emb_code 1)")
+        self.dims = dims
+        dev = self.device
+        D, DI, IPO = c.d_model, c.d_inner, c.in_proj_out
+        descs = (_C.Layer * c.n_layer)()
+        for li, L in enumerate(w.layers):
+            lw = LayerWeights()
+            lw.in_bits = self._tile_bits(L["in_packed"], IPO, D)
+            lw.in_scale = _dev(L["in_scale"], dev)
+            lw.in_lora_A, lw.in_lora_A_scale = _dev(L["in_lA"], dev), _dev(L["in_lA_s"], dev)
+            lw.in_lora_B, lw.in_lora_B_scale = _dev(L["in_lB"], dev), _dev(L["in_lB_s"], dev)
+            lw.out_bits = self._tile_bits(L["out_packed"], D, DI)
+            lw.out_scale = _dev(L["out_scale"], dev)
+            lw.out_lora_A, lw.out_lora_A_scale = _dev(L["out_lA"], dev), _dev(L["out_lA_s"], dev)
+            lw.out_lora_B, lw.out_lora_B_scale = _dev(L["out_lB"], dev), _dev(L["out_lB_s"], dev)
+            lw.conv_weight, lw.conv_bias = _dev(L["conv_w"], dev), _dev(L["conv_b"], dev)
+            lw.A_log, lw.D, lw.dt_bias = _dev(L["A_log"], dev), _dev(L["D"], dev), _dev(L["dt_bias"], dev)
+            lw.norm_weight = _dev(L["norm_w"].astype(np.float32), dev)
+            lw.layer_norm_weight = _dev(L["ln_w"].astype(np.float32), dev)
+            self.layers.append(lw)
+            d = descs[li]
+            for field, t in (("in_bits", lw.in_bits), ("in_scale", lw.in_scale), ("in_lA", lw.in_lora_A),
+                             ("in_lA_s", lw.in_lora_A_scale), ("in_lB", lw.in_lora_B), ("in_lB_s", lw.in_lora_B_scale),
+                             ("out_bits", lw.out_bits), ("out_scale", lw.out_scale), ("out_lA", lw.out_lora_A),
+                             ("out_lA_s", lw.out_lora_A_scale), ("out_lB", lw.out_lora_B),
+                             ("out_lB_s", lw.out_lora_B_scale), ("conv_w", lw.conv_weight), ("conv_b", lw.conv_bias),
+                             ("A_log", lw.A_log), ("D", lw.D), ("dt_bias", lw.dt_bias),
+                             ("norm_w", lw.norm_weight), ("ln_w", lw.layer_norm_weight)):
+                setattr(d, field, t.data_ptr())
+        emb_src = _dev(w.emb, dev)
+        self.embedding = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, D), dtype=torch.int8, device=dev)
+        _C.check(_C.lib().dfssm_tile_embedding(emb_src.data_ptr(), self.embedding.data_ptr(), c.vocab_size, D,
+                                               _C.stream()), "tile_embedding")
+        del emb_src
+        self.embedding_scale = _dev(w.emb_scale, dev)
+        self.norm_f_weight = _dev(w.norm_f.astype(np.float32), dev)
+        self._descs = descs
+        self._model = _C.Model(dims, descs, self.embedding.data_ptr(), self.embedding_scale.data_ptr(),
+                               self.norm_f_weight.data_ptr())
+        torch.cuda.synchronize(dev)
+
+    # ------------------------------------------------------------------ state
+    def _alloc_state(self):
+        c, B, d = self.cfg, self.batch_size, self.device
+        self.h_state = torch.zeros(c.n_layer, B, c.nheads, c.p, c.d_state, dtype=torch.float32, device=d)
+        self.conv_state = torch.zeros(c.n_layer, B, c.d_xbc, 3, dtype=torch.float16, device=d)
+        self.h_states = [self.h_state[l] for l in range(c.n_layer)]        # reference attribute names
+        self.conv_states = [self.conv_state[l] for l in range(c.n_layer)]
+        self._state = _C.State(self.h_state.data_ptr(), self.conv_state.data_ptr())
+        self.x = torch.zeros(B, c.d_model, dtype=torch.float16, device=d)
+        self.logits = torch.empty(B, c.vocab_size, dtype=torch.float16, device=d)
+        self._tok = torch.zeros(B, dtype=torch.int64, device=d)
+        self._next = torch.zeros(B, dtype=torch.int64, device=d)
+        nbytes = _C.lib().dfssm_workspace_bytes(self.dims)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=d)
+        _C.check(_C.lib().dfssm_workspace_init(self.dims, self.workspace.data_ptr(), _C.stream()), "workspace_init")
+        self._err = _C.lib().dfssm_workspace_error_flag(self.dims, self.workspace.data_ptr())
+        # one eager head launch outside any capture (sets the kernel's LDS attribute)
+        _C.check(_C.lib().dfssm_lmhead_argmax(self._model, self.x.data_ptr(), self.workspace.data_ptr(),
+                                              self.logits.data_ptr(), self._next.data_ptr(), None,
+                                              _C.stream()), "lmhead")
+        torch.cuda.synchronize(d)
+
+    def reset_state(self):
+        self.h_state.zero_()
+        self.conv_state.zero_()
+
+    # ------------------------------------------------------------------ steps
+    def _decode(self, tokens: Optional[torch.Tensor], logits: Optional[torch.Tensor], nxt: torch.Tensor, fuse: bool):
+        _C.check(_C.lib().dfssm_decode_step(
+            self._model, None if tokens is None else tokens.data_ptr(), self.x.data_ptr(), self._state,
+            self.workspace.data_ptr(), None if logits is None else logits.data_ptr(), nxt.data_ptr(),
+            1 if fuse else 0, _C.stream()), "decode_step")
+
+    def decode_step_eager(self, token_ids: Optional[torch.Tensor] = None, want_logits: bool = True):
+        """One decode step without graphs (tests, debugging). Returns (logits or None, next)."""
+        if token_ids is not None:
+            self._tok.copy_(token_ids.view(-1).to(self.device, torch.int64))
+        self._decode(self._tok if token_ids is not None else None,
+                     self.logits if want_logits else None, self._next, fuse=True)
+        return (self.logits if want_logits else None), self._next
+
+    def _capture(self, fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def _capture_graph(self):
+        self._graph = self._capture(lambda: self._decode(self._tok, self.logits, self._next, fuse=True))
+
+    def forward(self, token_ids):
+        """token_ids (batch,) int64 -> fp16 logits (batch, vocab); advances the state by one token."""
+        tok = torch.as_tensor(token_ids).view(-1)
+        if tok.numel() != self.batch_size:
+            raise ValueError(f"expected {self.batch_size} token ids, got {tok.numel()}")
+        if tok.device.type == "cpu":
+            if int(tok.min()) < 0 or int(tok.max()) >= self.cfg.vocab_size:
+                raise IndexError("token id out of range")
+        self._tok.copy_(tok.to(self.device, torch.int64))
+        if self._graph is None:
+            self._capture_graph()
+        self._graph.replay()
+        return self.logits.clone()
+
+    def _gen_graph(self, S: int):
+        if S not in self._gen_graphs:
+            hist = torch.zeros(S, self.batch_size, dtype=torch.int64, device=self.device)
+
+            def body():
+                for i in range(S):
+                    self._decode(None, None, hist[i], fuse=True)
+            self._gen_graphs[S] = (self._capture(body), hist)
+        return self._gen_graphs[S]
+
+    def ingest(self, prompt: torch.Tensor) -> None:
+        """Consume a (batch, T) prompt token by token; afterwards self._next holds the greedy
+        token after the prompt and self.x its embedding."""
+        prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
+        if prompt.dim() == 1:
+            prompt = prompt.view(-1, 1)
+        if self._graph is None:
+            self._capture_graph()
+        for t in range(prompt.shape[1]):
+            self._tok.copy_(prompt[:, t])
+            self._graph.replay()
+
+    def decode(self, n_steps: int, steps_per_graph: int = 8) -> torch.Tensor:
+        """n_steps greedy steps continuing from the current state (x holds the embedding of
+        self._next). Returns the (batch, n_steps) tokens produced, the first being the token after
+        the one already in x."""
+        S = max(1, min(steps_per_graph, n_steps))
+        out = []
+        done = 0
+        while done < n_steps:
+            s = S if n_steps - done >= S else 1
+            g, hist = self._gen_graph(s)
+            g.replay()
+            out.append(hist.t().clone())
+            done += s
+        return torch.cat(out, dim=1)[:, :n_steps]
+
+    def generate(self, n_tokens=128, prompt=None, return_tokens=False, verbose=True):
+        """Greedy decode timed like the reference's generate (df_ssm_inference.py:226-243).
+
+        The timed region holds n_tokens decode steps: the first consumes the last prompt token
+        (token 0 without a prompt, as in the reference), each later one the previous greedy
+        token. With return_tokens, returns the (batch, n_tokens) greedy tokens those steps
+        produced; earlier prompt tokens are ingested before the timer starts.
+        """
+        B = self.batch_size
+        self.reset_state()
+        if prompt is None:
+            prompt = torch.zeros(B, 1, dtype=torch.int64)
+        prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
+        if prompt.dim() == 1:
+            prompt = prompt.view(-1, 1)
+        # graphs are captured before the timer starts; capture executes nothing
+        if self._graph is None:
+            self._capture_graph()
+        S = 8 if n_tokens > 8 else 1
+        self._gen_graph(S)
+        self._gen_graph(1)
+        if prompt.shape[1] > 1:
+            self.ingest(prompt[:, :-1])
+        torch.cuda.synchronize(self.device)
+        start = time.perf_counter()
+        self._tok.copy_(prompt[:, -1])
+        self._graph.replay()
+        first = self._next.clone()
+        rest = self.decode(n_tokens - 1, S) if n_tokens > 1 else None
+        torch.cuda.synchronize(self.device)
+        elapsed = time.perf_counter() - start
+        total = n_tokens * B
+        if verbose:
+            print(f"batch={B}  {n_tokens} steps  {total} total tokens")
+            print(f"  {elapsed*1000:.1f} ms  ({total/elapsed:.0f} tok/s total, "
+                  f"{elapsed/n_tokens*1e6:.0f} μs/step, {total/elapsed/B:.0f} tok/s/seq)")
+        self.last_elapsed = elapsed
+        if return_tokens:
+            return first[:, None] if rest is None else torch.cat([first[:, None], rest], dim=1)
+        return None
+
+    def error_flag(self) -> int:
+        """Nonzero if an out-of-range token id reached the embedding kernel."""
+        off = self._err - self.workspace.data_ptr()
+        return int(self.workspace[off:off + 4].view(torch.int32).item())
+
+
+if __name__ == "__main__":
+    import argparse
+    p = argparse.ArgumentParser()
+    p.add_argument("model"); p.add_argument("--batch_size", type=int, default=1)
+    p.add_argument("--n_tokens", type=int, default=128)
+    a = p.parse_args()
+    DFSSMModel(a.model, batch_size=a.batch_size).generate(n_tokens=a.n_tokens)

@@ -1,0 +1,151 @@
+/*
+ * dfssm.h -- C ABI of libdfssm_hip.so, the MI355X (gfx950) DF-SSM decode-step library.
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer (HBM) owned by the caller, unless marked "host".
+ *  - fp16 tensors are passed as uint16_t bit patterns; fp32 as float; row-major, C-contiguous
+ *    unless a leading dimension (ld_*) is given, in elements.
+ *  - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null stream), never
+ *    allocates device memory, never synchronizes, and is therefore capturable into a HIP graph.
+ *  - Every function returns 0 on success, a negative DFSSM_E* code when argument validation
+ *    fails (nothing is launched), or a positive hipError_t from the launch.
+ *  - The library keeps no state between calls; concurrent calls are safe when they touch
+ *    disjoint buffers or are ordered on one stream.
+ *
+ * Model-specific constraints (checked by dfssm_check_dims): d_state = 128, ngroups = 1,
+ * LoRA rank 16, d_conv = 4, P = d_inner / nheads a multiple of 16, d_model and d_inner multiples
+ * of 512 and at most 8192, nheads a multiple of 8, batch 1..4, int8 embedding (emb_code 1).
+ */
+#ifndef DFSSM_H
+#define DFSSM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFSSM_ABI_VERSION 1
+
+#define DFSSM_OK 0
+#define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
+#define DFSSM_E_DIMS (-2)        /* model dimensions not supported by the kernels */
+#define DFSSM_E_BATCH (-3)       /* batch size not supported */
+#define DFSSM_E_ALIGN (-4)       /* pointer or leading dimension misaligned */
+#define DFSSM_E_RANGE (-5)       /* index (layer, token count, size) out of range */
+
+typedef struct dfssm_dims {
+  int32_t n_layer, d_model, d_inner, d_state, nheads, headdim, ngroups, vocab_size;
+  int32_t batch;     /* sequences decoded together */
+  int32_t emb_code;  /* 1 = int8 table + fp16 row scale */
+} dfssm_dims;
+
+/* Device pointers of one layer, in .dfssm order (training/export_dfssm.py:135-185). The sign bits
+ * are in the tiled layout produced by dfssm_tile_bits; everything else is as stored in the file,
+ * except the two norm weights, which are fp32 (fp16 files are widened at load). */
+typedef struct dfssm_layer {
+  const uint32_t* in_bits;   const uint16_t* in_scale;
+  const int8_t* in_lA;       const uint16_t* in_lA_s;
+  const int8_t* in_lB;       const uint16_t* in_lB_s;
+  const uint32_t* out_bits;  const uint16_t* out_scale;
+  const int8_t* out_lA;      const uint16_t* out_lA_s;
+  const int8_t* out_lB;      const uint16_t* out_lB_s;
+  const uint16_t* conv_w;    const uint16_t* conv_b;
+  const float* A_log;        const float* D;          const float* dt_bias;
+  const float* norm_w;       const float* ln_w;
+} dfssm_layer;
+
+typedef struct dfssm_model {
+  dfssm_dims dims;
+  const dfssm_layer* layers;     /* HOST array of n_layer descriptors (device pointers inside) */
+  const int8_t* emb;             /* int8 table in the tiled layout of dfssm_tile_embedding */
+  const uint16_t* emb_scale;     /* (V) fp16 row scales */
+  const float* norm_f;           /* (D) fp32 */
+} dfssm_model;
+
+typedef struct dfssm_state {
+  float* h;                      /* (n_layer, batch, nheads, P, d_state) fp32 SSM state */
+  uint16_t* conv;                /* (n_layer, batch, d_xbc, 3) fp16 conv shift register */
+} dfssm_state;
+
+/* ---- library ---------------------------------------------------------------------------- */
+int dfssm_version(void);
+const char* dfssm_error_string(int code);
+/* 0 if the kernels support `dims`, else DFSSM_E_DIMS / DFSSM_E_BATCH. */
+int dfssm_check_dims(const dfssm_dims* dims);
+
+/* ---- load-time layout ------------------------------------------------------------------ */
+/* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, d_model) int8 table. */
+size_t dfssm_tiled_bits_bytes(int rows, int k);
+size_t dfssm_tiled_emb_bytes(int vocab, int d_model);
+/* Re-tile row-major packed sign bits (the .dfssm int32 words, export_dfssm.py:34-42) for the
+ * scaffold kernels. Replaces the load-time unpack of df_ssm_inference.py:23-29,70-74: the copy
+ * stays 1 bit per weight. k must be a multiple of 512. */
+int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* stream);
+/* Re-tile the (V, D) int8 embedding for the gather and the tied head. */
+int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream);
+
+/* ---- single operators ------------------------------------------------------------------ */
+/* Scaffold GEMM: acc[m][n] = sum_k q[m][k] * (bit ? +1 : -1) (exact int32) and, if y_out is
+ * non-NULL, y = fp16(fp16(fp16(acc) * xscale[m]) * wscale[n]). Replaces torch._int_mm plus the
+ * dequant of _scaffold_matmul, df_ssm_inference.py:154-158. M = 1..4. */
+int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
+                        const uint16_t* wscale, int M, int N, int K, int32_t* acc_out,
+                        uint16_t* y_out, void* stream);
+
+/* RMSNorm + int8 quantization of M rows (the prologue of every projection):
+ * xn = fp16((x * r) * w), q = int8 activations, s = fp16 scales.
+ * Replaces _rms_norm + _quantize_to_int8, df_ssm_inference.py:141-152. */
+int dfssm_rmsnorm_quantize(const uint16_t* x, const float* w, int M, int K, uint16_t* xn_out,
+                           int8_t* q_out, uint16_t* s_out, void* stream);
+
+/* conv1d shift-register step + SiLU, in place on xbc (rows of stride ld_xbc) and conv_state
+ * (batch, channels, 3). Replaces df_ssm_kernels.conv_step (df_ssm_kernels.cu:109-125). */
+int dfssm_conv_step(uint16_t* conv_state, uint16_t* xbc, int ld_xbc, const uint16_t* conv_w,
+                    const uint16_t* conv_b, int batch, int channels, void* stream);
+
+/* Mamba-2 SSM step with an fp32 state h (batch, nheads, headdim, d_state). xbc rows hold
+ * x | B | C (after the conv), dt rows the raw dt. Writes y (batch, ld_y). Replaces
+ * df_ssm_kernels.ssm_step (df_ssm_kernels.cu:127-151); the reference's fp16 state becomes fp32
+ * and the caller need not zero y. */
+int dfssm_ssm_step(float* h_state, const uint16_t* xbc, int ld_xbc, const uint16_t* dt, int ld_dt,
+                   const float* dt_bias, const float* A_log, const float* D, uint16_t* y_out,
+                   int ld_y, int batch, int nheads, int headdim, int d_state, void* stream);
+
+/* ---- decode ----------------------------------------------------------------------------- */
+/* Workspace for the layer/decode calls; init zeroes what must start at zero (once, before use). */
+size_t dfssm_workspace_bytes(const dfssm_dims* dims);
+int dfssm_workspace_init(const dfssm_dims* dims, void* workspace, void* stream);
+
+/* x = embedding(tokens): x (batch, D) fp16. Out-of-range tokens read row 0 and set the
+ * workspace error flag (dfssm_workspace_error_flag). Replaces df_ssm_inference.py:220. */
+int dfssm_embed(const dfssm_model* model, const int64_t* tokens, uint16_t* x, void* workspace,
+                void* stream);
+/* Device address of the int error flag inside the workspace. */
+int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace);
+
+/* One residual block on x (batch, D) fp16, in place: RMSNorm, in_proj scaffold + LoRA, conv,
+ * SSM, gate, gated RMSNorm, out_proj scaffold + LoRA, residual. Replaces one iteration of
+ * _run_layers, df_ssm_inference.py:161-207. 3 kernel launches. */
+int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                     void* workspace, void* stream);
+
+/* Final RMSNorm, tied int8 head and greedy argmax: logits (batch, V) fp16 (may be NULL),
+ * next (batch) int64. If x_next is non-NULL the embedding of `next` is written there (it may
+ * alias x). Replaces df_ssm_inference.py:210,224,236. */
+int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* workspace,
+                        uint16_t* logits, int64_t* next, uint16_t* x_next, void* stream);
+
+/* One whole decode step: if tokens != NULL, x = embedding(tokens) first; then every layer,
+ * then the head. With fuse_next_embed != 0, x receives the embedding of the greedy tokens, so
+ * the following step can pass tokens = NULL. Replaces forward() + argmax,
+ * df_ssm_inference.py:219-224,236. */
+int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
+                      const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
+                      int fuse_next_embed, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DFSSM_H */

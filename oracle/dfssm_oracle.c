@@ -89,15 +89,24 @@ void or_unpack_bits(const uint32_t* packed, int rows, int kwords, int8_t* out) {
 
 /* ---------------------------------------------------------------- scaffold (row a5) -------- */
 
+/* byte -> its 8 signs (bit i of the byte -> element i), the unpack of or_unpack_bits 8 at a time */
+static int8_t sign_lut[256][8];
+static void init_sign_lut(void) {
+  for (int v = 0; v < 256; ++v)
+    for (int i = 0; i < 8; ++i) sign_lut[v][i] = ((v >> i) & 1) ? 1 : -1;
+}
+
 /* acc[m][n] = sum_k q[m][k] * w[n][k], exact int32 (torch._int_mm, df_ssm_inference.py:157). */
 void or_scaffold_acc(const uint32_t* bits, const int8_t* q, int M, int N, int K, int32_t* acc) {
   const int kw = K / 32;
+  if (sign_lut[0][0] == 0) init_sign_lut();
 #pragma omp parallel
   {
     int8_t* w = (int8_t*)malloc((size_t)K);
 #pragma omp for schedule(static)
     for (int n = 0; n < N; ++n) {
-      or_unpack_bits(bits + (size_t)n * kw, 1, kw, w);
+      const uint8_t* rb = (const uint8_t*)(bits + (size_t)n * kw); /* little-endian words */
+      for (int j = 0; j < K / 8; ++j) memcpy(w + 8 * j, sign_lut[rb[j]], 8);
       for (int m = 0; m < M; ++m) {
         const int8_t* qm = q + (size_t)m * K;
         int32_t s = 0;
@@ -282,21 +291,24 @@ void or_embed(const int8_t* E8, const uint16_t* sE, const uint16_t* E16, int emb
  * next[m] = first index of the maximum fp16 logit (torch.argmax, :236). */
 void or_lm_head(const uint16_t* xf, const int8_t* E8, const uint16_t* sE, const uint16_t* E16, int emb_code,
                 int M, int V, int D, uint16_t* logits, int64_t* next) {
+  double* xd = (double*)malloc(sizeof(double) * (size_t)M * D);
+  for (long i = 0; i < (long)M * D; ++i) xd[i] = hf(xf[i]);
 #pragma omp parallel for schedule(static)
   for (int v = 0; v < V; ++v)
     for (int m = 0; m < M; ++m) {
       double s = 0.0;
-      const uint16_t* xm = xf + (size_t)m * D;
+      const double* xm = xd + (size_t)m * D;
       if (emb_code) {
         const int8_t* e = E8 + (size_t)v * D;
-        for (int k = 0; k < D; ++k) s += (double)hf(xm[k]) * (double)e[k];
+        for (int k = 0; k < D; ++k) s += xm[k] * (double)e[k];
         logits[(size_t)m * V + v] = or_f2h((float)s * hf(sE[v]));
       } else {
         const uint16_t* e = E16 + (size_t)v * D;
-        for (int k = 0; k < D; ++k) s += (double)hf(xm[k]) * (double)hf(e[k]);
+        for (int k = 0; k < D; ++k) s += xm[k] * (double)hf(e[k]);
         logits[(size_t)m * V + v] = r16(s);
       }
     }
+  free(xd);
   for (int m = 0; m < M; ++m) {
     int64_t best = 0;
     float bv = hf(logits[(size_t)m * V]);

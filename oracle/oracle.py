@@ -272,10 +272,10 @@ class OracleModel:
         return logits, nxt
 
     def generate(self, prompts: np.ndarray, n_new: int, keep_logits: bool = False):
-        """Consume `prompts` (B, T) step by step, then decode n_new greedy tokens.
+        """Consume `prompts` (B, T) step by step, then decode greedily: T + n_new - 1 steps.
 
-        Returns (generated (B, n_new) int64, list of per-step logits if keep_logits). The token fed
-        after the prompt is the argmax of the last prompt step's logits.
+        Returns (generated (B, n_new) int64, list of per-step logits if keep_logits). generated[:, 0]
+        is the argmax after the last prompt token; generated[:, i] is fed to step T + i.
         """
         B, T = prompts.shape
         assert B == self.B
@@ -289,9 +289,10 @@ class OracleModel:
         out = np.empty((B, n_new), np.int64)
         for i in range(n_new):
             out[:, i] = nxt
-            logits, nxt = self.step(out[:, i])
-            if keep_logits:
-                all_logits.append(logits)
+            if i + 1 < n_new:            # the last greedy token is recorded, not consumed
+                logits, nxt = self.step(out[:, i])
+                if keep_logits:
+                    all_logits.append(logits)
         return out, all_logits
 
 
