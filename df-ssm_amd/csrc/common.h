@@ -19,6 +19,66 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }  // RNE
 __device__ __forceinline__ float r16(float f) { return (float)(f16)f; }  // round through fp16
 
+// Correctly rounded fp32 square root. v_sqrt_f32 is accurate to 1 ulp only; the fp64 square root
+// rounded to fp32 is the correctly rounded fp32 result (53 >= 2*24 + 2, so the double rounding is
+// innocuous), which is what IEEE sqrtf on the host returns.
+__device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
+// exp and log1p of the decode step: the same operation sequence as the spec's CPU restatement,
+// built from correctly rounded operations only (+ - * /, fma, rint, bit moves), so results are
+// identical bit for bit on the host and the GPU.
+//  exp: Cody & Waite reduction x = n ln2 + r (ln2 as 9-bit head + tail), |r| <= ln2/2, degree-7
+//       Taylor polynomial of e^r in Horner form, e^x = p 2^n; e^x for x < -86 returns 0 (so
+//       nonzero results are normal numbers), overflow returns +inf. Max error 0.91 ulp.
+//  log1p (y >= 0): u = 1+y = m 2^e, m in [sqrt(1/2), sqrt(2)), log m = 2 atanh((m-1)/(m+1)) with
+//       the atanh series to s^9, plus the correction (y - (u-1))/u for the rounding of 1+y.
+//       Max error 2.3 ulp.
+__device__ __forceinline__ float dev_expf(float x) {
+  if (x != x) return x;
+  if (x < -86.0f) return 0.0f;
+  if (x > 89.0f) return __builtin_inff();
+  const float n = __builtin_rintf(x * 1.44269502f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.42860677e-6f, r);
+  float p = 1.98412698e-4f;
+  p = __builtin_fmaf(p, r, 1.38888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  const float sc = __builtin_bit_cast(float, (uint32_t)(ni + 127) << 23);
+  return p * sc;
+}
+
+__device__ __forceinline__ float dev_log_pos(float u) {  // finite u >= 1
+  const uint32_t b = __builtin_bit_cast(uint32_t, u);
+  int e = (int)(b >> 23) - 127;
+  float m = __builtin_bit_cast(float, (b & 0x7fffffu) | 0x3f800000u);
+  if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 0.111111111f;
+  p = __builtin_fmaf(p, s2, 0.142857143f);
+  p = __builtin_fmaf(p, s2, 0.2f);
+  p = __builtin_fmaf(p, s2, 0.333333333f);
+  p = p * s2;
+  const float t = 2.0f * s;
+  const float lm = __builtin_fmaf(t, p, t);
+  const float ef = (float)e;
+  return __builtin_fmaf(ef, 0.693145751953125f, __builtin_fmaf(ef, 1.42860677e-6f, lm));
+}
+
+__device__ __forceinline__ float dev_log1pf(float y) {  // y >= 0
+  if (y != y || y == 0.0f || y == __builtin_inff()) return y;
+  const float u = 1.0f + y;
+  const float lg = dev_log_pos(u);
+  return lg + (y - (u - 1.0f)) / u;
+}
+
 // Wave64 sums (xor butterfly: every lane ends with the total).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll

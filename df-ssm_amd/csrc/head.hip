@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
     for (int k = tid; k < D; k += 256) { double v = (double)h2f(xm[k]); ps += v * v; }
     const double ss = block_sum_f64<256>(ps, red_d);
     const float var = (float)ss * (1.0f / (float)D);
-    const float r = 1.0f / sqrtf(var + 1e-5f);
+    const float r = 1.0f / sqrt_rn(var + 1e-5f);
     for (int k = tid; k < D; k += 256) xf[m * D + k] = (double)r16((h2f(xm[k]) * r) * a.norm_f[k]);
   }
   __syncthreads();

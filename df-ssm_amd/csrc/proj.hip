@@ -58,7 +58,7 @@ __device__ void proj_prologue_row(const ProjArgs& a, int m, ProjLds<M>& L) {
     ss = block_sum_f64<kNT>(part, L.red_d);
   }
   const float var = (float)ss * (1.0f / (float)K);
-  const float r = 1.0f / sqrtf(var + 1e-5f);
+  const float r = 1.0f / sqrt_rn(var + 1e-5f);
   // 2) xn = fp16((x * r) * w), amax
   float amax = 0.0f;
   for (int k = tid; k < K; k += kNT) {
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kNT) void proj_kernel(ProjArgs a) {
           o = o + s2 * h2f(wc[2]);
           o = o + xv * h2f(wc[3]);
           o = o + h2f(a.conv_b[ch]);
-          const float sig = 1.0f / (1.0f + expf(-o));
+          const float sig = 1.0f / (1.0f + dev_expf(-o));
           out = o * sig;
         }
         a.out[(size_t)m * a.ld_out + n] = f2h(out);

@@ -5,7 +5,7 @@
 // thread streams 32 B of fp32 state and the workgroup 8 KiB contiguous; the C.h readout is
 // reduced over the 16 lanes that share a row. Arithmetic (ssm_step_kernel,
 // df_ssm_kernels.cu:77-101, with an fp32 state and P = d_inner/nheads):
-//   dt = log1p(exp(dt_raw + dt_bias)); Abar = exp(dt * -exp(A_log))
+//   dt = log1p(exp(dt_raw + dt_bias)); Abar = exp(dt * -exp(A_log))   (dev_expf, dev_log1pf)
 //   h = fma(Abar, h, (x*dt) * B_n);   y = fp16(sum_n C_n h_n + x * D)
 // and, when a gate is requested, g = fp16(y * fp16(z * fp16(sigmoid(z)))) (df_ssm_inference.py
 // :194-195) with sum(g^2) of the block written to a per-block slot for the gated RMSNorm.
@@ -31,8 +31,8 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs a) {
   const f32x4 h1 = ld_nt_f4(hp + 4);
 
   const uint16_t* xr = a.xbc + (size_t)m * a.ld_xbc;
-  const float dt = log1pf(expf(h2f(a.dt[(size_t)m * a.ld_dt + head]) + a.dt_bias[head]));
-  const float abar = expf(dt * -expf(a.A_log[head]));
+  const float dt = dev_log1pf(dev_expf(h2f(a.dt[(size_t)m * a.ld_dt + head]) + a.dt_bias[head]));
+  const float abar = dev_expf(dt * -dev_expf(a.A_log[head]));
   const float xv = h2f(xr[head * a.P + p]);
   const float X = xv * dt;
   const uint4 b8 = *(const uint4*)(xr + DI + n0);
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs a) {
     float outv = y;
     if (a.z) {
       const float z = h2f(a.z[(size_t)m * a.ld_z + head * a.P + p]);
-      const float sg = r16(1.0f / (1.0f + expf(-z)));
+      const float sg = r16(1.0f / (1.0f + dev_expf(-z)));
       const float sz = r16(z * sg);
       outv = r16(y * sz);
       gsqd = (double)outv * (double)outv;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void conv_kernel(ConvArgs a) {
   o = o + s2 * h2f(wc[2]);
   o = o + xv * h2f(wc[3]);
   o = o + h2f(a.b[ch]);
-  const float sig = 1.0f / (1.0f + expf(-o));
+  const float sig = 1.0f / (1.0f + dev_expf(-o));
   *xp = f2h(o * sig);
 }
 

@@ -5,6 +5,9 @@ dfssm/libdfssm_hip.so. Flags:
   --offload-arch=gfx950          MI355X only
   -ffp-contract=off              the kernels spell out every fused multiply-add they want
   -target-feature -packed-fp32-ops  no packed fp32 VALU instructions
+  -target-feature -fma-mix-insts    no v_fma_mix*: the compiler otherwise folds
+                                 fptrunc(fmul_f32(a, b)) into one fma_mix rounding the exact product
+                                 straight to fp16, which differs from fp32-then-fp16 on ties
 """
 from __future__ import annotations
 
@@ -24,6 +27,7 @@ LIB = os.path.join(PKG, "libdfssm_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts",
          "-I" + os.path.join(REPO, "include"), "-I" + CSRC]
 
 

@@ -19,7 +19,8 @@
  *          exist so that the restated dataflow can be compared with the compiled reference
  *          layer_forward (cpu_inference.c:303-376) built with HEADDIM=64.
  *
- * Sums over a vector are accumulated in double and rounded once to fp32; the reference sums in
+ * exp / log1p are this file's own or_expf / or_log1pf (see there), shared bit-for-bit with the
+ * HIP kernels. Sums over a vector are accumulated in double and rounded once to fp32; the reference sums in
  * fp32 in an order that no reference test fixes, so sums carry a tolerance, not bit-exactness.
  * Integer work (bit unpack, scaffold accumulators, quantized values) is exact.
  *
@@ -74,6 +75,75 @@ static inline float hf(uint16_t h) { return or_h2f(h); }
 
 void or_f2h_array(const float* in, uint16_t* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_f2h(in[i]); }
 void or_h2f_array(const uint16_t* in, float* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_h2f(in[i]); }
+
+/* ---------------------------------------------------------------- exp / log1p -------------- */
+
+/* exp and log1p of the decode step. The reference calls CUDA's expf/log1pf
+ * (df_ssm_kernels.cu:45,78-79), whose results no reference test fixes; this build defines its
+ * own, written with correctly rounded operations only (+ - * /, fmaf, rintf, bit moves) so that
+ * the HIP kernels, which spell out the same sequence, produce the same bits:
+ *
+ * exp: Cody & Waite argument reduction x = n ln2 + r with ln2 split into a 9-bit head and a tail,
+ *      |r| <= ln2/2, then the degree-7 Taylor polynomial of e^r in Horner form; e^x = p 2^n with
+ *      2^n assembled from exponent bits. Results below e^-86 are returned as 0, so every nonzero
+ *      output is a normal number; overflow gives +inf.
+ * log: u = m 2^e with m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s), s = (m-1)/(m+1), with the
+ *      atanh series to s^9; log1p(y) = log(1+y) + (y - ((1+y) - 1)) / (1+y) (the standard
+ *      correction for the rounding of 1+y).
+ * Accuracy (checked against fp64 libm in tests): exp <= 2 ulp, log1p <= 3 ulp. */
+float or_expf(float x) {
+  if (x != x) return x;
+  if (x < -86.0f) return 0.0f;
+  if (x > 89.0f) return INFINITY;
+  const float n = rintf(x * 1.44269502f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.42860677e-6f, r);
+  float p = 1.98412698e-4f;
+  p = fmaf(p, r, 1.38888889e-3f);
+  p = fmaf(p, r, 8.33333333e-3f);
+  p = fmaf(p, r, 4.16666667e-2f);
+  p = fmaf(p, r, 1.66666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  const uint32_t eb = (uint32_t)(ni + 127) << 23;
+  float sc;
+  memcpy(&sc, &eb, 4);
+  return p * sc;
+}
+
+static float or_log_pos(float u) { /* finite u >= 1 */
+  uint32_t b;
+  memcpy(&b, &u, 4);
+  int e = (int)(b >> 23) - 127;
+  const uint32_t mb = (b & 0x7fffffu) | 0x3f800000u;
+  float m;
+  memcpy(&m, &mb, 4);
+  if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 0.111111111f;
+  p = fmaf(p, s2, 0.142857143f);
+  p = fmaf(p, s2, 0.2f);
+  p = fmaf(p, s2, 0.333333333f);
+  p = p * s2;
+  const float t = 2.0f * s;
+  const float lm = fmaf(t, p, t);
+  const float ef = (float)e;
+  return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860677e-6f, lm));
+}
+
+float or_log1pf(float y) { /* y >= 0 (softplus argument) */
+  if (y != y || y == 0.0f || y == INFINITY) return y;
+  const float u = 1.0f + y;
+  const float lg = or_log_pos(u);
+  return lg + (y - (u - 1.0f)) / u;
+}
+
+void or_expf_array(const float* x, float* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_expf(x[i]); }
+void or_log1pf_array(const float* x, float* out, long n) { for (long i = 0; i < n; ++i) out[i] = or_log1pf(x[i]); }
 
 /* ---------------------------------------------------------------- bits (row a2) ------------ */
 
@@ -215,7 +285,7 @@ void or_conv_step(uint16_t* state, uint16_t* xbc, int ld, const uint16_t* w, con
       o = o + s2 * hf(wc[2]);
       o = o + xv * hf(wc[3]);
       o = o + hf(b[ch]);
-      float sig = 1.0f / (1.0f + expf(-o));
+      float sig = 1.0f / (1.0f + or_expf(-o));
       *xp = or_f2h(o * sig);
     }
 }
@@ -223,7 +293,7 @@ void or_conv_step(uint16_t* state, uint16_t* xbc, int ld, const uint16_t* w, con
 /* ---------------------------------------------------------------- SSM (row a8) ------------- */
 
 /* ssm_step_kernel, df_ssm_kernels.cu:53-103, with an fp32 state and P = d_inner/nheads:
- *   dt = log1p(exp(dt_raw + dt_bias)); Abar = exp(dt * -exp(A_log))
+ *   dt = log1p(exp(dt_raw + dt_bias)); Abar = exp(dt * -exp(A_log))   (or_expf / or_log1pf)
  *   h[p][n] = fma(Abar, h[p][n], (x_p * dt) * B_n)
  *   y_p = fp16(sum_n C_n * h[p][n] + x_p * D)
  * x = xbc[0:DI], B = xbc[DI:DI+N], C = xbc[DI+N:DI+2N] (ngroups = 1: B and C shared by all heads,
@@ -236,8 +306,8 @@ void or_ssm_step(float* h, const uint16_t* xbc, int ld_xbc, const uint16_t* dt_r
   for (int m = 0; m < M; ++m)
     for (int hd = 0; hd < H; ++hd) {
       const uint16_t* xr = xbc + (size_t)m * ld_xbc;
-      float dt = log1pf(expf(hf(dt_raw[(size_t)m * ld_dt + hd]) + dt_bias[hd]));
-      float abar = expf(dt * -expf(A_log[hd]));
+      float dt = or_log1pf(or_expf(hf(dt_raw[(size_t)m * ld_dt + hd]) + dt_bias[hd]));
+      float abar = or_expf(dt * -or_expf(A_log[hd]));
       for (int p = 0; p < P; ++p) {
         float xv = hf(xr[hd * P + p]);
         float X = xv * dt;
@@ -261,7 +331,7 @@ void or_gate(const uint16_t* y, const uint16_t* z, int ld_z, int M, int DI, uint
   for (int m = 0; m < M; ++m)
     for (int k = 0; k < DI; ++k) {
       float zv = hf(z[(size_t)m * ld_z + k]);
-      float sg = hf(or_f2h(1.0f / (1.0f + expf(-zv))));
+      float sg = hf(or_f2h(1.0f / (1.0f + or_expf(-zv))));
       float sz = hf(or_f2h(zv * sg));
       g[(size_t)m * DI + k] = or_f2h(hf(y[(size_t)m * DI + k]) * sz);
     }

@@ -114,8 +114,11 @@ def test_conv_ssm_128_steps(B):
             ys.append((_np16(g_y).astype(np.float32), r_y.astype(np.float32)))
     gh = g_h.cpu().numpy()
     rel = np.abs(gh - r_h).max() / np.abs(r_h).max()
-    print(f"B={B} state max rel err {rel:.3e}")
-    assert rel <= 1e-3
-    np.testing.assert_allclose(_np16(g_conv).astype(np.float32), r_conv.astype(np.float32), atol=2e-3, rtol=2e-3)
+    print(f"B={B} state max rel err {rel:.3e}, bit-exact {np.array_equal(gh, r_h)}")
+    assert rel <= 1e-3                      # the north-star tolerance
+    # the state update uses only correctly rounded elementwise operations on identical inputs,
+    # so it is in fact bit-exact
+    np.testing.assert_array_equal(gh, r_h)
+    np.testing.assert_array_equal(_np16(g_conv).view(np.uint16), r_conv.view(np.uint16))
     for gy, ry in ys:
         assert np.abs(gy - ry).max() <= 1e-3 * np.abs(ry).max() + 1e-3
