@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""DF-SSM decode throughput on one MI355X.
+
+Workload: the 1.3B-shaped DF-SSM (d_model 2048, 48 layers, d_inner 4096,
+64 heads x 64, d_state 128, vocab 50288, rank-16 int8 LoRA, int8 tied embedding) with seeded
+random-init weights, written to and loaded from a .dfssm file; a seeded 32-token prompt per
+sequence is ingested step by step, then greedy decode steps are timed. One step = one token for
+every sequence of the batch: embedding, 48 layers, final norm, tied head, argmax, with the
+greedy token fed back on the device (HIP graph of 8 steps per replay). value = batch * steps /
+seconds over the timed steps, inputs resident in HBM.
+
+Also reported: per-kernel timing of the three layer kernels and the head (HIP events around graphs
+of back-to-back launches, minus the per-launch cost of an empty-kernel graph), the roofline of the
+dominant kernel, the whole-step HBM roofline fraction, and the reference CPU decode (the
+reference's cpu_inference.c, HEADDIM 64, compiled in oracle/_ref) on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 128] [--warmup 16] [--batch 1] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "df-ssm_amd"))
+sys.path.insert(0, REPO)
+
+PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
+STEPS_PER_GRAPH = 8
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(cfg, B):
+    """Bytes a decode step must move: every weight once + SSM/conv state read and written."""
+    from dfssm.format import layer_bytes
+    D, DI, H, P, N, C, V, L = (cfg.d_model, cfg.d_inner, cfg.nheads, cfg.p, cfg.d_state, cfg.d_xbc,
+                               cfg.vocab_size, cfg.n_layer)
+    IPO = cfg.in_proj_out
+    weights = L * layer_bytes(cfg) + V * D + 2 * V + 4 * D
+    state = B * L * 2 * (H * P * N * 4 + C * 3 * 2)
+    per_phase = {
+        # in_proj: bits, scales, LoRA A/B, ln_w, conv w/b, conv state r+w, x in, proj out
+        0: IPO * D // 8 + 2 * IPO + 16 * IPO + 2 * IPO + 16 * D + 32 + 4 * D + 8 * C + 2 * C
+           + B * C * 6 * 2 + B * D * 2 + B * IPO * 2,
+        # SSM: state r+w, x/B/C/dt/z in, params, g out, block partials
+        1: B * H * P * N * 4 * 2 + B * (DI + 2 * N + H + DI) * 2 + 12 * H + B * DI * 2 + B * H * (P // 16) * 8,
+        # out_proj: bits, scales, LoRA, norm_w, g in, partials, x r+w
+        2: D * DI // 8 + 2 * D + 16 * D + 2 * D + 16 * DI + 32 + 4 * DI + B * DI * 2
+           + B * H * (P // 16) * 8 + B * D * 4,
+        # head: int8 table + row scales + norm_f + x
+        3: V * D + 2 * V + 4 * D + B * D * 2,
+    }
+    return weights, state, per_phase
+
+
+def build_model(B, path):
+    import torch
+    from df_ssm_inference import DFSSMModel
+    from dfssm.format import expected_size, write_dfssm
+    from dfssm.synth import config_1p3b, make_weights
+    cfg = config_1p3b()
+    w = None
+    if not (os.path.exists(path) and os.path.getsize(path) == expected_size(cfg)):
+        t = time.time()
+        w = make_weights(cfg, seed=0)
+        write_dfssm(path + ".tmp", w)
+        os.replace(path + ".tmp", path)
+        log(f"wrote synthetic 1.3B model to {path} ({time.time() - t:.1f}s)")
+    t = time.time()
+    m = DFSSMModel(path, device="cuda:0", batch_size=B)
+    torch.cuda.synchronize()
+    log(f"loaded {path} for batch {B} ({time.time() - t:.1f}s)")
+    return m, w
+
+
+def time_decode(m, prompts, steps, warmup):
+    import torch
+    m.reset_state()
+    m.ingest(torch.from_numpy(prompts))
+    g, _ = m._gen_graph(STEPS_PER_GRAPH)
+    for _ in range(max(1, warmup // STEPS_PER_GRAPH)):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // STEPS_PER_GRAPH)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1)
+    return ms, reps * STEPS_PER_GRAPH
+
+
+def time_kernels(m, reps=10):
+    """Per-launch time of each layer kernel (48 launches of one phase per graph) and of the head,
+    and of an empty kernel in the same arrangement (the dispatch cost between dependent launches).
+    Returns {name: (us_per_launch, launches_per_step)} with the empty-kernel cost subtracted."""
+    import torch
+    from dfssm import _C
+    L = m.cfg.n_layer
+    lib = _C.lib()
+
+    def graph_time(body, n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            body()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+    one = torch.zeros(1, device="cuda:0")
+    empty = graph_time(lambda: [one.mul_(1.0) for _ in range(L)], L)
+    out = {"empty": (empty, 0)}
+    names = {0: "in_proj+conv", 1: "ssm+gate", 2: "out_proj+residual"}
+    for p in (0, 1, 2):
+        def body(p=p):
+            for li in range(L):
+                _C.check(lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state,
+                                               m.workspace.data_ptr(), _C.stream()))
+        out[names[p]] = (graph_time(body, L) - empty, L)
+
+    def head():
+        for _ in range(L):
+            _C.check(lib.dfssm_lmhead_argmax(m._model, m.x.data_ptr(), m.workspace.data_ptr(), None,
+                                             m._next.data_ptr(), None, _C.stream()))
+    out["head+argmax"] = (graph_time(head, L) - empty, 1)
+    return out
+
+
+def cpu_baseline(weights, prompt, n_tokens):
+    from oracle import ref_driver
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    if not ref_driver.available():
+        log("reference CPU kernels unavailable (not built or no AVX-512 VNNI on this host)")
+        return None
+    m = ref_driver.RefCPUModel(weights)
+    toks, secs = m.generate(prompt, n_tokens)
+    return {"value": round(n_tokens / secs, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"batch 1, 1.3B shape: warm-up step, reset, {len(prompt)}-token prompt untimed, "
+                      f"{n_tokens} timed greedy steps of the reference cpu_inference.c (HEADDIM 64, "
+                      f"AVX-512 VNNI, OpenMP {threads} threads) + NumPy fp32 head; {secs:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=48)
+    ap.add_argument("--model-path", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_1p3b_seed0.dfssm"))
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
+              "is described in DESIGN.md and not measured", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from dfssm.synth import make_prompts
+
+    B = a.batch
+    m, w = build_model(B, a.model_path)
+    cfg = m.cfg
+    prompts = make_prompts(B, cfg.vocab_size, 32)
+    ms, steps = time_decode(m, prompts, a.steps, a.warmup)
+    ms_per_step = ms / steps
+    tok_s = B * steps / (ms / 1e3)
+    weights, state, per_phase = algorithmic_bytes(cfg, B)
+    step_bytes = weights + state
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode batch {B}: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, "
+        f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / PEAK_GBS:.1f}% of HBM peak)")
+
+    kt = time_kernels(m)
+    phase_of = {"in_proj+conv": 0, "ssm+gate": 1, "out_proj+residual": 2, "head+argmax": 3}
+    kernels = {}
+    for name, (us, n) in kt.items():
+        if name == "empty":
+            continue
+        b = per_phase[phase_of[name]]
+        kernels[name] = {"us_per_launch": round(us, 2), "launches_per_step": n,
+                         "us_per_step": round(us * n, 1), "bytes_per_launch": b,
+                         "gbs": round(b / (us * 1e-6) / 1e9, 1)}
+        log(f"  {name:18s} {us:7.2f} us/launch x{n:2d}  {b / 1e6:8.3f} MB  {b / (us * 1e-6) / 1e9:7.1f} GB/s")
+    log(f"  empty-kernel dispatch cost {kt['empty'][0]:.2f} us/launch (subtracted)")
+    dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
+    d = kernels[dom]
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["gbs"] / PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]}
+
+    cpu = None
+    if not a.no_cpu:
+        from dfssm.format import read_dfssm
+        wts = w if w is not None else read_dfssm(a.model_path)
+        cpu = cpu_baseline(wts, prompts[0], a.cpu_steps)
+        if cpu:
+            log(f"reference CPU: {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": "decode tok/s, 1.3B-shape b=1 & b=32; scaffold matmul % HBM roofline",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded random-init weights of the 1.3B shape, .dfssm file; seeded prompts)",
+        "config": {"workload": f"config3: 1.3B-shape DF-SSM greedy decode, batch {B}, 32-token prompt "
+                               f"ingested, {steps} timed steps", "batch": B, "d_model": cfg.d_model,
+                   "n_layer": cfg.n_layer, "d_inner": cfg.d_inner, "nheads": cfg.nheads, "headdim": cfg.p,
+                   "d_state": cfg.d_state, "vocab": cfg.vocab_size, "embedding": "int8+row scale",
+                   "arith": "1-bit x int8 scaffold (int32 acc), fp16 activations, fp32 SSM state"},
+        "step_roofline": {"bytes_per_step": step_bytes, "weights": weights, "state": state,
+                          "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
+                          "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -51,7 +51,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
 inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-bool kdim_ok(int k) { return k > 0 && k % 512 == 0 && k <= 8192; }
+bool kdim_ok(int k) { return k > 0 && k % 512 == 0 && k <= 5120; }
 
 __global__ void zero_u32_kernel(uint32_t* p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -204,13 +204,13 @@ int dfssm_embed(const dfssm_model* model, const int64_t* tokens, uint16_t* x, vo
   return hip_status(launch_embed(a, r.B, as_stream(stream)));
 }
 
-int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
-                     void* workspace, void* stream) {
+int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
+                      const dfssm_state* state, void* workspace, void* stream) {
   int rc = check_model(model);
   if (rc) return rc;
   if (!x || !state || !state->h || !state->conv || !workspace) return DFSSM_E_NULL;
   const Derived r = derive(&model->dims);
-  if (layer < 0 || layer >= r.L) return DFSSM_E_RANGE;
+  if (layer < 0 || layer >= r.L || phase < 0 || phase > 2) return DFSSM_E_RANGE;
   const dfssm_layer& Lw = model->layers[layer];
   if (!Lw.in_bits || !Lw.in_scale || !Lw.in_lA || !Lw.in_lA_s || !Lw.in_lB || !Lw.in_lB_s ||
       !Lw.out_bits || !Lw.out_scale || !Lw.out_lA || !Lw.out_lA_s || !Lw.out_lB || !Lw.out_lB_s ||
@@ -226,33 +226,32 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
   uint16_t* g = (uint16_t*)(ws + w.g);
   double* slots = (double*)(ws + w.slots);
   hipStream_t s = as_stream(stream);
-  float* h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
-  uint16_t* conv = state->conv + (size_t)layer * r.B * r.C * 3;
 
-  ProjArgs ai{};
-  ai.bits = Lw.in_bits; ai.wscale = Lw.in_scale; ai.lA = Lw.in_lA; ai.lAs = Lw.in_lA_s;
-  ai.lB = Lw.in_lB; ai.lBs = Lw.in_lB_s;
-  ai.act = x; ai.ld_act = r.D; ai.norm_w = Lw.ln_w;
-  ai.out = proj; ai.ld_out = r.IPO;
-  ai.conv_state = conv; ai.conv_w = Lw.conv_w; ai.conv_b = Lw.conv_b;
-  ai.conv_lo = r.DI; ai.conv_c = r.C;
-  ai.N = r.IPO; ai.K = r.D;
-  rc = hip_status(launch_proj(ai, r.B, DFSSM_MODE_IN, s));
-  if (rc) return rc;
-
-  SsmArgs as{};
-  as.h = h;
-  as.xbc = proj + r.DI; as.ld_xbc = r.IPO;
-  as.dt = proj + r.DI + r.C; as.ld_dt = r.IPO;
-  as.z = proj; as.ld_z = r.IPO;
-  as.dt_bias = Lw.dt_bias; as.A_log = Lw.A_log; as.D = Lw.D;
-  as.y_out = g; as.ld_y = r.DI;
-  as.sumsq_slots = slots; as.n_slots = r.n_slots;
-  as.H = r.H; as.P = r.P; as.N = r.N;
-  rc = hip_status(launch_ssm(as, r.B, s));
-  if (rc) return rc;
-
-  ProjArgs ao{};
+  if (phase == 0) {  // RMSNorm + quantize + in_proj scaffold + LoRA + conv/SiLU -> proj
+    ProjArgs ai{};
+    ai.bits = Lw.in_bits; ai.wscale = Lw.in_scale; ai.lA = Lw.in_lA; ai.lAs = Lw.in_lA_s;
+    ai.lB = Lw.in_lB; ai.lBs = Lw.in_lB_s;
+    ai.act = x; ai.ld_act = r.D; ai.norm_w = Lw.ln_w;
+    ai.out = proj; ai.ld_out = r.IPO;
+    ai.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
+    ai.conv_w = Lw.conv_w; ai.conv_b = Lw.conv_b;
+    ai.conv_lo = r.DI; ai.conv_c = r.C;
+    ai.N = r.IPO; ai.K = r.D;
+    return hip_status(launch_proj(ai, r.B, DFSSM_MODE_IN, s));
+  }
+  if (phase == 1) {  // SSM step + gate -> g, per-block sum(g^2)
+    SsmArgs as{};
+    as.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
+    as.xbc = proj + r.DI; as.ld_xbc = r.IPO;
+    as.dt = proj + r.DI + r.C; as.ld_dt = r.IPO;
+    as.z = proj; as.ld_z = r.IPO;
+    as.dt_bias = Lw.dt_bias; as.A_log = Lw.A_log; as.D = Lw.D;
+    as.y_out = g; as.ld_y = r.DI;
+    as.sumsq_slots = slots; as.n_slots = r.n_slots;
+    as.H = r.H; as.P = r.P; as.N = r.N;
+    return hip_status(launch_ssm(as, r.B, s));
+  }
+  ProjArgs ao{};  // gated RMSNorm + quantize + out_proj scaffold + LoRA + residual -> x
   ao.bits = Lw.out_bits; ao.wscale = Lw.out_scale; ao.lA = Lw.out_lA; ao.lAs = Lw.out_lA_s;
   ao.lB = Lw.out_lB; ao.lBs = Lw.out_lB_s;
   ao.act = g; ao.ld_act = r.DI; ao.norm_w = Lw.norm_w;
@@ -260,6 +259,15 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
   ao.out = x; ao.ld_out = r.D;
   ao.N = r.D; ao.K = r.DI;
   return hip_status(launch_proj(ao, r.B, DFSSM_MODE_OUT, s));
+}
+
+int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                     void* workspace, void* stream) {
+  for (int phase = 0; phase < 3; ++phase) {
+    const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
+    if (rc) return rc;
+  }
+  return DFSSM_OK;
 }
 
 int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* workspace,

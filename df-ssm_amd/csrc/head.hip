@@ -24,11 +24,13 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x;
   const int D = a.D, CH = D / 16, CPW = CH / 4;
-  const uint4* E = (const uint4*)a.emb + ((size_t)g * CH + wave * CPW) * 64 + lane;
+  const u32x4* E = (const u32x4*)a.emb + ((size_t)g * CH + wave * CPW) * 64 + lane;
 
-  u32x4 pre[4];
+  // first group of chunks in flight before the prologue (the table does not depend on x)
+  constexpr int G = 8;  // chunks per group; D is a multiple of 512, so CPW is a multiple of 8
+  u32x4 cur[G], nxt[G];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) if (c < CPW) pre[c] = ld_nt(E + (size_t)c * 64);
+  for (int c = 0; c < G; ++c) cur[c] = ld_nt(E + (size_t)c * 64);
 
   for (int m = 0; m < M; ++m) {
     const uint16_t* xm = a.x + (size_t)m * D;
@@ -44,22 +46,24 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   double acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.0;
-  for (int c = 0; c < CPW; ++c) {
-    u32x4 e4;
-    if (c < 4) {
+  for (int c0 = 0; c0 < CPW; c0 += G) {
+    if (c0 + G < CPW) {
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) if (cc == c) e4 = pre[cc];
-    } else {
-      e4 = ld_nt(E + (size_t)c * 64);
+      for (int c = 0; c < G; ++c) nxt[c] = ld_nt(E + (size_t)(c0 + G + c) * 64);
     }
-    const uint32_t ev[4] = {e4.x, e4.y, e4.z, e4.w};
-    const int k0 = (wave * CPW + c) * 16;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const double e = (double)(int)(int8_t)(ev[j >> 2] >> (8 * (j & 3)));
+    for (int c = 0; c < G; ++c) {
+      const u32x4 e4 = cur[c];
+      const int k0 = (wave * CPW + c0 + c) * 16;
 #pragma unroll
-      for (int m = 0; m < M; ++m) acc[m] = __builtin_fma(xf[m * D + k0 + j], e, acc[m]);
+      for (int j = 0; j < 16; ++j) {
+        const double e = (double)(int)(int8_t)(e4[j >> 2] >> (8 * (j & 3)));
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = __builtin_fma(xf[m * D + k0 + j], e, acc[m]);
+      }
     }
+#pragma unroll
+    for (int c = 0; c < G; ++c) cur[c] = nxt[c];
   }
 #pragma unroll
   for (int m = 0; m < M; ++m) part[wave][m][lane] = acc[m];

@@ -14,7 +14,7 @@
  *
  * Model-specific constraints (checked by dfssm_check_dims): d_state = 128, ngroups = 1,
  * LoRA rank 16, d_conv = 4, P = d_inner / nheads a multiple of 16, d_model and d_inner multiples
- * of 512 and at most 8192, nheads a multiple of 8, batch 1..4, int8 embedding (emb_code 1).
+ * of 512 and at most 5120, nheads a multiple of 8, batch 1..4, int8 embedding (emb_code 1).
  */
 #ifndef DFSSM_H
 #define DFSSM_H
@@ -130,6 +130,13 @@ int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace);
  * _run_layers, df_ssm_inference.py:161-207. 3 kernel launches. */
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream);
+
+/* One of the three kernels of dfssm_layer_step: phase 0 = RMSNorm + in_proj + LoRA + conv/SiLU
+ * (df_ssm_inference.py:165-182), 1 = SSM step + gate (:185-195), 2 = gated RMSNorm + out_proj +
+ * LoRA + residual (:196-207). Running phases 0, 1, 2 in order equals dfssm_layer_step; exposed
+ * for per-kernel timing and for callers that interleave their own work. */
+int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
+                      const dfssm_state* state, void* workspace, void* stream);
 
 /* Final RMSNorm, tied int8 head and greedy argmax: logits (batch, V) fp16 (may be NULL),
  * next (batch) int64. If x_next is non-NULL the embedding of `next` is written there (it may
