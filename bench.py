@@ -9,7 +9,7 @@ every sequence of the batch: embedding, 48 layers, final norm, tied head, argmax
 greedy token fed back on the device (HIP graph of 8 steps per replay). value = batch * steps /
 seconds over the timed steps, inputs resident in HBM.
 
-Also reported: per-kernel timing of the three layer kernels and the head (HIP events around graphs
+Also reported: per-kernel timing of the five layer kernels and the head (HIP events around graphs
 of back-to-back launches, minus the per-launch cost of an empty-kernel graph), the roofline of the
 dominant kernel, the whole-step HBM roofline fraction, and the reference CPU decode (the
 reference's cpu_inference.c, HEADDIM 64, compiled in oracle/_ref) on a bounded sample.
@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(REPO, "df-ssm_amd"))
 sys.path.insert(0, REPO)
 
 PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
+PHASE_NAMES = ("prep_in", "in_proj+conv", "ssm+gate", "prep_out", "out_proj+residual")
 STEPS_PER_GRAPH = 8
 
 
@@ -44,15 +45,19 @@ def algorithmic_bytes(cfg, B):
     IPO = cfg.in_proj_out
     weights = L * layer_bytes(cfg) + V * D + 2 * V + 4 * D
     state = B * L * 2 * (H * P * N * 4 + C * 3 * 2)
+    ns = H * (P // 16)  # SSM blocks per sequence (partials of sum(g^2))
     per_phase = {
-        # in_proj: bits, scales, LoRA A/B, ln_w, conv w/b, conv state r+w, x in, proj out
-        0: IPO * D // 8 + 2 * IPO + 16 * IPO + 2 * IPO + 16 * D + 32 + 4 * D + 8 * C + 2 * C
-           + B * C * 6 * 2 + B * D * 2 + B * IPO * 2,
+        # prep_in: x, ln_w, LoRA B + scales in; q bytes, bit planes, scalars, h out
+        0: B * D * 2 + 4 * D + 16 * D + 32 + B * (2 * D + 8 + 64),
+        # gemv_in: bits, scales, LoRA A + scales, planes + prep scalars, conv w/b + state r+w, proj out
+        1: IPO * D // 8 + 2 * IPO + 16 * IPO + 2 * IPO + B * (D + 8 + 64) + 8 * C + 2 * C
+           + B * C * 6 * 2 + B * IPO * 2,
         # SSM: state r+w, x/B/C/dt/z in, params, g out, block partials
-        1: B * H * P * N * 4 * 2 + B * (DI + 2 * N + H + DI) * 2 + 12 * H + B * DI * 2 + B * H * (P // 16) * 8,
-        # out_proj: bits, scales, LoRA, norm_w, g in, partials, x r+w
-        2: D * DI // 8 + 2 * D + 16 * D + 2 * D + 16 * DI + 32 + 4 * DI + B * DI * 2
-           + B * H * (P // 16) * 8 + B * D * 4,
+        1.5: B * H * P * N * 4 * 2 + B * (DI + 2 * N + H + DI) * 2 + 12 * H + B * DI * 2 + B * ns * 8,
+        # prep_out: g, partials, norm_w, LoRA B + scales in; q, planes, scalars, h out
+        2: B * DI * 2 + B * ns * 8 + 4 * DI + 16 * DI + 32 + B * (2 * DI + 8 + 64),
+        # gemv_out: bits, scales, LoRA A + scales, planes + scalars, x r+w
+        2.5: D * DI // 8 + 2 * D + 16 * D + 2 * D + B * (DI + 8 + 64) + B * D * 4,
         # head: int8 table + row scales + norm_f + x
         3: V * D + 2 * V + 4 * D + B * D * 2,
     }
@@ -124,13 +129,12 @@ def time_kernels(m, reps=10):
     one = torch.zeros(1, device="cuda:0")
     empty = graph_time(lambda: [one.mul_(1.0) for _ in range(L)], L)
     out = {"empty": (empty, 0)}
-    names = {0: "in_proj+conv", 1: "ssm+gate", 2: "out_proj+residual"}
-    for p in (0, 1, 2):
+    for p, name in enumerate(PHASE_NAMES):
         def body(p=p):
             for li in range(L):
                 _C.check(lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state,
                                                m.workspace.data_ptr(), _C.stream()))
-        out[names[p]] = (graph_time(body, L) - empty, L)
+        out[name] = (graph_time(body, L) - empty, L)
 
     def head():
         for _ in range(L):
@@ -187,7 +191,8 @@ def main():
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / PEAK_GBS:.1f}% of HBM peak)")
 
     kt = time_kernels(m)
-    phase_of = {"in_proj+conv": 0, "ssm+gate": 1, "out_proj+residual": 2, "head+argmax": 3}
+    phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
+                "head+argmax": 3}
     kernels = {}
     for name, (us, n) in kt.items():
         if name == "empty":

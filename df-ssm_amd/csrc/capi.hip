@@ -30,7 +30,7 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, part_val, part_idx, ticket, err, total;
+  size_t proj, g, slots, q, planes, qsum, xs, h, part_val, part_idx, ticket, err, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -40,6 +40,12 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.proj = off;     off = align_up(off + (size_t)r.B * r.IPO * 2);
   w.g = off;        off = align_up(off + (size_t)r.B * r.DI * 2);
   w.slots = off;    off = align_up(off + (size_t)r.B * r.n_slots * 8);
+  const int kq = r.D > r.DI ? r.D : r.DI;  // row stride of the prep buffers
+  w.q = off;        off = align_up(off + (size_t)r.B * kq);
+  w.planes = off;   off = align_up(off + (size_t)r.B * kq);
+  w.qsum = off;     off = align_up(off + (size_t)r.B * 4);
+  w.xs = off;       off = align_up(off + (size_t)r.B * 4);
+  w.h = off;        off = align_up(off + (size_t)r.B * 16 * 4);
   w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.ticket = off;   off = align_up(off + 4);
@@ -127,12 +133,12 @@ int dfssm_rmsnorm_quantize(const uint16_t* x, const float* w, int M, int K, uint
                            int8_t* q_out, uint16_t* s_out, void* stream) {
   if (!x || !w || !xn_out || !q_out || !s_out) return DFSSM_E_NULL;
   if (M < 1 || !kdim_ok(K)) return DFSSM_E_DIMS;
-  ProjArgs a{};
-  a.act = x;
-  a.ld_act = K;
-  a.norm_w = w;
+  PrepArgs a{};
+  a.act = x; a.ld_act = K; a.norm_w = w;
+  a.q_out = q_out; a.ld_q = K;
+  a.xn_out = xn_out; a.xs16_out = s_out;
   a.K = K;
-  return hip_status(launch_prologue(a, M, xn_out, q_out, s_out, as_stream(stream)));
+  return hip_status(launch_prep(a, M, DFSSM_MODE_IN, as_stream(stream)));
 }
 
 int dfssm_conv_step(uint16_t* conv_state, uint16_t* xbc, int ld_xbc, const uint16_t* conv_w,
@@ -210,36 +216,44 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
   if (rc) return rc;
   if (!x || !state || !state->h || !state->conv || !workspace) return DFSSM_E_NULL;
   const Derived r = derive(&model->dims);
-  if (layer < 0 || layer >= r.L || phase < 0 || phase > 2) return DFSSM_E_RANGE;
+  if (layer < 0 || layer >= r.L || phase < 0 || phase >= DFSSM_LAYER_PHASES) return DFSSM_E_RANGE;
   const dfssm_layer& Lw = model->layers[layer];
   if (!Lw.in_bits || !Lw.in_scale || !Lw.in_lA || !Lw.in_lA_s || !Lw.in_lB || !Lw.in_lB_s ||
       !Lw.out_bits || !Lw.out_scale || !Lw.out_lA || !Lw.out_lA_s || !Lw.out_lB || !Lw.out_lB_s ||
       !Lw.conv_w || !Lw.conv_b || !Lw.A_log || !Lw.D || !Lw.dt_bias || !Lw.norm_w || !Lw.ln_w)
     return DFSSM_E_NULL;
   if (!aligned16(Lw.in_bits) || !aligned16(Lw.out_bits) || !aligned16(Lw.in_lA) ||
-      !aligned16(Lw.out_lA) || !aligned16(state->h) || ((uintptr_t)Lw.in_lB & 3u) ||
-      ((uintptr_t)Lw.out_lB & 3u) || !aligned16(workspace))
+      !aligned16(Lw.out_lA) || !aligned16(state->h) || ((uintptr_t)Lw.in_lB & 7u) ||
+      ((uintptr_t)Lw.out_lB & 7u) || !aligned16(workspace) || !aligned16(Lw.ln_w) || !aligned16(Lw.norm_w))
     return DFSSM_E_ALIGN;
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
   uint16_t* proj = (uint16_t*)(ws + w.proj);
   uint16_t* g = (uint16_t*)(ws + w.g);
   double* slots = (double*)(ws + w.slots);
+  const int kq = r.D > r.DI ? r.D : r.DI;
   hipStream_t s = as_stream(stream);
 
-  if (phase == 0) {  // RMSNorm + quantize + in_proj scaffold + LoRA + conv/SiLU -> proj
-    ProjArgs ai{};
-    ai.bits = Lw.in_bits; ai.wscale = Lw.in_scale; ai.lA = Lw.in_lA; ai.lAs = Lw.in_lA_s;
-    ai.lB = Lw.in_lB; ai.lBs = Lw.in_lB_s;
-    ai.act = x; ai.ld_act = r.D; ai.norm_w = Lw.ln_w;
-    ai.out = proj; ai.ld_out = r.IPO;
-    ai.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
-    ai.conv_w = Lw.conv_w; ai.conv_b = Lw.conv_b;
-    ai.conv_lo = r.DI; ai.conv_c = r.C;
-    ai.N = r.IPO; ai.K = r.D;
-    return hip_status(launch_proj(ai, r.B, DFSSM_MODE_IN, s));
+  if (phase == 0 || phase == 3) {  // prologue of in_proj (x) / out_proj (gated g)
+    PrepArgs p{};
+    const bool in = phase == 0;
+    p.act = in ? x : g;
+    p.ld_act = in ? r.D : r.DI;
+    p.norm_w = in ? Lw.ln_w : Lw.norm_w;
+    p.sumsq_slots = in ? nullptr : slots;
+    p.n_slots = in ? 0 : r.n_slots;
+    p.lB = in ? Lw.in_lB : Lw.out_lB;
+    p.lBs = in ? Lw.in_lB_s : Lw.out_lB_s;
+    p.q_out = (int8_t*)(ws + w.q);
+    p.planes_out = (uint32_t*)(ws + w.planes);
+    p.ld_q = kq;
+    p.s_out = (int*)(ws + w.qsum);
+    p.xs_out = (float*)(ws + w.xs);
+    p.h_out = (float*)(ws + w.h);
+    p.K = in ? r.D : r.DI;
+    return hip_status(launch_prep(p, r.B, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s));
   }
-  if (phase == 1) {  // SSM step + gate -> g, per-block sum(g^2)
+  if (phase == 2) {  // SSM step + gate -> g, per-block sum(g^2)
     SsmArgs as{};
     as.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
     as.xbc = proj + r.DI; as.ld_xbc = r.IPO;
@@ -251,19 +265,31 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
     as.H = r.H; as.P = r.P; as.N = r.N;
     return hip_status(launch_ssm(as, r.B, s));
   }
-  ProjArgs ao{};  // gated RMSNorm + quantize + out_proj scaffold + LoRA + residual -> x
-  ao.bits = Lw.out_bits; ao.wscale = Lw.out_scale; ao.lA = Lw.out_lA; ao.lAs = Lw.out_lA_s;
-  ao.lB = Lw.out_lB; ao.lBs = Lw.out_lB_s;
-  ao.act = g; ao.ld_act = r.DI; ao.norm_w = Lw.norm_w;
-  ao.sumsq_slots = slots; ao.n_slots = r.n_slots;
-  ao.out = x; ao.ld_out = r.D;
-  ao.N = r.D; ao.K = r.DI;
-  return hip_status(launch_proj(ao, r.B, DFSSM_MODE_OUT, s));
+  ProjArgs a{};
+  a.planes = (const uint32_t*)(ws + w.planes);
+  a.ld_q = kq;
+  a.qsum = (const int*)(ws + w.qsum);
+  a.xs = (const float*)(ws + w.xs);
+  a.h = (const float*)(ws + w.h);
+  if (phase == 1) {  // in_proj scaffold + LoRA + conv/SiLU -> proj
+    a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
+    a.out = proj; a.ld_out = r.IPO;
+    a.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
+    a.conv_w = Lw.conv_w; a.conv_b = Lw.conv_b;
+    a.conv_lo = r.DI; a.conv_c = r.C;
+    a.N = r.IPO; a.K = r.D;
+    return hip_status(launch_proj(a, r.B, DFSSM_MODE_IN, s));
+  }
+  // phase 4: out_proj scaffold + LoRA + residual -> x
+  a.bits = Lw.out_bits; a.wscale = Lw.out_scale; a.lA = Lw.out_lA; a.lAs = Lw.out_lA_s;
+  a.out = x; a.ld_out = r.D;
+  a.N = r.D; a.K = r.DI;
+  return hip_status(launch_proj(a, r.B, DFSSM_MODE_OUT, s));
 }
 
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream) {
-  for (int phase = 0; phase < 3; ++phase) {
+  for (int phase = 0; phase < DFSSM_LAYER_PHASES; ++phase) {
     const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
     if (rc) return rc;
   }

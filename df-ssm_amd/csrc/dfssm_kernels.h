@@ -8,18 +8,36 @@
 
 namespace dfssm {
 
-struct ProjArgs {
-  const uint32_t* bits;      // tiled sign bits [N_pad/64][K/128][64][4]
-  const uint16_t* wscale;    // (N) fp16 per-row scale
-  const int8_t* lA;          // (N, 16) LoRA A, int8
-  const uint16_t* lAs;       // (N) fp16
-  const int8_t* lB;          // (16, K) LoRA B, int8
-  const uint16_t* lBs;       // (16) fp16
+// Prologue of a projection, once per activation row (prep_kernel).
+struct PrepArgs {
   const uint16_t* act;       // activation rows (M, ld_act) fp16: x (IN) or gated g (OUT)
   int ld_act;
   const float* norm_w;       // (K) fp32 RMSNorm weight: ln_w (IN) or norm_w (OUT)
   const double* sumsq_slots; // OUT: (M, n_slots) per-block sum(g^2) from the SSM kernel
   int n_slots;
+  const int8_t* lB;          // (16, K) LoRA B, int8 (null: no LoRA intermediate)
+  const uint16_t* lBs;       // (16) fp16
+  int8_t* q_out;             // (M, ld_q) int8 activations, or null
+  uint32_t* planes_out;      // (M, ld_q/32, 8) bit planes of q, or null
+  int ld_q;
+  int* s_out;                // (M) sum of q
+  float* xs_out;             // (M) activation scale (an fp16 value)
+  float* h_out;              // (M, 16) LoRA intermediate (fp16 values)
+  uint16_t* xn_out;          // (M, K) normalized activations, or null
+  uint16_t* xs16_out;        // (M) activation scale as fp16 bits, or null
+  int K;
+};
+
+struct ProjArgs {
+  const uint32_t* bits;      // tiled sign bits [N_pad/64][K/128][64][4]
+  const uint16_t* wscale;    // (N) fp16 per-row scale
+  const int8_t* lA;          // (N, 16) LoRA A, int8
+  const uint16_t* lAs;       // (N) fp16
+  const uint32_t* planes;    // prep: (M, ld_q/32, 8) bit planes
+  int ld_q;
+  const int* qsum;           // prep: (M)
+  const float* xs;           // prep: (M)
+  const float* h;            // prep: (M, 16)
   uint16_t* out;             // IN: proj (M, ld_out); OUT: residual x (M, ld_out), updated in place
   int ld_out;
   int32_t* acc_out;          // optional (M, N) int32 scaffold accumulators
@@ -91,7 +109,7 @@ struct EmbedArgs {
 };
 
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);
-hipError_t launch_prologue(const ProjArgs& a, int M, uint16_t* xn, int8_t* q, uint16_t* s, hipStream_t st);
+hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s);
 hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s);
 hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);

@@ -10,12 +10,8 @@
 //   acc = sum_k q_k * (2 bit_k - 1) = 2 * sum_{bit=1} q - sum_k q_k          (exact int32)
 // i.e. 16 VALU ops (and + bcnt-accumulate per plane) per 32 weights per activation row.
 //
-// Prologue (every workgroup recomputes it; the activation vector is 4-10 KiB and L2-resident):
-//   MODE_IN : xn = RMSNorm(x) * ln_w             (df_ssm_inference.py:141-145,165)
-//   MODE_OUT: yn = RMSNorm(g) * norm_w with sum(g^2) taken from the SSM kernel's per-block
-//             partials                            (df_ssm_inference.py:194-196)
-//   then the int8 quantizer (:147-152), the bit planes, sum q, and the rank-16 LoRA
-//   intermediate h16 = fp16(xn @ B16^T)          (:173,204).
+// The prologue of a projection (RMSNorm, int8 quantizer, bit planes, sum q, rank-16 LoRA
+// intermediate) runs once per sequence in prep_kernel; the GEMV kernels read its results.
 // Epilogue per row n: y = fp16(fp16(fp16(acc) * s_x) * s_w[n]) (:158), out = fp16(y + h16.A16[n])
 // (:173,204); MODE_IN additionally applies the depthwise conv + SiLU to the xBC rows
 // (df_ssm_kernels.cu:27-47) and writes z | xBC | dt_raw; MODE_OUT adds the residual (:207).
@@ -26,147 +22,97 @@ namespace dfssm {
 
 constexpr int kMaxK = 5120;          // largest d_model / d_inner supported
 
-// Workgroup size: 1024 threads (16 waves) for one activation row, so the redundant prologue is
-// spread over the whole CU; 512 for 2..4 rows, which need more registers per thread.
-template <int M> struct ProjShape {
-  static constexpr int NT = M == 1 ? 1024 : 512;
-  static constexpr int NW = NT / 64;
-  static constexpr int MaxCPW = (kMaxK / 128 + NW - 1) / NW;  // 16-byte bit chunks per lane
-  static constexpr int MaxLB = 16 * kMaxK / NT / 8;            // 8-byte LoRA-B vectors per thread
-  static constexpr int Slices = NT / 16;                        // LoRA-h column slices
+// ------------------------------------------------------------------------------------------
+// prep_kernel: the per-projection prologue, computed once per sequence (16 workgroups of 1024
+// threads per activation row m):
+//   MODE_IN : xn = fp16((x * r) * ln_w), r = 1/sqrt(sum(x^2)/K + 1e-5)  (df_ssm_inference.py:141-145)
+//   MODE_OUT: the same on the gated g with sum(g^2) from the SSM kernel's per-block partials
+//   s = fp16(fp16(max(amax, 1e-4)) / 127), q = clamp(rne(fp16(xn / s)))     (:147-152)
+//   planes[m][word][b] = bit b of q for the 32 columns of `word`; S = sum q
+//   h[m][r] = fp16(sum_k xn_k * fp16(B_i8[r,k] * B_s[r]))                   (:83,173,204)
+// ------------------------------------------------------------------------------------------
+constexpr int kPT = 1024;
+constexpr int kPW = kPT / 64;
+
+struct PrepLds {
+  uint16_t xn[kMaxK];
+  double red_d[kPW];
+  float red_f[kPW];
+  int red_i[kPW];
 };
 
-template <int M>
-struct ProjLds {
-  uint32_t planes[M][kMaxK / 32][8];  // bit planes of q, per 32-column word
-  uint16_t xn[M][kMaxK];              // normalized activations (fp16)
-  double lora_part[M][DFSSM_LORA_R][ProjShape<M>::Slices];
-  float hl[M][DFSSM_LORA_R];          // h16 values (as float)
-  int T[ProjShape<M>::NW][M][64];     // per-wave partial sum_{bit=1} q
-  double red_d[ProjShape<M>::NW][M];
-  float red_f[ProjShape<M>::NW][M];
-  int red_i[ProjShape<M>::NW][M];
-  int S[M];
-  float xs[M];
-};
-
-// Block reductions of M values at once (one pair of barriers for all rows).
-template <int M, int kNW>
-__device__ __forceinline__ void block_sum_f64_m(double (&v)[M], double (&red)[kNW][M]) {
-#pragma unroll
-  for (int m = 0; m < M; ++m) v[m] = wave_sum_f64(v[m]);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0)
-#pragma unroll
-    for (int m = 0; m < M; ++m) red[threadIdx.x >> 6][m] = v[m];
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    double t = 0.0;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) t += red[w][m];
-    v[m] = t;
-  }
-}
-template <int M, int kNW>
-__device__ __forceinline__ void block_max_f32_m(float (&v)[M], float (&red)[kNW][M]) {
-#pragma unroll
-  for (int m = 0; m < M; ++m) v[m] = wave_max_f32(v[m]);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0)
-#pragma unroll
-    for (int m = 0; m < M; ++m) red[threadIdx.x >> 6][m] = v[m];
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float t = red[0][m];
-#pragma unroll
-    for (int w = 1; w < kNW; ++w) t = fmaxf(t, red[w][m]);
-    v[m] = t;
-  }
-}
-template <int M, int kNW>
-__device__ __forceinline__ void block_sum_i32_m(int (&v)[M], int (&red)[kNW][M]) {
-#pragma unroll
-  for (int m = 0; m < M; ++m) v[m] = wave_sum_i32(v[m]);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0)
-#pragma unroll
-    for (int m = 0; m < M; ++m) red[threadIdx.x >> 6][m] = v[m];
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    int t = 0;
-#pragma unroll
-    for (int w = 0; w < kNW; ++w) t += red[w][m];
-    v[m] = t;
-  }
-}
-
-// Prologue for all M activation rows. av[m] is the 16-byte vector `tid` of row m (K <= 8 * kNT),
-// lb the thread's LoRA-B slice (row tid % 16, columns (tid / 16) * K / 64 ..). Builds xn (LDS), the
-// scales, the bit planes, sum q, and h16.
-template <int M, int MODE>
-__device__ __forceinline__ void proj_prologue(const ProjArgs& a, const u32x4 (&av)[M], const double (&slot_part)[M],
-                                              const uint2 (&lb)[ProjShape<M>::MaxLB], ProjLds<M>& L) {
-  constexpr int kNT = ProjShape<M>::NT, kNW = ProjShape<M>::NW, kMaxLB = ProjShape<M>::MaxLB;
-  const int K = a.K, tid = threadIdx.x, lane = tid & 63;
+// Grid (16, M): workgroup (r, m) recomputes the normalization and quantization of row m (K
+// elements, a few per thread), writes the q bytes and bit planes of column slice r (K/16 columns),
+// and the LoRA intermediate h[m][r]; workgroup (0, m) also writes sum q and the scale.
+template <int MODE>
+__global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
+  __shared__ PrepLds L;
+  const int rr = blockIdx.x, m = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int K = a.K;
   const bool has_v = tid < K / 8;
-  // 1) sum of squares -> r (MODE_OUT: the SSM kernel's per-block partials)
-  double ss[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    if (MODE == DFSSM_MODE_IN) {
-      double part = 0.0;
-      if (has_v) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const double xv = (double)h2f((uint16_t)(av[m][e >> 1] >> (16 * (e & 1))));
-          part += xv * xv;
-        }
-      }
-      ss[m] = part;
-    } else {
-      ss[m] = slot_part[m];
-    }
-  }
-  block_sum_f64_m<M, kNW>(ss, L.red_d);
-  // 2) xn = fp16((x * r) * w) into LDS, amax
-  float amax[M];
+  const uint16_t* act = a.act + (size_t)m * a.ld_act;
+  // loads first: the activation vector, norm weights, LoRA-B row r, the partials
+  const u32x4 av = has_v ? *(const u32x4*)(act + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
   f32x4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = {0.f, 0.f, 0.f, 0.f};
+  uint2 b8 = make_uint2(0u, 0u);
   if (has_v) {
     w0 = *(const f32x4*)(a.norm_w + 8 * tid);
     w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
+    if (a.lB) b8 = *(const uint2*)(a.lB + (size_t)rr * K + 8 * tid);
   }
-  const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float var = (float)ss[m] * (1.0f / (float)K);
-    const float r = 1.0f / sqrt_rn(var + 1e-5f);
-    float mx = 0.0f;
+  const float bs = a.lB ? h2f(a.lBs[rr]) : 0.0f;
+  double part = 0.0;
+  if (MODE == DFSSM_MODE_IN) {
     if (has_v) {
-      uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float x0 = r16((h2f((uint16_t)(av[m][e >> 1])) * r) * wv[e]);
-        const float x1 = r16((h2f((uint16_t)(av[m][e >> 1] >> 16)) * r) * wv[e + 1]);
-        mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
-        o[e >> 1] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+      for (int e = 0; e < 8; ++e) {
+        const double xv = (double)h2f((uint16_t)(av[e >> 1] >> (16 * (e & 1))));
+        part += xv * xv;
       }
-      *(u32x4*)&L.xn[m][8 * tid] = u32x4{o[0], o[1], o[2], o[3]};
     }
-    amax[m] = mx;
+  } else {
+    for (int j = tid; j < a.n_slots; j += kPT) part += a.sumsq_slots[(size_t)m * a.n_slots + j];
   }
-  block_max_f32_m<M, kNW>(amax, L.red_f);  // also publishes xn to the block
-  // 3) q, planes (ballot over 64 consecutive columns; lanes 0..15 collect the 16 words), sum q
-  int qsum[M];
+  const double ss = block_sum_f64<kPT>(part, L.red_d);
+  // xn into LDS, amax
+  const float var = (float)ss * (1.0f / (float)K);
+  const float r = 1.0f / sqrt_rn(var + 1e-5f);
+  const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+  float mx = 0.0f;
+  double hacc = 0.0;
+  if (has_v) {
+    uint32_t o[4];
+    const uint32_t bw[2] = {b8.x, b8.y};
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float xs = quant_scale(amax[m]);
-    int acc = 0;
-    for (int k0 = (tid & ~63); k0 < K; k0 += kNT) {
-      const int q = quant_i8(h2f(L.xn[m][k0 + lane]), xs);
-      acc += q;
+    for (int e = 0; e < 8; e += 2) {
+      const float x0 = r16((h2f((uint16_t)(av[e >> 1])) * r) * wv[e]);
+      const float x1 = r16((h2f((uint16_t)(av[e >> 1] >> 16)) * r) * wv[e + 1]);
+      mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
+      o[e >> 1] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+      // LoRA intermediate of rank r over this thread's 8 columns (fp16 x fp16 is exact in fp32)
+      const float b0 = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
+      const float b1 = r16((float)(int8_t)(bw[(e + 1) >> 2] >> (8 * ((e + 1) & 3))) * bs);
+      hacc += (double)(x0 * b0);
+      hacc += (double)(x1 * b1);
+    }
+    const u32x4 ov = {o[0], o[1], o[2], o[3]};
+    *(u32x4*)&L.xn[8 * tid] = ov;
+    if (a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = ov;
+  }
+  if (a.lB) {
+    const double ht = block_sum_f64<kPT>(hacc, L.red_d);
+    if (tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + rr] = r16((float)ht);
+  }
+  const float amax = block_max_f32<kPT>(mx, L.red_f);  // also publishes xn to the block
+  const float xs = quant_scale(amax);
+  // q over all columns (for sum q); bytes and bit planes written for slice rr only
+  const int lo = rr * (K / 16), hi = lo + K / 16;
+  int qsum = 0;
+  for (int k0 = (tid & ~63); k0 < K; k0 += kPT) {
+    const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
+    qsum += q;
+    if (k0 >= lo && k0 < hi) {
+      if (a.q_out) a.q_out[(size_t)m * a.ld_q + k0 + lane] = (int8_t)q;
       const uint32_t qb = (uint32_t)q & 0xffu;
       uint32_t pw = 0u;
 #pragma unroll
@@ -175,71 +121,53 @@ __device__ __forceinline__ void proj_prologue(const ProjArgs& a, const u32x4 (&a
         pw = lane == b ? (uint32_t)mask : pw;
         pw = lane == 8 + b ? (uint32_t)(mask >> 32) : pw;
       }
-      if (lane < 16) L.planes[m][k0 / 32 + (lane >> 3)][lane & 7] = pw;
-    }
-    qsum[m] = acc;
-    if (tid == 0) L.xs[m] = xs;
-  }
-  block_sum_i32_m<M, kNW>(qsum, L.red_i);
-  // 4) LoRA intermediate h16[m][r] = fp16(sum_k xn_k * fp16(B_i8[r,k] * B_s[r])):
-  //    thread (r = tid % 16, slice = tid / 16) covers K/64 columns from registers.
-  if (a.lB) {
-    const int rr = tid & 15, slice = tid >> 4, per = K / (kNT / 16), nlb = per / 8;
-    const float bs = h2f(a.lBs[rr]);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      double acc[2] = {0.0, 0.0};
-      const uint16_t* xr = &L.xn[m][slice * per];
-#pragma unroll
-      for (int i = 0; i < kMaxLB; ++i) {
-        if (i < nlb) {
-          const uint2 bv = lb[i];
-          const u32x4 x8 = *(const u32x4*)(xr + 8 * i);
-          const uint32_t bw[2] = {bv.x, bv.y};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float b16 = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
-            const float xv = h2f((uint16_t)(x8[e >> 1] >> (16 * (e & 1))));
-            acc[e & 1] += (double)(xv * b16);   // fp16 x fp16 is exact in fp32
-          }
-        }
-      }
-      L.lora_part[m][rr][slice] = acc[0] + acc[1];
-    }
-    __syncthreads();
-    if (tid < M * DFSSM_LORA_R) {
-      const int m = tid >> 4, r = tid & 15;
-      double t = 0.0;
-#pragma unroll 8
-      for (int s = 0; s < kNT / 16; ++s) t += L.lora_part[m][r][s];
-      L.hl[m][r] = r16((float)t);
+      if (a.planes_out && lane < 16)
+        a.planes_out[((size_t)m * (a.ld_q / 32) + k0 / 32 + (lane >> 3)) * 8 + (lane & 7)] = pw;
     }
   }
-  if (tid < M) L.S[tid] = qsum[tid];
-  __syncthreads();
+  if (rr == 0) {
+    const int S = block_sum_i32<kPT>(qsum, L.red_i);
+    if (tid == 0) {
+      if (a.s_out) a.s_out[m] = S;
+      if (a.xs_out) a.xs_out[m] = xs;
+      if (a.xs16_out) a.xs16_out[m] = f2h(xs);
+    }
+  }
 }
 
+// ------------------------------------------------------------------------------------------
+// proj_kernel: 1-bit scaffold GEMV for M <= 4 activation rows + fused epilogue.
+// One workgroup (1024 threads, 16 waves) owns 64 output rows; lane l of every wave owns row
+// 64 g + l and wave w streams the 16-byte column chunks w, w + 16, ... of those rows. The bit
+// planes, sum q, scale and LoRA intermediate come from prep_kernel.
+// ------------------------------------------------------------------------------------------
+constexpr int kNT = 1024;
+constexpr int kNW = kNT / 64;
+constexpr int kMaxCPW = (kMaxK / 128 + kNW - 1) / kNW;
+
+template <int M>
+struct ProjLds {
+  uint32_t planes[M][kMaxK / 32][8];
+  int T[kNW][M][64];
+  float hl[M][DFSSM_LORA_R];
+  int S[M];
+  float xs[M];
+};
+
 template <int M, int MODE>
-__global__ __launch_bounds__(ProjShape<M>::NT) void proj_kernel(ProjArgs a) {
-  constexpr int kNT = ProjShape<M>::NT, kNW = ProjShape<M>::NW;
-  constexpr int kMaxCPW = ProjShape<M>::MaxCPW, kMaxLB = ProjShape<M>::MaxLB;
+__global__ __launch_bounds__(kNT) void proj_kernel(ProjArgs a) {
   __shared__ ProjLds<M> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x;
-  const int K = a.K, CH = K / 128;
+  const int K = a.K, CH = K / 128, KW = K / 32;
 
-  // ---- every load that does not depend on another workgroup's output, issued first ----
-  u32x4 av[M];
+  // ---- loads: this lane's sign-bit chunks (independent of the activations) first ----
+  const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + lane;
+  u32x4 wb[kMaxCPW];
 #pragma unroll
-  for (int m = 0; m < M; ++m)
-    av[m] = tid < K / 8 ? *(const u32x4*)(a.act + (size_t)m * a.ld_act + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
-  double slot_part[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    double p = 0.0;
-    if (MODE == DFSSM_MODE_OUT)
-      for (int j = tid; j < a.n_slots; j += kNT) p += a.sumsq_slots[(size_t)m * a.n_slots + j];
-    slot_part[m] = p;
+  for (int j = 0; j < kMaxCPW; ++j) {
+    const int c = wave + kNW * j;
+    wb[j] = c < CH ? ld_nt(bits + (size_t)c * 64) : u32x4{0u, 0u, 0u, 0u};
   }
   // epilogue row data: thread (m = tid / 64, row n = 64 g + lane)
   const int n = g * 64 + lane;
@@ -264,24 +192,18 @@ __global__ __launch_bounds__(ProjShape<M>::NT) void proj_kernel(ProjArgs a) {
     }
     if (MODE == DFSSM_MODE_OUT) xres = a.out[(size_t)em * a.ld_out + n];
   }
-  // LoRA-B slice of this thread
-  uint2 lb[kMaxLB];
-  {
-    const int rr = tid & 15, slice = tid >> 4, per = K / (kNT / 16), nlb = per / 8;
-    const int8_t* src = a.lB ? a.lB + (size_t)rr * K + slice * per : nullptr;
-#pragma unroll
-    for (int i = 0; i < kMaxLB; ++i) lb[i] = (src && i < nlb) ? *(const uint2*)(src + 8 * i) : make_uint2(0u, 0u);
+  // prep results: planes (M * K bytes), scale, sum q, LoRA intermediate
+  const int pv = M * KW * 8 / 4;  // 16-byte vectors of planes
+  for (int i = tid; i < pv; i += kNT) {
+    const int m = i / (KW * 2), r = i % (KW * 2);
+    *((u32x4*)&L.planes[m][0][0] + r) = *((const u32x4*)(a.planes + (size_t)m * (a.ld_q / 32) * 8) + r);
   }
-  // this lane's sign-bit chunks: wave w takes chunks w, w + 16, ... of the row group
-  const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + lane;
-  u32x4 wb[kMaxCPW];
-#pragma unroll
-  for (int j = 0; j < kMaxCPW; ++j) {
-    const int c = wave + kNW * j;
-    wb[j] = c < CH ? ld_nt(bits + (size_t)c * 64) : u32x4{0u, 0u, 0u, 0u};
+  if (tid < M * DFSSM_LORA_R) L.hl[tid >> 4][tid & 15] = a.h[(size_t)(tid >> 4) * DFSSM_LORA_R + (tid & 15)];
+  if (tid < M) {
+    L.S[tid] = a.qsum[tid];
+    L.xs[tid] = a.xs[tid];
   }
-
-  proj_prologue<M, MODE>(a, av, slot_part, lb, L);
+  __syncthreads();
 
   uint32_t cnt[M][8];
 #pragma unroll
@@ -359,30 +281,6 @@ __global__ __launch_bounds__(ProjShape<M>::NT) void proj_kernel(ProjArgs a) {
       a.out[(size_t)m * a.ld_out + n] = f2h(h2f(xres) + out);
     }
   }
-}
-
-// Stand-alone RMSNorm + quantizer (one workgroup per activation row): writes xn, q and the scale.
-__global__ __launch_bounds__(ProjShape<1>::NT) void prologue_kernel(ProjArgs a, uint16_t* xn_out, int8_t* q_out, uint16_t* s_out) {
-  constexpr int kNT = ProjShape<1>::NT, kMaxLB = ProjShape<1>::MaxLB;
-  __shared__ ProjLds<1> L;
-  const int m = blockIdx.x, tid = threadIdx.x;
-  ProjArgs b = a;
-  b.act = a.act + (size_t)m * a.ld_act;
-  b.lB = nullptr;
-  u32x4 av[1];
-  av[0] = tid < a.K / 8 ? *(const u32x4*)(b.act + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
-  const double slot_part[1] = {0.0};
-  uint2 lb[kMaxLB];
-#pragma unroll
-  for (int i = 0; i < kMaxLB; ++i) lb[i] = make_uint2(0u, 0u);
-  proj_prologue<1, DFSSM_MODE_IN>(b, av, slot_part, lb, L);
-  const float xs = L.xs[0];
-  for (int k = tid; k < a.K; k += kNT) {
-    const uint16_t v = L.xn[0][k];
-    xn_out[(size_t)m * a.K + k] = v;
-    q_out[(size_t)m * a.K + k] = (int8_t)quant_i8(h2f(v), xs);
-  }
-  if (tid == 0) s_out[m] = f2h(xs);
 }
 
 // Stand-alone scaffold GEMM for given int8 activations (tests / microbench): acc and y only.
@@ -474,9 +372,9 @@ template <int M>
 static hipError_t launch_proj_m(const ProjArgs& a, int mode, hipStream_t s) {
   const int groups = (a.N + 63) / 64;
   if (mode == DFSSM_MODE_IN)
-    hipLaunchKernelGGL((proj_kernel<M, DFSSM_MODE_IN>), dim3(groups), dim3(ProjShape<M>::NT), 0, s, a);
+    hipLaunchKernelGGL((proj_kernel<M, DFSSM_MODE_IN>), dim3(groups), dim3(kNT), 0, s, a);
   else
-    hipLaunchKernelGGL((proj_kernel<M, DFSSM_MODE_OUT>), dim3(groups), dim3(ProjShape<M>::NT), 0, s, a);
+    hipLaunchKernelGGL((proj_kernel<M, DFSSM_MODE_OUT>), dim3(groups), dim3(kNT), 0, s, a);
   return hipGetLastError();
 }
 
@@ -490,6 +388,14 @@ hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s) {
   }
 }
 
+hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
+  if (mode == DFSSM_MODE_IN)
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(kPT), 0, s, a);
+  else
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(DFSSM_LORA_R, M), dim3(kPT), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s) {
   const int groups = (a.N + 63) / 64;
   switch (M) {
@@ -499,11 +405,6 @@ hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s) {
     case 4: hipLaunchKernelGGL(scaffold_kernel<4>, dim3(groups), dim3(kNTs), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_prologue(const ProjArgs& a, int M, uint16_t* xn, int8_t* q, uint16_t* sc, hipStream_t s) {
-  hipLaunchKernelGGL(prologue_kernel, dim3(M), dim3(ProjShape<1>::NT), 0, s, a, xn, q, sc);
   return hipGetLastError();
 }
 

@@ -127,14 +127,16 @@ int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace);
 
 /* One residual block on x (batch, D) fp16, in place: RMSNorm, in_proj scaffold + LoRA, conv,
  * SSM, gate, gated RMSNorm, out_proj scaffold + LoRA, residual. Replaces one iteration of
- * _run_layers, df_ssm_inference.py:161-207. 3 kernel launches. */
+ * _run_layers, df_ssm_inference.py:161-207. 5 kernel launches. */
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream);
 
-/* One of the three kernels of dfssm_layer_step: phase 0 = RMSNorm + in_proj + LoRA + conv/SiLU
- * (df_ssm_inference.py:165-182), 1 = SSM step + gate (:185-195), 2 = gated RMSNorm + out_proj +
- * LoRA + residual (:196-207). Running phases 0, 1, 2 in order equals dfssm_layer_step; exposed
- * for per-kernel timing and for callers that interleave their own work. */
+/* One of the kernels of dfssm_layer_step, in order: 0 = RMSNorm + int8 quantization + LoRA
+ * intermediate of x (df_ssm_inference.py:165-168,173), 1 = in_proj scaffold + LoRA + conv/SiLU
+ * (:169-182), 2 = SSM step + gate (:185-195), 3 = gated RMSNorm + quantization + LoRA
+ * intermediate (:196-199,204), 4 = out_proj scaffold + LoRA + residual (:200-207). Running the
+ * phases in order equals dfssm_layer_step; exposed for per-kernel timing. */
+#define DFSSM_LAYER_PHASES 5
 int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
                       const dfssm_state* state, void* workspace, void* stream);
 
