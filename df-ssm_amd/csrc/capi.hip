@@ -75,7 +75,7 @@ const char* dfssm_error_string(int code) {
     case DFSSM_OK: return "ok";
     case DFSSM_E_NULL: return "required pointer is NULL";
     case DFSSM_E_DIMS: return "model dimensions not supported by the kernels";
-    case DFSSM_E_BATCH: return "batch size not supported (1..4)";
+    case DFSSM_E_BATCH: return "batch size not supported (1..64)";
     case DFSSM_E_ALIGN: return "pointer or leading dimension misaligned (16-byte rows required)";
     case DFSSM_E_RANGE: return "index out of range";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
@@ -90,7 +90,7 @@ int dfssm_check_dims(const dfssm_dims* d) {
   if (d->d_inner % d->nheads) return DFSSM_E_DIMS;
   const int P = d->d_inner / d->nheads;
   if (P % 16 || d->nheads % 8) return DFSSM_E_DIMS;
-  if (d->batch < 1 || d->batch > 4) return DFSSM_E_BATCH;
+  if (d->batch < 1 || d->batch > 64) return DFSSM_E_BATCH;
   return DFSSM_OK;
 }
 
@@ -122,11 +122,20 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
                         uint16_t* y_out, void* stream) {
   if (!tiled_bits || !q || (!acc_out && !y_out)) return DFSSM_E_NULL;
   if (y_out && (!xscale || !wscale)) return DFSSM_E_NULL;
-  if (M < 1 || M > 4) return DFSSM_E_BATCH;
+  if (M < 1 || M > 64) return DFSSM_E_BATCH;
   if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
-  if (!aligned16(tiled_bits)) return DFSSM_E_ALIGN;
-  ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, N, K};
-  return hip_status(launch_scaffold(a, M, as_stream(stream)));
+  if (!aligned16(tiled_bits) || !aligned16(q)) return DFSSM_E_ALIGN;
+  if (M <= 4) {
+    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, N, K};
+    return hip_status(launch_scaffold(a, M, as_stream(stream)));
+  }
+  GemmArgs a{};
+  a.bits = tiled_bits; a.wscale = y_out ? wscale : nullptr;
+  a.q = q; a.ld_q = K; a.M = M;
+  a.xs16 = xscale;
+  a.out = y_out; a.ld_out = N; a.acc_out = acc_out;
+  a.N = N; a.K = K;
+  return hip_status(launch_gemm(a, DFSSM_MODE_SCAFFOLD, as_stream(stream)));
 }
 
 int dfssm_rmsnorm_quantize(const uint16_t* x, const float* w, int M, int K, uint16_t* xn_out,
@@ -265,13 +274,33 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
     as.H = r.H; as.P = r.P; as.N = r.N;
     return hip_status(launch_ssm(as, r.B, s));
   }
+  const bool in = phase == 1;
+  if (r.B > 4) {  // int8 matrix-core path
+    GemmArgs a{};
+    a.q = (const int8_t*)(ws + w.q); a.ld_q = kq; a.M = r.B;
+    a.xs = (const float*)(ws + w.xs);
+    a.h = (const float*)(ws + w.h);
+    if (in) {
+      a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
+      a.out = proj; a.ld_out = r.IPO;
+      a.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
+      a.conv_w = Lw.conv_w; a.conv_b = Lw.conv_b;
+      a.conv_lo = r.DI; a.conv_c = r.C;
+      a.N = r.IPO; a.K = r.D;
+    } else {
+      a.bits = Lw.out_bits; a.wscale = Lw.out_scale; a.lA = Lw.out_lA; a.lAs = Lw.out_lA_s;
+      a.out = x; a.ld_out = r.D;
+      a.N = r.D; a.K = r.DI;
+    }
+    return hip_status(launch_gemm(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s));
+  }
   ProjArgs a{};
   a.planes = (const uint32_t*)(ws + w.planes);
   a.ld_q = kq;
   a.qsum = (const int*)(ws + w.qsum);
   a.xs = (const float*)(ws + w.xs);
   a.h = (const float*)(ws + w.h);
-  if (phase == 1) {  // in_proj scaffold + LoRA + conv/SiLU -> proj
+  if (in) {  // in_proj scaffold + LoRA + conv/SiLU -> proj
     a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
     a.out = proj; a.ld_out = r.IPO;
     a.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
@@ -304,13 +333,20 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   const Derived r = derive(&model->dims);
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
-  HeadArgs a{};
-  a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
-  a.V = r.V; a.D = r.D; a.logits = logits;
-  a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
-  a.ticket = (unsigned*)(ws + w.ticket);
-  a.next = next; a.x_next = x_next;
-  return hip_status(launch_head(a, r.B, as_stream(stream)));
+  for (int m0 = 0; m0 < r.B; m0 += 4) {  // the head kernel takes up to 4 rows per launch
+    const int mb = r.B - m0 < 4 ? r.B - m0 : 4;
+    HeadArgs a{};
+    a.x = x + (size_t)m0 * r.D; a.norm_f = model->norm_f; a.emb = model->emb;
+    a.emb_scale = model->emb_scale;
+    a.V = r.V; a.D = r.D; a.logits = logits ? logits + (size_t)m0 * r.V : nullptr;
+    a.part_val = (float*)(ws + w.part_val) + (size_t)m0 * r.head_groups;
+    a.part_idx = (int*)(ws + w.part_idx) + (size_t)m0 * r.head_groups;
+    a.ticket = (unsigned*)(ws + w.ticket);
+    a.next = next + m0; a.x_next = x_next ? x_next + (size_t)m0 * r.D : nullptr;
+    rc = hip_status(launch_head(a, mb, as_stream(stream)));
+    if (rc) return rc;
+  }
+  return DFSSM_OK;
 }
 
 int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,

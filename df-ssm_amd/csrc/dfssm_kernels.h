@@ -5,6 +5,7 @@
 
 #define DFSSM_MODE_IN 0
 #define DFSSM_MODE_OUT 1
+#define DFSSM_MODE_SCAFFOLD 2
 
 namespace dfssm {
 
@@ -45,6 +46,27 @@ struct ProjArgs {
   uint16_t* conv_state;      // (M, conv_c, 3) fp16
   const uint16_t* conv_w;    // (conv_c, 4) fp16
   const uint16_t* conv_b;    // (conv_c) fp16
+  int conv_lo, conv_c;
+  int N, K;
+};
+
+// Batched projection on the int8 matrix cores (M = 1..64 rows; used for M >= 5).
+struct GemmArgs {
+  const uint32_t* bits;      // tiled sign bits
+  const uint16_t* wscale;    // (N) fp16
+  const int8_t* lA;          // (N, 16) (IN / OUT)
+  const uint16_t* lAs;       // (N) (IN / OUT)
+  const int8_t* q;           // (M, ld_q) int8 activations
+  int ld_q, M;
+  const float* xs;           // (M) activation scales (fp16 values) or null
+  const uint16_t* xs16;      // (M) fp16 activation scales (SCAFFOLD), used when xs is null
+  const float* h;            // (M, 16) LoRA intermediate (IN / OUT)
+  uint16_t* out;             // IN: proj; OUT: residual x (in place); SCAFFOLD: y (may be null)
+  int ld_out;
+  int32_t* acc_out;          // optional (M, N) accumulators
+  uint16_t* conv_state;      // IN: (M, conv_c, 3)
+  const uint16_t* conv_w;
+  const uint16_t* conv_b;
   int conv_lo, conv_c;
   int N, K;
 };
@@ -110,6 +132,7 @@ struct EmbedArgs {
 
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s);
+hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s);
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s);
 hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s);
 hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);

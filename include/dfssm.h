@@ -14,7 +14,7 @@
  *
  * Model-specific constraints (checked by dfssm_check_dims): d_state = 128, ngroups = 1,
  * LoRA rank 16, d_conv = 4, P = d_inner / nheads a multiple of 16, d_model and d_inner multiples
- * of 512 and at most 5120, nheads a multiple of 8, batch 1..4, int8 embedding (emb_code 1).
+ * of 512 and at most 5120, nheads a multiple of 8, batch 1..64, int8 embedding (emb_code 1).
  */
 #ifndef DFSSM_H
 #define DFSSM_H
@@ -89,7 +89,8 @@ int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model,
 /* ---- single operators ------------------------------------------------------------------ */
 /* Scaffold GEMM: acc[m][n] = sum_k q[m][k] * (bit ? +1 : -1) (exact int32) and, if y_out is
  * non-NULL, y = fp16(fp16(fp16(acc) * xscale[m]) * wscale[n]). Replaces torch._int_mm plus the
- * dequant of _scaffold_matmul, df_ssm_inference.py:154-158. M = 1..4. */
+ * dequant of _scaffold_matmul, df_ssm_inference.py:154-158. M = 1..64 (1..4 on the packed-bit
+ * VALU GEMV, 5..64 on the int8 matrix cores). */
 int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
                         const uint16_t* wscale, int M, int N, int K, int32_t* acc_out,
                         uint16_t* y_out, void* stream);

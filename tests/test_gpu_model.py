@@ -29,7 +29,7 @@ def tiny_weights():
     return make_weights(config_tiny(n_layer=3), seed=0)
 
 
-@pytest.mark.parametrize("B", [1, 2, 3, 4])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 16, 32, 64])
 def test_tiny_forward_stepwise(tiny_weights, B):
     w = tiny_weights
     print(f"tiny forward B={B}", flush=True)
@@ -54,7 +54,7 @@ def test_tiny_forward_stepwise(tiny_weights, B):
                                atol=2e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("B", [1, 4, 32])
 def test_tiny_generate_tokens(tiny_weights, B):
     """Graph-replayed generation (8 fused steps per replay) yields the oracle's greedy tokens."""
     w = tiny_weights
@@ -84,7 +84,7 @@ def w13():
     return make_weights(config_1p3b(), seed=0)
 
 
-@pytest.mark.parametrize("B,T,n", [(1, 32, 128), (4, 8, 8)])
+@pytest.mark.parametrize("B,T,n", [(1, 32, 128), (4, 8, 8), (8, 4, 4)])
 def test_1p3b_greedy(w13, B, T, n):
     """Config 3 at batch 1 (32-token seeded prompt, 128 generated) and a short batch-4 run:
     identical greedy tokens, state within 1e-3 after the run, final logits within 2e-2."""

@@ -29,7 +29,7 @@ def _tiled(bits_np, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096), (10576, 2560), (2048, 5120), (2320, 512)])
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16, 32, 64])
 def test_scaffold_acc_bit_exact(N, K, M):
     """Config 1: in_proj 2048->8512, out_proj 4096->2048 (+2.7B and tiny shapes), int8 ~N(0,40)."""
     print(f"scaffold N={N} K={K} M={M}", flush=True)
@@ -46,7 +46,7 @@ def test_scaffold_acc_bit_exact(N, K, M):
     np.testing.assert_array_equal(_np16(y).view(np.uint16), yref.view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 32])
 def test_scaffold_extremes(M):
     """All +127 / all -128 activations against all-set / all-clear / random bits: +-K*127, etc."""
     N, K = 192, 2048
