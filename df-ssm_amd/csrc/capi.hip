@@ -30,7 +30,7 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, part_val, part_idx, ticket, err, total;
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, ticket, err, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -46,6 +46,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.qsum = off;     off = align_up(off + (size_t)r.B * 4);
   w.xs = off;       off = align_up(off + (size_t)r.B * 4);
   w.h = off;        off = align_up(off + (size_t)r.B * 16 * 4);
+  w.xf = off;       off = align_up(off + (size_t)r.B * r.D * 2);
   w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.ticket = off;   off = align_up(off + 4);
@@ -333,19 +334,24 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   const Derived r = derive(&model->dims);
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
-  for (int m0 = 0; m0 < r.B; m0 += 4) {  // the head kernel takes up to 4 rows per launch
-    const int mb = r.B - m0 < 4 ? r.B - m0 : 4;
+  if (r.B > 4) {  // matrix-core head (fp32 accumulation)
     HeadArgs a{};
-    a.x = x + (size_t)m0 * r.D; a.norm_f = model->norm_f; a.emb = model->emb;
-    a.emb_scale = model->emb_scale;
-    a.V = r.V; a.D = r.D; a.logits = logits ? logits + (size_t)m0 * r.V : nullptr;
-    a.part_val = (float*)(ws + w.part_val) + (size_t)m0 * r.head_groups;
-    a.part_idx = (int*)(ws + w.part_idx) + (size_t)m0 * r.head_groups;
+    a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
+    a.V = r.V; a.D = r.D; a.logits = logits;
+    a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
     a.ticket = (unsigned*)(ws + w.ticket);
-    a.next = next + m0; a.x_next = x_next ? x_next + (size_t)m0 * r.D : nullptr;
-    rc = hip_status(launch_head(a, mb, as_stream(stream)));
-    if (rc) return rc;
+    a.next = next; a.x_next = x_next;
+    a.xf = (const uint16_t*)(ws + w.xf);
+    return hip_status(launch_head_batched(a, r.B, as_stream(stream)));
   }
+  HeadArgs a{};
+  a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
+  a.V = r.V; a.D = r.D; a.logits = logits;
+  a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
+  a.ticket = (unsigned*)(ws + w.ticket);
+  a.next = next; a.x_next = x_next;
+  rc = hip_status(launch_head(a, r.B, as_stream(stream)));
+  if (rc) return rc;
   return DFSSM_OK;
 }
 

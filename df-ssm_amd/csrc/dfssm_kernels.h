@@ -119,6 +119,7 @@ struct HeadArgs {
   unsigned* ticket;          // zero before the first launch; left zero by every launch
   int64_t* next;             // (M) greedy tokens
   uint16_t* x_next;          // optional (M, D): embedding of the greedy tokens
+  const uint16_t* xf;        // batched head: (M, D) scratch for the final-normed rows
 };
 
 struct EmbedArgs {
@@ -138,6 +139,7 @@ hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, h
 hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);
 hipError_t launch_conv(const ConvArgs& a, int M, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
+hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
 hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStream_t s);
 

@@ -6,11 +6,15 @@
 // four 0/1 bytes is one multiply and one mask: (nib * 0x00204081) & 0x01010101 -- the four
 // shifted copies of the nibble occupy disjoint bit ranges, so the product has no carries.
 //
-// One workgroup (256 threads, 4 waves) owns a group of 64 output rows; wave w owns rows 16w..16w+15
-// of it for all MI*16 activation rows (MI accumulator tiles per wave). K is walked in 512-column
-// chunks: the chunk's q tile (MI*16 x 512 bytes, LDS rows padded to avoid bank conflicts) and
-// the group's 4 KiB of sign bits are staged in LDS while the next chunk is already loading into
-// registers. Epilogues are those of the GEMV path (dequant, LoRA, conv + SiLU or residual).
+// One workgroup (1024 threads = 16 waves) owns a group of 64 output rows and up to 32 activation
+// rows (larger batches are split by the launcher). Wave w = (row tile rt = w % 4, k slot kq = w / 4).
+// The 16-byte bit chunks c of the row group (128 columns each) are dealt out as
+// c = kq + 4 j + 16 sb to lane group j = lane / 16 of wave slot kq, block sb: every lane keeps its
+// chunks in registers, loaded once, fully coalesced. Within an MFMA step lane group j supplies
+// columns 128 c + 16 s .. +15 of both operands; a consistent permutation of the k index between
+// A and B leaves the dot product unchanged. The q tile of all rows sits in LDS (one batch of
+// loads); the four k slots' int32 partials are added through LDS (exact), and the epilogue is
+// shared by all 16 waves.
 #include "common.h"
 #include "dfssm_kernels.h"
 
@@ -18,33 +22,38 @@ namespace dfssm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kGT = 256;
-constexpr int kKC = 512;        // K chunk
-constexpr int kQS = kKC + 16;   // LDS row stride of the q tile (bytes)
+constexpr int kGT = 1024;
+constexpr int kMaxSB = 3;  // bit-chunk blocks per lane: ceil(K / 128 / 16) for K <= 5120
 
 template <int MI, int MODE>
 __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   constexpr int MP = MI * 16;
-  __shared__ __attribute__((aligned(16))) int8_t qs[MP][kQS];
-  __shared__ __attribute__((aligned(16))) uint32_t bsm[kKC / 128][64][4];
+  extern __shared__ __attribute__((aligned(16))) int8_t qs[];  // MP rows x QS bytes; then partials
   __shared__ int Ssum[MP];
   __shared__ float hl[MP][DFSSM_LORA_R];
   __shared__ float xsl[MP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rt = wave & 3, kq = wave >> 2, j = lane >> 4;
   const int g = blockIdx.x;
-  const int K = a.K, CH = K / 128, nchunks = K / kKC, M = a.M;
+  const int K = a.K, CH = K / 128, M = a.M;
+  const int QS = K + 16;  // padded LDS row stride
 
-  for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
-    const int m = i >> 4;
-    hl[m][i & 15] = (a.h && m < M) ? a.h[i] : 0.0f;
+  // ---- loads, all issued before any use: bits (registers), q tile (LDS), epilogue rows ----
+  const int r = rt * 16 + (lane & 15);
+  u32x4 wb[kMaxSB];
+#pragma unroll
+  for (int sb = 0; sb < kMaxSB; ++sb) {
+    const int c = kq + 4 * j + 16 * sb;
+    wb[sb] = c < CH ? ld_nt((const u32x4*)a.bits + ((size_t)g * CH + c) * 64 + r) : u32x4{0u, 0u, 0u, 0u};
   }
-  if (tid < MP) {
-    Ssum[tid] = 0;
-    xsl[tid] = tid < M ? (a.xs ? a.xs[tid] : (a.xs16 ? h2f(a.xs16[tid]) : 0.0f)) : 0.0f;
+  const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
+  for (int v = tid; v < nvq; v += kGT) {
+    const int row = v / (K / 16), c16 = v % (K / 16);
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (row < M) x = *(const u32x4*)(a.q + (size_t)row * a.ld_q + c16 * 16);
+    *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
   }
-
-  // epilogue row data: lane's output row n (same for all its accumulator elements)
-  const int n = g * 64 + wave * 16 + (lane & 15);
+  const int n = g * 64 + r;
   const bool nrow = n < a.N;
   u32x4 la = {0u, 0u, 0u, 0u};
   float e_ws = 0.0f, e_as = 0.0f;
@@ -64,122 +73,147 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       cb = a.conv_b[ch];
     }
   }
-
-  // chunk loads: q tile vectors (row, 16-byte column) and this thread's 16 bytes of bits
-  u32x4 qreg[2 * MI];
-  u32x4 breg;
-  const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + tid;
-  auto load_chunk = [&](int t) {
+  for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
+    const int m = i >> 4;
+    hl[m][i & 15] = (a.h && m < M) ? a.h[(size_t)m * DFSSM_LORA_R + (i & 15)] : 0.0f;
+  }
+  if (tid < MP) {
+    xsl[tid] = tid < M ? (a.xs ? a.xs[tid] : (a.xs16 ? h2f(a.xs16[tid]) : 0.0f)) : 0.0f;
+  }
+  __syncthreads();
+  // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
+  for (int row = wave; row < MP; row += kGT / 64) {
+    int s = 0;
+    for (int c16 = lane; c16 < K / 16; c16 += 64) {
+      const u32x4 x = *(const u32x4*)(qs + (size_t)row * QS + c16 * 16);
 #pragma unroll
-    for (int p = 0; p < 2 * MI; ++p) {
-      const int v = tid + kGT * p, row = v >> 5, c16 = v & 31;
-      qreg[p] = row < M ? *(const u32x4*)(a.q + (size_t)row * a.ld_q + t * kKC + c16 * 16) : u32x4{0u, 0u, 0u, 0u};
+      for (int e = 0; e < 16; ++e) s += (int)(int8_t)(x[e >> 2] >> (8 * (e & 3)));
     }
-    breg = ld_nt(bits + (size_t)t * 4 * 64);
-  };
+    s = wave_sum_i32(s);
+    if (lane == 0) Ssum[row] = s;
+  }
 
+  // ---- MFMA over this wave's chunks ----
   v4i acc[MI];
 #pragma unroll
   for (int i = 0; i < MI; ++i) acc[i] = v4i{0, 0, 0, 0};
-  load_chunk(0);
-  for (int t = 0; t < nchunks; ++t) {
-    __syncthreads();  // previous chunk's readers are done
 #pragma unroll
-    for (int p = 0; p < 2 * MI; ++p) {
-      const int v = tid + kGT * p, row = v >> 5, c16 = v & 31;
-      *(u32x4*)&qs[row][c16 * 16] = qreg[p];
-      if (row < M) {
-        int s = 0;
+  for (int sb = 0; sb < kMaxSB; ++sb) {
+    if (kq + 16 * sb < CH) {  // wave-uniform: some lane group has a chunk in this block
+      const int c = kq + 4 * j + 16 * sb;
+      const bool valid = c < CH;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s += (int)(int8_t)(qreg[p][e >> 2] >> (8 * (e & 3)));
-        atomicAdd(&Ssum[row], s);
-      }
-    }
-    ((u32x4*)&bsm[0][0][0])[tid] = breg;
-    __syncthreads();
-    if (t + 1 < nchunks) load_chunk(t + 1);
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t w = wb[sb][s >> 1];
+        const uint32_t b16 = valid ? ((s & 1) ? (w >> 16) : (w & 0xffffu)) : 0u;
+        v4i B;
 #pragma unroll
-    for (int s = 0; s < kKC / 64; ++s) {
-      const int r = wave * 16 + (lane & 15);
-      const int kl = 64 * s + 16 * (lane >> 4);
-      const uint32_t w = bsm[kl >> 7][r][(kl & 127) >> 5];
-      const uint32_t b16 = (kl & 16) ? (w >> 16) : (w & 0xffffu);
-      v4i B;
+        for (int nib = 0; nib < 4; ++nib) B[nib] = (int)((((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u);
+        const int k = valid ? 128 * c + 16 * s : 0;
 #pragma unroll
-      for (int nib = 0; nib < 4; ++nib) B[nib] = (int)((((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u);
-#pragma unroll
-      for (int ib = 0; ib < MI; ++ib) {
-        const v4i A = *(const v4i*)&qs[ib * 16 + (lane & 15)][kl];
-        acc[ib] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[ib], 0, 0, 0);
+        for (int ib = 0; ib < MI; ++ib) {
+          const v4i A = *(const v4i*)(qs + (size_t)(ib * 16 + (lane & 15)) * QS + k);
+          acc[ib] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[ib], 0, 0, 0);
+        }
       }
     }
   }
+  __syncthreads();  // q tile no longer needed: reuse it for the partials
+  int* part = (int*)qs;  // [kq][rt][ib][e][lane]
+#pragma unroll
+  for (int ib = 0; ib < MI; ++ib)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[(((kq * 4 + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
   __syncthreads();
 
-  // epilogue: accumulator element (ib, v) is T[m = 16 ib + 4 (lane / 16) + v][n]
+  // ---- epilogue: wave (rt, kq) finishes accumulator element e = kq of each tile ----
   if (!nrow) return;
+  double aqd[DFSSM_LORA_R];
+#pragma unroll
+  for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
+    aqd[rr] = (double)r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * e_as);
 #pragma unroll
   for (int ib = 0; ib < MI; ++ib) {
+    const int e = kq;
+    const int m = ib * 16 + 4 * j + e;
+    if (m >= M) continue;
+    int T = 0;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int m = ib * 16 + 4 * (lane >> 4) + v;
-      if (m >= M) continue;
-      const int accv = 2 * acc[ib][v] - Ssum[m];
-      if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
-      const float y = r16(r16(r16((float)accv) * xsl[m]) * e_ws);
-      if (MODE == DFSSM_MODE_SCAFFOLD) {
-        if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
-        continue;
-      }
-      double lo = 0.0;
+    for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
+    const int accv = 2 * T - Ssum[m];
+    if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
+    const float y = r16(r16(r16((float)accv) * xsl[m]) * e_ws);
+    if (MODE == DFSSM_MODE_SCAFFOLD) {
+      if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
+      continue;
+    }
+    double lo = 0.0;
 #pragma unroll
-      for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
-        const float aq = r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * e_as);
-        lo += (double)hl[m][rr] * (double)aq;
+    for (int rr = 0; rr < DFSSM_LORA_R; ++rr) lo += (double)hl[m][rr] * aqd[rr];
+    float out = r16((float)lo + y);
+    uint16_t* op = a.out + (size_t)m * a.ld_out + n;
+    if (MODE == DFSSM_MODE_IN) {
+      if (conv_row) {
+        uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
+        const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
+        const uint16_t xo = f2h(out);
+        cs[0] = s1;
+        cs[1] = s2;
+        cs[2] = xo;
+        const float xv = h2f(xo);
+        float o = h2f(s0) * h2f((uint16_t)cw01);
+        o = o + h2f(s1) * h2f((uint16_t)(cw01 >> 16));
+        o = o + h2f(s2) * h2f((uint16_t)cw23);
+        o = o + xv * h2f((uint16_t)(cw23 >> 16));
+        o = o + h2f(cb);
+        const float sig = 1.0f / (1.0f + dev_expf(-o));
+        out = o * sig;
       }
-      float out = r16((float)lo + y);
-      uint16_t* op = a.out + (size_t)m * a.ld_out + n;
-      if (MODE == DFSSM_MODE_IN) {
-        if (conv_row) {
-          uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
-          const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
-          const uint16_t xo = f2h(out);
-          cs[0] = s1;
-          cs[1] = s2;
-          cs[2] = xo;
-          const float xv = h2f(xo);
-          float o = h2f(s0) * h2f((uint16_t)cw01);
-          o = o + h2f(s1) * h2f((uint16_t)(cw01 >> 16));
-          o = o + h2f(s2) * h2f((uint16_t)cw23);
-          o = o + xv * h2f((uint16_t)(cw23 >> 16));
-          o = o + h2f(cb);
-          const float sig = 1.0f / (1.0f + dev_expf(-o));
-          out = o * sig;
-        }
-        *op = f2h(out);
-      } else {
-        *op = f2h(h2f(*op) + out);
-      }
+      *op = f2h(out);
+    } else {
+      *op = f2h(h2f(*op) + out);
     }
   }
 }
 
-template <int MODE>
-static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
-  const int groups = (a.N + 63) / 64;
-  const int MI = (a.M + 15) / 16;
-  switch (MI) {
-    case 1: hipLaunchKernelGGL((gemm_kernel<1, MODE>), dim3(groups), dim3(kGT), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<2, MODE>), dim3(groups), dim3(kGT), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((gemm_kernel<3, MODE>), dim3(groups), dim3(kGT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((gemm_kernel<4, MODE>), dim3(groups), dim3(kGT), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+static size_t gemm_lds_bytes(int MI, int K) {
+  const size_t tile = (size_t)MI * 16 * (K + 16);
+  const size_t part = (size_t)16 * MI * 4 * 64 * 4;
+  return tile > part ? tile : part;
+}
+
+template <int MI, int MODE>
+static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
+  const size_t shm = gemm_lds_bytes(MI, a.K);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, MODE>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm_kernel<MI, MODE>), dim3((a.N + 63) / 64), dim3(kGT), shm, s, a);
   return hipGetLastError();
 }
 
+template <int MODE>
+static hipError_t launch_gemm_mode(const GemmArgs& a0, hipStream_t s) {
+  // rows per launch: the q tile (rows x (K + 16) bytes) must fit the 160 KiB of LDS
+  const int rows = a0.K <= 4096 ? 32 : 16;
+  for (int m0 = 0; m0 < a0.M; m0 += rows) {
+    GemmArgs a = a0;
+    a.M = a0.M - m0 < rows ? a0.M - m0 : rows;
+    a.q = a0.q + (size_t)m0 * a0.ld_q;
+    if (a0.xs) a.xs = a0.xs + m0;
+    if (a0.xs16) a.xs16 = a0.xs16 + m0;
+    if (a0.h) a.h = a0.h + (size_t)m0 * DFSSM_LORA_R;
+    if (a0.out) a.out = a0.out + (size_t)m0 * a0.ld_out;
+    if (a0.acc_out) a.acc_out = a0.acc_out + (size_t)m0 * a0.N;
+    if (a0.conv_state) a.conv_state = a0.conv_state + (size_t)m0 * a0.conv_c * 3;
+    const hipError_t e = a.M > 16 ? launch_gemm_mi<2, MODE>(a, s) : launch_gemm_mi<1, MODE>(a, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {
-  if (a.M < 1 || a.M > 64 || a.K % kKC) return hipErrorInvalidValue;
+  if (a.M < 1 || a.M > 64 || a.K % 512 || a.K > 5120) return hipErrorInvalidValue;
   switch (mode) {
     case DFSSM_MODE_IN: return launch_gemm_mode<DFSSM_MODE_IN>(a, s);
     case DFSSM_MODE_OUT: return launch_gemm_mode<DFSSM_MODE_OUT>(a, s);

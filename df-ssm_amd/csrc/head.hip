@@ -208,4 +208,204 @@ hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStre
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// Batched head (M = 5..64): logits on the fp16 matrix cores, v_mfma_f32_16x16x32_f16. A = xf
+// (fp16, 16 rows x 32 k), B = 16 vocabulary rows of the int8 table converted exactly to fp16 in
+// registers. Products are exact; the sum is accumulated in fp32 (not exact -- the 1..4-row kernel
+// above is). One workgroup (4 waves) owns 256 vocabulary rows (each wave 4 tiles of 16); xf is
+// staged in LDS 512 columns at a time. Argmax as above: per-workgroup pairs, then the last
+// workgroup to finish reduces them.
+// ---------------------------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+
+constexpr int kHT = 256;
+constexpr int kHV = 256;   // vocabulary rows per workgroup
+constexpr int kHK = 512;   // k chunk
+constexpr int kHS = kHK + 8;  // LDS row stride of the xf tile (halves)
+
+// xf[m] = fp16((x * r) * norm_f) for the batched head (one workgroup per row).
+__global__ __launch_bounds__(256) void final_norm_kernel(const uint16_t* __restrict__ x, const float* __restrict__ norm_f,
+                                                        uint16_t* __restrict__ xf, int D) {
+  __shared__ double red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* xm = x + (size_t)m * D;
+  double ps = 0.0;
+  for (int k = tid; k < D; k += 256) { const double v = (double)h2f(xm[k]); ps += v * v; }
+  const double ss = block_sum_f64<256>(ps, red);
+  const float var = (float)ss * (1.0f / (float)D);
+  const float r = 1.0f / sqrt_rn(var + 1e-5f);
+  for (int k = tid; k < D; k += 256) xf[(size_t)m * D + k] = f2h((h2f(xm[k]) * r) * norm_f[k]);
+}
+
+template <int MI>
+__global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
+  constexpr int MP = MI * 16;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[MP][kHS];
+  __shared__ float wbest[4][MP];
+  __shared__ int widx[4][MP];
+  __shared__ bool is_last;
+  __shared__ int next_tok[MP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int D = a.D, CH = D / 16;
+  const int v0 = blockIdx.x * kHV + wave * 64;
+  const int vpad = (a.V + 63) / 64 * 64;
+
+  f32x4m acc[4][MI];
+#pragma unroll
+  for (int vt = 0; vt < 4; ++vt)
+#pragma unroll
+    for (int ib = 0; ib < MI; ++ib) acc[vt][ib] = f32x4m{0.f, 0.f, 0.f, 0.f};
+
+  for (int t = 0; t < D / kHK; ++t) {
+    __syncthreads();
+    for (int i = tid; i < MP * (kHK / 8); i += kHT) {  // 16-byte vectors of the xf chunk
+      const int row = i / (kHK / 8), c8 = i % (kHK / 8);
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row < M) v = *(const u32x4*)(a.xf + (size_t)row * D + t * kHK + c8 * 8);
+      *(u32x4*)&xs[row][c8 * 8] = v;
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int ks = 0; ks < kHK / 32; ++ks) {
+      const int kl = ks * 32 + 8 * (lane >> 4);
+      const int k = t * kHK + kl;
+      f16x8 A[MI];
+#pragma unroll
+      for (int ib = 0; ib < MI; ++ib) A[ib] = *(const f16x8*)&xs[ib * 16 + (lane & 15)][kl];
+#pragma unroll
+      for (int vt = 0; vt < 4; ++vt) {
+        const int v = v0 + vt * 16 + (lane & 15);
+        // the tiled table holds V rounded up to 64 rows (zero padded); the last tile may pass it
+        const uint2 e8 = v < vpad ? *(const uint2*)(a.emb + (((size_t)(v >> 6) * CH + (k >> 4)) * 64 + (v & 63)) * 16 + (k & 15))
+                                  : make_uint2(0u, 0u);
+        f16x8 B;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = e < 4 ? e8.x : e8.y;
+          B[e] = (_Float16)(float)(int8_t)(w >> (8 * (e & 3)));
+        }
+#pragma unroll
+        for (int ib = 0; ib < MI; ++ib) acc[vt][ib] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[ib], B, acc[vt][ib], 0, 0, 0);
+      }
+    }
+  }
+
+  // logits and per-row best of this wave: element (vt, ib, j) is row m = 16 ib + 4 (lane/16) + j,
+  // vocabulary v = v0 + 16 vt + lane % 16
+  float best[MI][4];
+  int bidx[MI][4];
+#pragma unroll
+  for (int ib = 0; ib < MI; ++ib)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { best[ib][j] = -INFINITY; bidx[ib][j] = 0x7fffffff; }
+#pragma unroll
+  for (int vt = 0; vt < 4; ++vt) {
+    const int v = v0 + vt * 16 + (lane & 15);
+    if (v >= a.V) continue;
+    const float sc = h2f(a.emb_scale[v]);
+#pragma unroll
+    for (int ib = 0; ib < MI; ++ib)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = ib * 16 + 4 * (lane >> 4) + j;
+        if (m >= M) continue;
+        const uint16_t lh = f2h(acc[vt][ib][j] * sc);
+        if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
+        const float lv = h2f(lh);
+        if (lv > best[ib][j]) { best[ib][j] = lv; bidx[ib][j] = v; }  // v increases with vt
+      }
+  }
+  // reduce over the 16 lanes that share (lane / 16), then over the 4 waves
+#pragma unroll
+  for (int ib = 0; ib < MI; ++ib)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float b = best[ib][j];
+      int bi = bidx[ib][j];
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(b, o, 16);
+        const int oi = __shfl_xor(bi, o, 16);
+        if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+      }
+      if ((lane & 15) == 0) {
+        const int m = ib * 16 + 4 * (lane >> 4) + j;
+        wbest[wave][m] = b;
+        widx[wave][m] = bi;
+      }
+    }
+  __syncthreads();
+  if (tid < M) {
+    float b = wbest[0][tid];
+    int bi = widx[0][tid];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float ob = wbest[w][tid];
+      const int oi = widx[w][tid];
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    a.part_val[(size_t)tid * gridDim.x + blockIdx.x] = b;
+    a.part_idx[(size_t)tid * gridDim.x + blockIdx.x] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const unsigned tk = atomicAdd(a.ticket, 1u);
+    is_last = (tk == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  for (int m = wave; m < M; m += 4) {
+    float b = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = lane; j < (int)gridDim.x; j += 64) {
+      const float vv = __hip_atomic_load(a.part_val + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(b, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    if (lane == 0) {
+      if (bi < 0 || bi >= a.V) bi = 0;
+      a.next[m] = (int64_t)bi;
+      next_tok[m] = bi;
+    }
+  }
+  if (tid == 0) *a.ticket = 0u;
+  __syncthreads();
+  if (a.x_next) {
+    for (int m = 0; m < M; ++m) {
+      const int tk = next_tok[m];
+      const int tg = tk >> 6, tl = tk & 63;
+      const float sc = h2f(a.emb_scale[tk]);
+      for (int k = tid; k < D; k += kHT) {
+        const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
+        a.x_next[(size_t)m * D + k] = f2h((float)row[k & 15] * sc);
+      }
+    }
+  }
+}
+
+hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s) {
+  if (M < 1 || M > 64 || a.D % kHK || !a.xf) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(256), 0, s, a.x, a.norm_f, (uint16_t*)a.xf, a.D);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int groups = (a.V + kHV - 1) / kHV;
+  switch ((M + 15) / 16) {
+    case 1: hipLaunchKernelGGL(head_mfma_kernel<1>, dim3(groups), dim3(kHT), 0, s, a, M); break;
+    case 2: hipLaunchKernelGGL(head_mfma_kernel<2>, dim3(groups), dim3(kHT), 0, s, a, M); break;
+    case 3: hipLaunchKernelGGL(head_mfma_kernel<3>, dim3(groups), dim3(kHT), 0, s, a, M); break;
+    case 4: hipLaunchKernelGGL(head_mfma_kernel<4>, dim3(groups), dim3(kHT), 0, s, a, M); break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace dfssm
