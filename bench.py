@@ -10,7 +10,7 @@ greedy token fed back on the device (HIP graph of 8 steps per replay). value = b
 seconds over the timed steps, inputs resident in HBM.
 
 Also reported: per-kernel timing of the five layer kernels and the head (HIP events around graphs
-of back-to-back launches, minus the per-launch cost of an empty-kernel graph), the roofline of the
+of 48 back-to-back launches of one kernel, divided by the launch count), the roofline of the
 dominant kernel, the whole-step HBM roofline fraction, and the reference CPU decode (the
 reference's cpu_inference.c, HEADDIM 64, compiled in oracle/_ref) on a bounded sample.
 
@@ -104,9 +104,11 @@ def time_decode(m, prompts, steps, warmup):
 
 
 def time_kernels(m, reps=10):
-    """Per-launch time of each layer kernel (48 launches of one phase per graph) and of the head,
-    and of an empty kernel in the same arrangement (the dispatch cost between dependent launches).
-    Returns {name: (us_per_launch, launches_per_step)} with the empty-kernel cost subtracted."""
+    """Per-launch time of each layer kernel and of the head: HIP events on the launch stream around
+    `reps` replays of a graph of 48 back-to-back launches of that kernel alone, divided by the
+    launch count. This is the kernel's duration plus the gap between dependent launches, i.e. what
+    one launch costs inside the decode step; the same arrangement with an empty kernel gives the
+    gap alone. Returns {name: (us_per_launch, launches_per_step)}; "empty" holds the gap."""
     import torch
     from dfssm import _C
     L = m.cfg.n_layer
@@ -134,13 +136,13 @@ def time_kernels(m, reps=10):
             for li in range(L):
                 _C.check(lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state,
                                                m.workspace.data_ptr(), _C.stream()))
-        out[name] = (graph_time(body, L) - empty, L)
+        out[name] = (graph_time(body, L), L)
 
     def head():
         for _ in range(L):
             _C.check(lib.dfssm_lmhead_argmax(m._model, m.x.data_ptr(), m.workspace.data_ptr(), None,
                                              m._next.data_ptr(), None, _C.stream()))
-    out["head+argmax"] = (graph_time(head, L) - empty, 1)
+    out["head+argmax"] = (graph_time(head, L), 1)
     return out
 
 
@@ -158,38 +160,21 @@ def cpu_baseline(weights, prompt, n_tokens):
                       f"AVX-512 VNNI, OpenMP {threads} threads) + NumPy fp32 head; {secs:.1f} s"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
-    ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=48)
-    ap.add_argument("--model-path", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_1p3b_seed0.dfssm"))
-    a = ap.parse_args()
-    if a.gpus != 1:
-        print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
-              "is described in DESIGN.md and not measured", file=sys.stderr)
-        sys.exit(2)
-
-    import numpy as np
+def measure(B, path, steps, warmup):
+    """Decode throughput and per-kernel timing at batch B (one model instance)."""
     import torch
     from dfssm.synth import make_prompts
-
-    B = a.batch
-    m, w = build_model(B, a.model_path)
+    m, w = build_model(B, path)
     cfg = m.cfg
     prompts = make_prompts(B, cfg.vocab_size, 32)
-    ms, steps = time_decode(m, prompts, a.steps, a.warmup)
-    ms_per_step = ms / steps
-    tok_s = B * steps / (ms / 1e3)
+    ms, nsteps = time_decode(m, prompts, steps, warmup)
+    ms_per_step = ms / nsteps
+    tok_s = B * nsteps / (ms / 1e3)
     weights, state, per_phase = algorithmic_bytes(cfg, B)
     step_bytes = weights + state
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode batch {B}: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, "
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / PEAK_GBS:.1f}% of HBM peak)")
-
     kt = time_kernels(m)
     phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
                 "head+argmax": 3}
@@ -202,12 +187,64 @@ def main():
                          "us_per_step": round(us * n, 1), "bytes_per_launch": b,
                          "gbs": round(b / (us * 1e-6) / 1e9, 1)}
         log(f"  {name:18s} {us:7.2f} us/launch x{n:2d}  {b / 1e6:8.3f} MB  {b / (us * 1e-6) / 1e9:7.1f} GB/s")
-    log(f"  empty-kernel dispatch cost {kt['empty'][0]:.2f} us/launch (subtracted)")
-    dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
-    d = kernels[dom]
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": d["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["gbs"] / PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]}
+    log(f"  empty kernel in the same arrangement: {kt['empty'][0]:.2f} us/launch")
+    res = {"batch": B, "tok_s": round(tok_s, 1), "ms_per_step": round(ms_per_step, 4), "steps": nsteps,
+           "step_roofline": {"bytes_per_step": step_bytes, "weights": weights, "state": state,
+                             "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
+                             "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
+           "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2)}
+    del m
+    torch.cuda.empty_cache()
+    return res, w, prompts
+
+
+def copy_calibration(mib):
+    """10 copies of `mib` MiB between two device buffers: a kernel whose HBM traffic is known
+    (mib MiB read + mib MiB written per launch), to scale the profiler's FETCH_SIZE/WRITE_SIZE."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {mib} MiB x10")
+
+
+def roofline_of(res, name=None):
+    ks = res["kernels"]
+    dom = name or max(ks, key=lambda k: ks[k]["us_per_step"])
+    d = ks[dom]
+    return {"bound": "hbm", "kernel": dom, "batch": res["batch"], "achieved": d["gbs"], "peak": PEAK_GBS,
+            "unit": "GB/s", "frac": round(d["gbs"] / PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=1, help="batch of the headline value")
+    ap.add_argument("--batch2", type=int, default=32, help="second batch reported beside it (0: skip)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=48)
+    ap.add_argument("--model-path", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_1p3b_seed0.dfssm"))
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run 10 device-to-device copies of this many MiB (counter calibration) and exit")
+    a = ap.parse_args()
+    if a.copy_mib:
+        copy_calibration(a.copy_mib)
+        return
+    if a.gpus != 1:
+        print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
+              "is described in DESIGN.md and not measured", file=sys.stderr)
+        sys.exit(2)
+
+    main_res, w, prompts = measure(a.batch, a.model_path, a.steps, a.warmup)
+    second = None
+    if a.batch2 and a.batch2 != a.batch:
+        second, _, _ = measure(a.batch2, a.model_path, a.steps, a.warmup)
 
     cpu = None
     if not a.no_cpu:
@@ -217,24 +254,30 @@ def main():
         if cpu:
             log(f"reference CPU: {cpu['value']} tok/s on {cpu['cores']} threads")
 
+    from dfssm.synth import config_1p3b
+    cfg = config_1p3b()
+    B = a.batch
     out = {
         "metric": "decode tok/s, 1.3B-shape b=1 & b=32; scaffold matmul % HBM roofline",
-        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "value": main_res["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": main_res["steps"], "warmup": a.warmup,
+        "ms_per_step": main_res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded random-init weights of the 1.3B shape, .dfssm file; seeded prompts)",
         "config": {"workload": f"config3: 1.3B-shape DF-SSM greedy decode, batch {B}, 32-token prompt "
-                               f"ingested, {steps} timed steps", "batch": B, "d_model": cfg.d_model,
+                               f"ingested, {main_res['steps']} timed steps", "batch": B, "d_model": cfg.d_model,
                    "n_layer": cfg.n_layer, "d_inner": cfg.d_inner, "nheads": cfg.nheads, "headdim": cfg.p,
                    "d_state": cfg.d_state, "vocab": cfg.vocab_size, "embedding": "int8+row scale",
                    "arith": "1-bit x int8 scaffold (int32 acc), fp16 activations, fp32 SSM state"},
-        "step_roofline": {"bytes_per_step": step_bytes, "weights": weights, "state": state,
-                          "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
-                          "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
-        "kernels": kernels,
-        "roofline": roofline,
+        "roofline": roofline_of(main_res),
+        "scaffold_roofline": roofline_of(main_res, "in_proj+conv"),
+        "step_roofline": main_res["step_roofline"],
+        "kernels": main_res["kernels"],
         "cpu_baseline": cpu,
     }
+    if second:
+        out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],
+                         "step_roofline": second["step_roofline"], "roofline": roofline_of(second),
+                         "scaffold_roofline": roofline_of(second, "in_proj+conv"), "kernels": second["kernels"]}
     print(json.dumps(out), flush=True)
 
 

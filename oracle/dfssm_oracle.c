@@ -404,7 +404,10 @@ void or_c_rms_norm(const float* x, const float* w, float* out, int M, int dim) {
 }
 
 /* quantize_input_uint8, cpu_inference.c:65-97: s = 255/(2 max(amax, 1e-8)),
- * q = rne(clamp(x*s + 128, 0, 255)), x_scale = 1/s. */
+ * q = rne(clamp(x*s + 128, 0, 255)), x_scale = 1/s. x*s + 128 is one fused multiply-add: gcc
+ * contracts the _mm512_add_ps(_mm512_mul_ps(..)) of :86-87 at its default -ffp-contract=fast, and
+ * the compiled reference rounds e.g. fma(x, s, 128) = 0.50000006 (product -127.49999994) to 1
+ * where the unfused sum would be 0.5 -> 0. */
 void or_c_quantize_u8(const float* x, int K, uint8_t* q, float* x_scale) {
   float amax = 0.0f;
   for (int i = 0; i < K; ++i) { float a = fabsf(x[i]); if (a > amax) amax = a; }
@@ -412,7 +415,7 @@ void or_c_quantize_u8(const float* x, int K, uint8_t* q, float* x_scale) {
   float s = 255.0f / (2.0f * amax);
   *x_scale = 1.0f / s;
   for (int i = 0; i < K; ++i) {
-    float v = x[i] * s + 128.0f;
+    float v = fmaf(x[i], s, 128.0f);
     if (v < 0.0f) v = 0.0f;
     if (v > 255.0f) v = 255.0f;
     q[i] = (uint8_t)rintf(v);

@@ -38,7 +38,7 @@ def _dims(**kw):
     return _C.Dims(*[base[f] for f, _ in _C.Dims._fields_])
 
 
-@pytest.mark.parametrize("kw,rc", [({}, 0), ({"batch": 4}, 0), ({"batch": 5}, -3), ({"batch": 0}, -3),
+@pytest.mark.parametrize("kw,rc", [({}, 0), ({"batch": 4}, 0), ({"batch": 5}, 0), ({"batch": 64}, 0), ({"batch": 65}, -3), ({"batch": 0}, -3),
                                    ({"d_state": 64}, -2), ({"ngroups": 2}, -2), ({"d_model": 2000}, -2),
                                    ({"emb_code": 0}, -2), ({"nheads": 60}, -2),
                                    ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 0)])
@@ -52,13 +52,14 @@ def test_sizes():
     assert L.dfssm_tiled_bits_bytes(10576, 2560) == 10624 * 80 * 4   # rows padded to 64
     assert L.dfssm_tiled_emb_bytes(50288, 2048) == 50304 * 2048
     assert L.dfssm_workspace_bytes(_dims()) > 0
-    assert L.dfssm_workspace_bytes(_dims(batch=9)) == 0
+    assert L.dfssm_workspace_bytes(_dims(batch=65)) == 0
 
 
 def test_null_and_shape_rejections_before_launch():
     L = _C.lib()
     assert L.dfssm_scaffold_gemm(None, None, None, None, 1, 8, 2048, None, None, None) == -1
-    assert L.dfssm_scaffold_gemm(16, 16, None, None, 5, 8, 2048, 16, None, None) == -3
+    assert L.dfssm_scaffold_gemm(16, 16, None, None, 65, 8, 2048, 16, None, None) == -3
+    assert L.dfssm_scaffold_gemm(16, 16, None, None, 0, 8, 2048, 16, None, None) == -3
     assert L.dfssm_scaffold_gemm(16, 16, None, None, 1, 8, 1000, 16, None, None) == -2
     assert L.dfssm_scaffold_gemm(8, 16, None, None, 1, 8, 2048, 16, None, None) == -4
     assert L.dfssm_ssm_step(16, 16, 4352, 16, 64, 16, 16, 16, 16, 4096, 1, 64, 64, 64, None) == -2
