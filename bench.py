@@ -211,12 +211,33 @@ def copy_calibration(mib):
     log(f"copied {mib} MiB x10")
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_decode_1p3b.md")
+
+
+def measured_traffic(batch, phase):
+    """HBM bytes per launch of `phase` at `batch` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by a plain copy's reading); None if not profiled."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) == 9 and cells[0] == str(batch) and cells[2] == phase:
+            try:
+                return int(cells[6])
+            except ValueError:
+                return None
+    return None
+
+
 def roofline_of(res, name=None):
     ks = res["kernels"]
     dom = name or max(ks, key=lambda k: ks[k]["us_per_step"])
     d = ks[dom]
     return {"bound": "hbm", "kernel": dom, "batch": res["batch"], "achieved": d["gbs"], "peak": PEAK_GBS,
-            "unit": "GB/s", "frac": round(d["gbs"] / PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(d["gbs"] / PEAK_GBS, 4),
+            "traffic": measured_traffic(res["batch"], dom),
             "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]}
 
 
