@@ -60,6 +60,9 @@ def algorithmic_bytes(cfg, B):
         2.5: D * DI // 8 + 2 * D + 16 * D + 2 * D + B * (DI + 8 + 64) + B * D * 4,
         # head: int8 table + row scales + norm_f + x
         3: V * D + 2 * V + 4 * D + B * D * 2,
+        # one-launch layer (batch <= 4): the layer's weights, its SSM/conv state read and written,
+        # x read and written
+        4: layer_bytes(cfg) + B * (H * P * N * 4 + C * 3 * 2) * 2 + B * D * 4,
     }
     return weights, state, per_phase
 
@@ -131,12 +134,24 @@ def time_kernels(m, reps=10):
     one = torch.zeros(1, device="cuda:0")
     empty = graph_time(lambda: [one.mul_(1.0) for _ in range(L)], L)
     out = {"empty": (empty, 0)}
+    if m.batch_size <= 4:
+        # the decode path runs each layer as one launch at this batch
+        def layer():
+            for li in range(L):
+                _C.check(lib.dfssm_layer_step(m._model, li, m.x.data_ptr(), m._state,
+                                              m.workspace.data_ptr(), _C.stream()))
+        out["layer (one launch)"] = (graph_time(layer, L), L)
+        phases = ("in_proj+conv",)   # the stand-alone scaffold GEMV kernel, timed as a microbenchmark
+    else:
+        phases = PHASE_NAMES
     for p, name in enumerate(PHASE_NAMES):
+        if name not in phases:
+            continue
         def body(p=p):
             for li in range(L):
                 _C.check(lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state,
                                                m.workspace.data_ptr(), _C.stream()))
-        out[name] = (graph_time(body, L), L)
+        out[name] = (graph_time(body, L), L if m.batch_size > 4 else 0)
 
     def head():
         for _ in range(L):
@@ -175,9 +190,11 @@ def measure(B, path, steps, warmup):
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode batch {B}: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, "
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / PEAK_GBS:.1f}% of HBM peak)")
+    if m.error_flag():
+        raise RuntimeError(f"decode reported error flag {m.error_flag():#x}")
     kt = time_kernels(m)
     phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
-                "head+argmax": 3}
+                "head+argmax": 3, "layer (one launch)": 4}
     kernels = {}
     for name, (us, n) in kt.items():
         if name == "empty":

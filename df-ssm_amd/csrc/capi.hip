@@ -30,7 +30,8 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, ticket, err, total;
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, ticket, err, launches, proj_t,
+      g_t, h_t, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -51,6 +52,12 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
+  // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by
+  // dfssm_workspace_init together with the head's ticket and the error flag)
+  w.launches = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
+  w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
+  w.g_t = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
+  w.h_t = off;      off = align_up(off + 2 * (size_t)r.B * 16 * 4);
   w.total = off;
   return w;
 }
@@ -109,6 +116,12 @@ int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* s
   if (!src || !dst) return DFSSM_E_NULL;
   if (rows <= 0 || !kdim_ok(k)) return DFSSM_E_DIMS;
   return hip_status(launch_tile_bits(src, dst, rows, k / 32, as_stream(stream)));
+}
+
+int dfssm_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, void* stream) {
+  if (!B || !Bs || !out) return DFSSM_E_NULL;
+  if (K <= 0) return DFSSM_E_DIMS;
+  return hip_status(launch_dequant_lora_b(B, Bs, K, out, as_stream(stream)));
 }
 
 int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream) {
@@ -189,7 +202,8 @@ int dfssm_workspace_init(const dfssm_dims* dims, void* workspace, void* stream) 
   int rc = dfssm_check_dims(dims);
   if (rc) return rc;
   const WsLayout w = ws_layout(dims);
-  // ticket and error flag are adjacent 256-byte slots; clear both with a fill kernel
+  // ticket, error flag and the fused-layer flags and epoch are the tail of the workspace; a fill
+  // kernel clears them
   uint32_t* p = (uint32_t*)((char*)workspace + w.ticket);
   const int n = (int)((w.total - w.ticket) / 4);
   hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, as_stream(stream), p, n);
@@ -220,22 +234,61 @@ int dfssm_embed(const dfssm_model* model, const int64_t* tokens, uint16_t* x, vo
   return hip_status(launch_embed(a, r.B, as_stream(stream)));
 }
 
-int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
-                      const dfssm_state* state, void* workspace, void* stream) {
+static int check_layer_args(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                            void* workspace) {
   int rc = check_model(model);
   if (rc) return rc;
   if (!x || !state || !state->h || !state->conv || !workspace) return DFSSM_E_NULL;
-  const Derived r = derive(&model->dims);
-  if (layer < 0 || layer >= r.L || phase < 0 || phase >= DFSSM_LAYER_PHASES) return DFSSM_E_RANGE;
+  if (layer < 0 || layer >= model->dims.n_layer) return DFSSM_E_RANGE;
   const dfssm_layer& Lw = model->layers[layer];
   if (!Lw.in_bits || !Lw.in_scale || !Lw.in_lA || !Lw.in_lA_s || !Lw.in_lB || !Lw.in_lB_s ||
       !Lw.out_bits || !Lw.out_scale || !Lw.out_lA || !Lw.out_lA_s || !Lw.out_lB || !Lw.out_lB_s ||
-      !Lw.conv_w || !Lw.conv_b || !Lw.A_log || !Lw.D || !Lw.dt_bias || !Lw.norm_w || !Lw.ln_w)
+      !Lw.conv_w || !Lw.conv_b || !Lw.A_log || !Lw.D || !Lw.dt_bias || !Lw.norm_w || !Lw.ln_w ||
+      !Lw.in_lBq || !Lw.out_lBq)
     return DFSSM_E_NULL;
+  if (!aligned16(Lw.in_lBq) || !aligned16(Lw.out_lBq)) return DFSSM_E_ALIGN;
   if (!aligned16(Lw.in_bits) || !aligned16(Lw.out_bits) || !aligned16(Lw.in_lA) ||
       !aligned16(Lw.out_lA) || !aligned16(state->h) || ((uintptr_t)Lw.in_lB & 7u) ||
-      ((uintptr_t)Lw.out_lB & 7u) || !aligned16(workspace) || !aligned16(Lw.ln_w) || !aligned16(Lw.norm_w))
+      ((uintptr_t)Lw.out_lB & 7u) || !aligned16(workspace) || !aligned16(Lw.ln_w) || !aligned16(Lw.norm_w) ||
+      !aligned16(x))
     return DFSSM_E_ALIGN;
+  return DFSSM_OK;
+}
+
+// The whole layer in one launch (batch <= 4).
+static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                       void* workspace, void* stream) {
+  const Derived r = derive(&model->dims);
+  const dfssm_layer& Lw = model->layers[layer];
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  FusedArgs a{};
+  a.in_bits = Lw.in_bits; a.in_ws = Lw.in_scale; a.in_lA = Lw.in_lA; a.in_lAs = Lw.in_lA_s;
+  a.in_lBq = Lw.in_lBq;
+  a.out_bits = Lw.out_bits; a.out_ws = Lw.out_scale; a.out_lA = Lw.out_lA; a.out_lAs = Lw.out_lA_s;
+  a.out_lBq = Lw.out_lBq;
+  a.conv_w = Lw.conv_w; a.conv_b = Lw.conv_b;
+  a.A_log = Lw.A_log; a.Dp = Lw.D; a.dt_bias = Lw.dt_bias;
+  a.norm_w = Lw.norm_w; a.ln_w = Lw.ln_w;
+  a.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
+  a.conv = state->conv + (size_t)layer * r.B * r.C * 3;
+  a.x = x;
+  a.projT = (uint32_t*)(ws + w.proj_t);
+  a.gT = (uint32_t*)(ws + w.g_t);
+  a.hT = (uint32_t*)(ws + w.h_t);
+  a.launches = (uint32_t*)(ws + w.launches);
+  a.err = (int*)(ws + w.err);
+  a.D = r.D; a.DI = r.DI; a.N = r.N; a.H = r.H; a.P = r.P; a.IPO = r.IPO; a.C = r.C;
+  return hip_status(launch_fused_layer(a, r.B, as_stream(stream)));
+}
+
+int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
+                      const dfssm_state* state, void* workspace, void* stream) {
+  int rc = check_layer_args(model, layer, x, state, workspace);
+  if (rc) return rc;
+  if (phase < 0 || phase >= DFSSM_LAYER_PHASES) return DFSSM_E_RANGE;
+  const Derived r = derive(&model->dims);
+  const dfssm_layer& Lw = model->layers[layer];
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
   uint16_t* proj = (uint16_t*)(ws + w.proj);
@@ -319,6 +372,11 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
 
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream) {
+  int rc = check_layer_args(model, layer, x, state, workspace);
+  if (rc) return rc;
+  const Derived r = derive(&model->dims);
+  if (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P))
+    return fused_layer(model, layer, x, state, workspace, stream);
   for (int phase = 0; phase < DFSSM_LAYER_PHASES; ++phase) {
     const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
     if (rc) return rc;

@@ -131,6 +131,34 @@ struct EmbedArgs {
   int V, D;
 };
 
+// One whole layer for 1..4 sequences in a single launch (fused.hip).
+struct FusedArgs {
+  const uint32_t* in_bits; const uint16_t* in_ws; const int8_t* in_lA; const uint16_t* in_lAs;
+  const uint16_t* in_lBq;    // (16, D) fp16(B_i8 * B_s)
+  const uint32_t* out_bits; const uint16_t* out_ws; const int8_t* out_lA; const uint16_t* out_lAs;
+  const uint16_t* out_lBq;   // (16, DI)
+  const uint16_t* conv_w; const uint16_t* conv_b;
+  const float* A_log; const float* Dp; const float* dt_bias;
+  const float* norm_w; const float* ln_w;
+  float* h;                  // (M, H, P, N) fp32 state of this layer
+  uint16_t* conv;            // (M, C, 3) fp16 conv state of this layer
+  uint16_t* x;               // (M, D) residual, updated in place
+  // words exchanged between workgroups of a launch: (tag << 16) | fp16 bits, tag = the launch's
+  // epoch mod 2^16
+  uint32_t* projT;           // (M, IPO): z | conv'd xBC | dt_raw
+  uint32_t* gT;              // (M, DI): gated SSM output
+  uint32_t* hT;              // (2, M, 16): LoRA intermediates of in_proj / out_proj
+  uint32_t* launches;        // (G) launch count of each workgroup
+  int* err;                  // error flags (bit 2: a wait timed out)
+  int D, DI, N, H, P, IPO, C;
+};
+constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
+constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
+
+bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);
+hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s);
+hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, hipStream_t s);
+
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s);

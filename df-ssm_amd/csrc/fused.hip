@@ -1,0 +1,620 @@
+// One decode layer for 1..4 sequences in a single launch (gfx950).
+//
+// At batch <= 4 a layer moves ~7.8 MB, and the five-kernel form spends most of its time in
+// launch gaps and per-kernel ramp-up. Here one grid of G workgroups (1024 threads, one per CU,
+// all co-resident) runs the layer in three phases:
+//   A  in_proj: workgroup w < gA = ceil(IPO/64) owns output rows 64w..64w+63: RMSNorm, int8
+//      quantizer and the activation bit planes of its own GEMV chunks (the inputs are 4 KiB of
+//      x, L2-resident), the packed-bit GEMV, dequantization, LoRA, conv + SiLU, and stores its
+//      rows. Workgroups gA..gA+15 compute the 16 LoRA intermediates (one rank each); the GEMV
+//      workgroups pick them up just before their epilogue.
+//   B  SSM + gate: item (sequence, head, 16-row block); a workgroup reads only the projection
+//      words the item needs (z, x, B, C, dt), updates the fp32 state and writes g.
+//   C  out_proj: workgroup w < gC = D/64 reads all of g, runs the gated RMSNorm prologue and the
+//      GEMV and adds the residual into x; workgroups gC..gC+15 compute the out_proj LoRA
+//      intermediates as in phase A.
+// The weights and the state do not depend on the activations, so each workgroup issues those
+// loads first.
+//
+// Data passed between workgroups of one launch travels as 32-bit words (tag << 16) | fp16 value,
+// stored and loaded with device-scope (agent) coherent accesses, which do not hit stale lines of
+// another XCD's L2. The tag is the launch's epoch mod 2^16; workgroup w keeps its own launch count
+// in the workspace (read at the start, written back at the end, by w alone), so every workgroup
+// of a launch derives the same epoch without any shared counter. A consumer polls the data words
+// it needs until they carry the current tag: one memory round trip, no flags, no clearing (every
+// word is rewritten by every launch). A 32-bit store
+// is single-copy atomic, so tag and value always arrive together. Every poll is bounded: on a
+// timeout the thread sets bit 2 of the workspace error flag and goes on, so the grid always
+// drains (the host reports the error).
+//
+// Arithmetic is that of prep_kernel + proj_kernel + ssm_kernel; every sum that the kernels
+// split differently (sum of squares, LoRA intermediate, C.h readout) is a sum of exactly
+// representable products accumulated in fp64.
+#include "common.h"
+#include "dfssm_kernels.h"
+
+namespace dfssm {
+
+constexpr int kFT = 1024;
+constexpr int kFW = kFT / 64;
+constexpr int kFMaxK = 5120;
+constexpr int kFMaxCPW = (kFMaxK / 128 + kFW - 1) / kFW;
+constexpr uint32_t kSpinMax = 1u << 18;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <class T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int M>
+struct FusedLds {
+  uint32_t planes[M][kFMaxK / 32][8];
+  int T[kFW][M][64];
+  uint16_t xn[kFMaxK];
+  double rd[M][kFW];   // per-wave partial sums (squares; LoRA rank)
+  float rf[M][kFW];    // per-wave partial amax
+  int ri[M][kFW];      // per-wave partial sum q
+  float hl[M][DFSSM_LORA_R];
+  float xs[M];
+};
+
+// Epilogue inputs of one output row, loaded ahead of the GEMV.
+struct EpiRow {
+  u32x4 la;
+  uint32_t cw01, cw23;
+  uint16_t ws, as, cs0, cs1, cs2, cb, xres;
+};
+
+// Conv-state update of one row, stored after the row group's outputs.
+struct ConvPend {
+  uint16_t* p;
+  uint16_t v0, v1, v2;
+};
+
+// Activations of columns 8 tid .. 8 tid + 7 (IN only) and their norm weights.
+template <int M>
+struct PIn {
+  u32x4 av[M];
+  f32x4 w0, w1;
+};
+
+template <int M, bool OUT>
+__device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K, const float* norm_w) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int m = 0; m < M; ++m) pi.av[m] = u32x4{0u, 0u, 0u, 0u};
+  pi.w0 = f32x4{0.f, 0.f, 0.f, 0.f};
+  pi.w1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (tid < K / 8) {
+    if (!OUT) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) pi.av[m] = *(const u32x4*)(act + (size_t)m * K + 8 * tid);
+    }
+    pi.w0 = *(const f32x4*)(norm_w + 8 * tid);
+    pi.w1 = *(const f32x4*)(norm_w + 8 * tid + 4);
+  }
+}
+
+__device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t* bits, int grp, int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, CH = K / 128;
+  const u32x4* b = (const u32x4*)bits + (size_t)grp * CH * 64 + lane;
+#pragma unroll
+  for (int j = 0; j < kFMaxCPW; ++j) {
+    const int c = wave + kFW * j;
+    wb[j] = c < CH ? ld_nt(b + (size_t)c * 64) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Row n = 64 grp + lane of sequence m = tid / 64 (threads tid < M * 64).
+template <int M, bool IN>
+__device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
+  EpiRow e{};
+  const int tid = threadIdx.x, m = tid >> 6, n = grp * 64 + (tid & 63);
+  const int N = IN ? a.IPO : a.D;
+  if (tid >= M * 64 || n >= N) return e;
+  e.la = *(const u32x4*)((IN ? a.in_lA : a.out_lA) + (size_t)n * DFSSM_LORA_R);
+  e.ws = (IN ? a.in_ws : a.out_ws)[n];
+  e.as = (IN ? a.in_lAs : a.out_lAs)[n];
+  if (IN) {
+    const int ch = n - a.DI;
+    if (ch >= 0 && ch < a.C) {
+      const uint16_t* cs = a.conv + ((size_t)m * a.C + ch) * 3;
+      e.cs0 = cs[0]; e.cs1 = cs[1]; e.cs2 = cs[2];
+      const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
+      e.cw01 = wc[0]; e.cw23 = wc[1];
+      e.cb = a.conv_b[ch];
+    }
+  } else {
+    e.xres = a.x[(size_t)m * a.D + n];
+  }
+  return e;
+}
+
+__device__ __forceinline__ uint32_t tagged(uint32_t tag, uint16_t v) { return (tag << 16) | v; }
+
+// Poll a tagged word until it carries `tag`; returns its fp16 bits. After a timeout (`ok`
+// false) polls return at once.
+__device__ __forceinline__ uint32_t poll1(const uint32_t* p, uint32_t tag, bool& ok, int* err) {
+  uint32_t v = ld_dev(p);
+  for (uint32_t it = 0; ok && (v >> 16) != tag; ++it) {
+    if (it == kSpinMax) {
+      ok = false;
+      atomicOr(err, 4);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    v = ld_dev(p);
+  }
+  return v & 0xffffu;
+}
+__device__ __forceinline__ bool tag_ok2(uint64_t v, uint32_t tag) {
+  return ((uint32_t)v >> 16) == tag && ((uint32_t)(v >> 32) >> 16) == tag;
+}
+__device__ __forceinline__ uint32_t pack2(uint64_t v) { return ((uint32_t)v & 0xffffu) | ((uint32_t)(v >> 32) << 16); }
+
+// N pairs of adjacent tagged words at p + 2 j (8-byte aligned), all loads in flight together;
+// out[j] = the pair's two fp16 values packed low | high.
+template <int N>
+__device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t (&out)[N], bool& ok, int* err) {
+  uint64_t v[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = ld_dev((const uint64_t*)p + j);
+  for (uint32_t it = 0; ok; ++it) {
+    bool good = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) good = good && tag_ok2(v[j], tag);
+    if (good) break;
+    if (it == kSpinMax) {
+      ok = false;
+      atomicOr(err, 4);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (!tag_ok2(v[j], tag)) v[j] = ld_dev((const uint64_t*)p + j);
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) out[j] = pack2(v[j]);
+}
+
+// RMSNorm of the M activation rows (K columns) into L.xn, one row at a time, with `body(m, mx)`
+// run after each row's normalized values are in LDS (mx = this thread's max |xn|). IN: x loaded
+// ahead (pi.av); OUT: the gated g of this launch, polled from its tagged words (gT).
+template <int M, bool OUT, class Body>
+__device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K,
+                                          uint32_t tag, int* err, Body body) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool has_v = tid < K / 8;
+  const float wv[8] = {pi.w0[0], pi.w0[1], pi.w0[2], pi.w0[3], pi.w1[0], pi.w1[1], pi.w1[2], pi.w1[3]};
+  bool ok = true;
+  for (int m = 0; m < M; ++m) {
+    u32x4 av = {0u, 0u, 0u, 0u};
+    double part = 0.0;
+    if (has_v) {
+      if (OUT) {
+        uint32_t w4[4];
+        pollv<4>(gT + (size_t)m * K + 8 * tid, tag, w4, ok, err);
+        av = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      } else {
+        av = pi.av[m];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double xv = (double)h2f((uint16_t)(av[e >> 1] >> (16 * (e & 1))));
+        part += xv * xv;
+      }
+    }
+    const double wsum = wave_sum_dpp_f64(part);
+    if (lane == 0) L.rd[m][wave] = wsum;
+    __syncthreads();  // also: every wave is done with the previous row's xn
+    double ss = 0.0;
+#pragma unroll
+    for (int w = 0; w < kFW; ++w) ss += L.rd[m][w];
+    const float var = (float)ss * (1.0f / (float)K);
+    const float r = 1.0f / sqrt_rn(var + 1e-5f);
+    float mx = 0.0f;
+    if (has_v) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float x0 = r16((h2f((uint16_t)(av[e >> 1])) * r) * wv[e]);
+        const float x1 = r16((h2f((uint16_t)(av[e >> 1] >> 16)) * r) * wv[e + 1]);
+        mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
+        o[e >> 1] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+      }
+      *(u32x4*)&L.xn[8 * tid] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    body(m, mx);
+  }
+}
+
+// Projection prologue (GEMV workgroups): per row the amax, the quantization scale, and each
+// wave's bit planes of its own GEMV chunks (no barrier before the GEMV) with their sum q.
+template <int M, bool OUT>
+__device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K, uint32_t tag, int* err) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int CH = K / 128;
+  norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float mx) {
+    const float wmax = wave_max_dpp_f32(mx);
+    if (lane == 0) L.rf[m][wave] = wmax;
+    __syncthreads();  // publishes xn and the partial maxima
+    float amax = L.rf[m][0];
+#pragma unroll
+    for (int w = 1; w < kFW; ++w) amax = fmaxf(amax, L.rf[m][w]);
+    const float xs = quant_scale(amax);
+    if (tid == 0) L.xs[m] = xs;
+    int qsum = 0;
+    for (int c = wave; c < CH; c += kFW) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int k0 = 128 * c + 64 * hh;
+        const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
+        qsum += q;
+        const uint32_t qb = (uint32_t)q & 0xffu;
+        uint32_t pw = 0u;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint64_t mask = __ballot((qb >> b) & 1u);
+          pw = lane == b ? (uint32_t)mask : pw;
+          pw = lane == 8 + b ? (uint32_t)(mask >> 32) : pw;
+        }
+        if (lane < 16) L.planes[m][k0 / 32 + (lane >> 3)][lane & 7] = pw;
+      }
+    }
+    const int wq = wave_sum_dpp_i32(qsum);
+    if (lane == 0) L.ri[m][wave] = wq;
+  });
+}
+
+// LoRA intermediate of rank r for every row (LoRA workgroups): h[m][r] =
+// fp16(sum_k xn_k * Bq[r][k]), fp16 x fp16 products exact in fp32, summed in fp64, stored as a
+// tagged word hout[m * 16 + r].
+template <int M, bool OUT>
+__device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT, int K, const float* norm_w,
+                          const uint16_t* lBq, int r, uint32_t* hout, uint32_t tag, int* err) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool has_v = tid < K / 8;
+  PIn<M> pi;
+  load_pin<M, OUT>(pi, x, K, norm_w);
+  const u32x4 b8 = has_v ? *(const u32x4*)(lBq + (size_t)r * K + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
+  norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float) {
+    double hacc = 0.0;
+    if (has_v) {
+      const u32x4 xv8 = *(const u32x4*)&L.xn[8 * tid];  // this thread's own columns
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = h2f((uint16_t)(xv8[e >> 1] >> (16 * (e & 1))));
+        const float bv = h2f((uint16_t)(b8[e >> 1] >> (16 * (e & 1))));
+        hacc += (double)(xv * bv);
+      }
+    }
+    const double hw = wave_sum_dpp_f64(hacc);
+    __syncthreads();  // the sum-of-squares partials of this row have been read by every wave
+    if (lane == 0) L.rd[m][wave] = hw;
+    __syncthreads();
+    if (tid == 0) {
+      double t = 0.0;
+#pragma unroll
+      for (int w = 0; w < kFW; ++w) t += L.rd[m][w];
+      st_dev(hout + m * DFSSM_LORA_R + r, tagged(tag, f2h((float)t)));
+    }
+  });
+}
+
+// Packed-bit GEMV of one 64-row group: per-wave partials into L.T (no barrier).
+template <int M>
+__device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[kFMaxCPW], int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int CH = K / 128;
+  uint32_t cnt[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) cnt[m][b] = 0u;
+#pragma unroll
+  for (int j = 0; j < kFMaxCPW; ++j) {
+    const int c = wave + kFW * j;
+    if (c < CH) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = wb[j][i];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const u32x4 p0 = *(const u32x4*)&L.planes[m][c * 4 + i][0];
+          const u32x4 p1 = *(const u32x4*)&L.planes[m][c * 4 + i][4];
+          cnt[m][0] += __builtin_popcount(w & p0[0]);
+          cnt[m][1] += __builtin_popcount(w & p0[1]);
+          cnt[m][2] += __builtin_popcount(w & p0[2]);
+          cnt[m][3] += __builtin_popcount(w & p0[3]);
+          cnt[m][4] += __builtin_popcount(w & p1[0]);
+          cnt[m][5] += __builtin_popcount(w & p1[1]);
+          cnt[m][6] += __builtin_popcount(w & p1[2]);
+          cnt[m][7] += __builtin_popcount(w & p1[3]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    int t = 0;
+#pragma unroll
+    for (int b = 0; b < 7; ++b) t += (int)(cnt[m][b] << b);
+    t -= (int)(cnt[m][7] << 7);
+    L.T[wave][m][lane] = t;
+  }
+}
+
+// LoRA intermediates of this phase (threads < 16 M): the first load is issued before the GEMV
+// (lora_issue), the poll completes after it (lora_finish) into L.hl; the caller then passes a
+// barrier.
+__device__ __forceinline__ uint32_t lora_issue(const uint32_t* hsrc, int M) {
+  return (int)threadIdx.x < M * DFSSM_LORA_R ? ld_dev(hsrc + threadIdx.x) : 0u;
+}
+template <int M>
+__device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc, uint32_t v, uint32_t tag, int* err) {
+  const int tid = threadIdx.x;
+  if (tid < M * DFSSM_LORA_R) {
+    bool ok = true;
+    if ((v >> 16) != tag) v = poll1(hsrc + tid, tag, ok, err);
+    L.hl[tid / DFSSM_LORA_R][tid % DFSSM_LORA_R] = h2f((uint16_t)v);
+  }
+}
+
+// Epilogue of one 64-row group (after the barrier that publishes L.T and L.hl).
+template <int M, bool IN>
+__device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag) {
+  ConvPend cp{nullptr, 0, 0, 0};
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int N = IN ? a.IPO : a.D;
+  const int n = grp * 64 + lane;
+  if (tid < M * 64 && n < N) {
+    const int m = tid >> 6;
+    int T = 0, S = 0;
+#pragma unroll
+    for (int w = 0; w < kFW; ++w) {
+      T += L.T[w][m][lane];
+      S += L.ri[m][w];
+    }
+    const int acc = 2 * T - S;
+    const float y = r16(r16(r16((float)acc) * L.xs[m]) * h2f(er.ws));
+    const float eas = h2f(er.as);
+    double lo = 0.0;
+#pragma unroll
+    for (int r = 0; r < DFSSM_LORA_R; ++r) {
+      const float aq = r16((float)(int8_t)(er.la[r >> 2] >> (8 * (r & 3))) * eas);
+      lo += (double)L.hl[m][r] * (double)aq;
+    }
+    float out = r16((float)lo + y);
+    if (IN) {
+      const int ch = n - a.DI;
+      if (ch >= 0 && ch < a.C) {
+        // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later)
+        const uint16_t xo = f2h(out);
+        cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, er.cs1, er.cs2, xo};
+        const float xv = h2f(xo);
+        float o = h2f(er.cs0) * h2f((uint16_t)er.cw01);
+        o = o + h2f(er.cs1) * h2f((uint16_t)(er.cw01 >> 16));
+        o = o + h2f(er.cs2) * h2f((uint16_t)er.cw23);
+        o = o + xv * h2f((uint16_t)(er.cw23 >> 16));
+        o = o + h2f(er.cb);
+        const float sig = 1.0f / (1.0f + dev_expf(-o));
+        out = o * sig;
+      }
+      st_dev(a.projT + (size_t)m * a.IPO + n, tagged(tag, f2h(out)));
+    } else {
+      a.x[(size_t)m * a.D + n] = f2h(h2f(er.xres) + out);
+    }
+  }
+  return cp;
+}
+
+__device__ __forceinline__ void store_conv(const ConvPend& cp) {
+  if (cp.p) {
+    cp.p[0] = cp.v0;
+    cp.p[1] = cp.v1;
+    cp.p[2] = cp.v2;
+  }
+}
+
+// SSM + gate of item `it` = (sequence m, head, 16-row block pb): wave w owns state row
+// p = 16 pb + w, lane l the state columns 2l, 2l+1. The state store of an item is deferred
+// (pend_v, pend_p) behind the next item's loads.
+template <int M>
+__device__ void ssm_item(const FusedArgs& a, int it, bool pre, f32x2 hpre, uint32_t tag, f32x2& pend_v,
+                         float*& pend_p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int PB = a.P / 16, NI = a.H * PB;
+  const int m = it / NI, rem = it % NI, head = rem / PB, pb = rem % PB;
+  const int p = pb * 16 + wave;
+  const int bc0 = 2 * a.DI, dtr = 2 * a.DI + 2 * a.N + head;
+  const float A = -dev_expf(a.A_log[head]);
+  const uint32_t* pr = a.projT + (size_t)m * a.IPO;
+  float* hp = a.h + (((size_t)m * a.H + head) * a.P + p) * a.N + 2 * lane;
+  const f32x2 h0 = pre ? hpre : __builtin_nontemporal_load((const f32x2*)hp);
+  // the item's projection words, all polled together: B and C pairs of this lane, dt, x, z
+  bool ok = true;
+  const uint32_t* q[5] = {pr + bc0 + 2 * lane, pr + bc0 + a.N + 2 * lane, pr + dtr, pr + a.DI + head * a.P + p,
+                          pr + head * a.P + p};
+  uint64_t v0 = ld_dev((const uint64_t*)q[0]), v1 = ld_dev((const uint64_t*)q[1]);
+  uint32_t v2 = ld_dev(q[2]), v3 = ld_dev(q[3]), v4 = ld_dev(q[4]);
+  for (uint32_t it = 0; ok; ++it) {
+    if (tag_ok2(v0, tag) && tag_ok2(v1, tag) && (v2 >> 16) == tag && (v3 >> 16) == tag && (v4 >> 16) == tag) break;
+    if (it == kSpinMax) {
+      ok = false;
+      atomicOr(a.err, 4);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    if (!tag_ok2(v0, tag)) v0 = ld_dev((const uint64_t*)q[0]);
+    if (!tag_ok2(v1, tag)) v1 = ld_dev((const uint64_t*)q[1]);
+    if ((v2 >> 16) != tag) v2 = ld_dev(q[2]);
+    if ((v3 >> 16) != tag) v3 = ld_dev(q[3]);
+    if ((v4 >> 16) != tag) v4 = ld_dev(q[4]);
+  }
+  const uint32_t bp = pack2(v0), cp = pack2(v1);
+  const uint16_t dth = (uint16_t)v2, xh = (uint16_t)v3, zh = (uint16_t)v4;
+  const float dt = dev_log1pf(dev_expf(h2f(dth) + a.dt_bias[head]));
+  const float abar = dev_expf(dt * A);
+  const float xv = h2f(xh);
+  const float X = xv * dt;
+  f32x2 hv;
+  hv.x = __builtin_fmaf(abar, h0.x, X * h2f((uint16_t)bp));
+  hv.y = __builtin_fmaf(abar, h0.y, X * h2f((uint16_t)(bp >> 16)));
+  double acc = (double)h2f((uint16_t)cp) * (double)hv.x + (double)h2f((uint16_t)(cp >> 16)) * (double)hv.y;
+  if (pend_p) __builtin_nontemporal_store(pend_v, (f32x2*)pend_p);
+  pend_v = hv;
+  pend_p = hp;
+  acc = wave_sum_dpp_f64(acc);
+  if (lane == 0) {
+    const float y = r16((float)acc + xv * a.Dp[head]);
+    const float z = h2f(zh);
+    const float sg = r16(1.0f / (1.0f + dev_expf(-z)));
+    const float sz = r16(z * sg);
+    const float gv = r16(y * sz);
+    st_dev(a.gT + (size_t)m * a.DI + head * a.P + p, tagged(tag, f2h(gv)));
+  }
+}
+
+template <int M>
+__global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
+  __shared__ FusedLds<M> L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const uint32_t epoch = ld_dev(a.launches + wg) + 1u;  // used first at the phase-A stores
+  const uint32_t tag = epoch & 0xffffu;
+  const int gA = (a.IPO + 63) / 64, gC = a.D / 64;
+  const int NI = a.H * (a.P / 16), items = M * NI;
+  uint32_t* hA = a.hT;
+  uint32_t* hC = a.hT + M * DFSSM_LORA_R;
+
+  // ---- loads that do not depend on the activations ----
+  u32x4 wa[kFMaxCPW];
+  EpiRow ea{};
+  PIn<M> pa;
+  if (wg < gA) {
+    load_bits(wa, a.in_bits, wg, a.D);
+    ea = load_epi<M, true>(a, wg);
+    load_pin<M, false>(pa, a.x, a.D, a.ln_w);
+  }
+  f32x2 hpre = {0.f, 0.f};
+  if (wg < items) {
+    const int PB = a.P / 16;
+    const int m = wg / NI, rem = wg % NI, head = rem / PB, p = (rem % PB) * 16 + wave;
+    hpre = __builtin_nontemporal_load((const f32x2*)(a.h + (((size_t)m * a.H + head) * a.P + p) * a.N + 2 * lane));
+  }
+
+  // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
+  if (wg < gA) {
+    prologue<M, false>(L, pa, nullptr, a.D, tag, a.err);
+    for (int grp = wg; grp < gA; grp += G) {
+      if (grp != wg) {
+        load_bits(wa, a.in_bits, grp, a.D);
+        ea = load_epi<M, true>(a, grp);
+      }
+      const uint32_t hv = lora_issue(hA, M);
+      gemv_partials<M>(L, wa, a.D);
+      lora_finish<M>(L, hA, hv, tag, a.err);
+      __syncthreads();
+      store_conv(epilogue<M, true>(L, a, ea, grp, tag));
+      __syncthreads();
+    }
+  } else if (wg < gA + DFSSM_LORA_R) {
+    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag, a.err);
+  }
+  // ---- phase B: SSM + gate ----
+  u32x4 wc[kFMaxCPW];
+  EpiRow ec{};
+  if (wg < gC) {  // phase-C weights, loaded while phase B runs
+    load_bits(wc, a.out_bits, wg, a.DI);
+    ec = load_epi<M, false>(a, wg);
+  }
+  f32x2 pend_v = {0.f, 0.f};
+  float* pend_p = nullptr;
+  for (int it = wg; it < items; it += G) ssm_item<M>(a, it, it == wg, hpre, tag, pend_v, pend_p);
+  if (pend_p) __builtin_nontemporal_store(pend_v, (f32x2*)pend_p);
+  // ---- phase C: out_proj + residual (workgroups < gC), LoRA ranks (gC .. gC + 15) ----
+  if (wg < gC) {
+    __syncthreads();  // LDS reuse after phase A
+    PIn<M> pc;
+    load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
+    prologue<M, true>(L, pc, a.gT, a.DI, tag, a.err);
+    for (int grp = wg; grp < gC; grp += G) {
+      if (grp != wg) {
+        load_bits(wc, a.out_bits, grp, a.DI);
+        ec = load_epi<M, false>(a, grp);
+      }
+      const uint32_t hv = lora_issue(hC, M);
+      gemv_partials<M>(L, wc, a.DI);
+      lora_finish<M>(L, hC, hv, tag, a.err);
+      __syncthreads();
+      (void)epilogue<M, false>(L, a, ec, grp, tag);
+      __syncthreads();
+    }
+  } else if (wg < gC + DFSSM_LORA_R) {
+    __syncthreads();
+    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag, a.err);
+  }
+  __syncthreads();  // every wave of this workgroup has read its launch count
+  if (tid == 0) st_dev(a.launches + wg, epoch);
+}
+
+static int fused_grid() {
+  static int grid[16] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+  if (grid[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<4>),
+                                                     kFT, 0) != hipSuccess || per_cu < 1)
+      return 0;
+    // one workgroup per CU: all co-resident whatever the per-CU occupancy
+    grid[dev] = cus < kFusedMaxGrid ? cus : kFusedMaxGrid;
+  }
+  return grid[dev];
+}
+
+// The grid must hold the phase-A and phase-C workgroups plus their 16 LoRA workgroups, and every
+// workgroup that reads x in phase A must also own an SSM item: phase C overwrites x once it has
+// seen every item's output, which then implies that all reads of x are done.
+bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
+  const int G = fused_grid();
+  const int gA = (IPO + 63) / 64, gC = D / 64, items = M * H * (P / 16);
+  return G >= 1 && M >= 1 && M <= 4 && gA <= kFusedMaxGroups && D <= kFMaxK && DI <= kFMaxK &&
+         G >= gA + DFSSM_LORA_R && G >= gC + DFSSM_LORA_R && items >= gA + DFSSM_LORA_R;
+}
+
+// out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.
+__global__ void dequant_lora_b_kernel(const int8_t* __restrict__ B, const uint16_t* __restrict__ Bs, int K,
+                                      uint16_t* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < DFSSM_LORA_R * K) out[i] = f2h((float)B[i] * h2f(Bs[i / K]));
+}
+
+hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, hipStream_t s) {
+  const int n = DFSSM_LORA_R * K;
+  hipLaunchKernelGGL(dequant_lora_b_kernel, dim3((n + 255) / 256), dim3(256), 0, s, B, Bs, K, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
+  if (!fused_layer_supported(M, a.IPO, a.D, a.DI, a.H, a.P)) return hipErrorNotSupported;
+  const int G = fused_grid();
+  switch (M) {
+    case 1: hipLaunchKernelGGL(layer_fused_kernel<1>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(layer_fused_kernel<2>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(layer_fused_kernel<3>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(layer_fused_kernel<4>, dim3(G), dim3(kFT), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace dfssm

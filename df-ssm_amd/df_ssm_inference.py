@@ -9,7 +9,8 @@ Same surface as the reference (df_ssm_inference.py:47-252):
     python df_ssm_inference.py model.dfssm --batch_size B --n_tokens N
 
 What runs underneath is different: the scaffold stays 1 bit per weight in HBM (re-tiled, not
-unpacked to int8), every layer is three hand-written gfx950 kernels behind the C ABI of
+unpacked to int8), every layer is one hand-written gfx950 kernel launch at batch <= 4 (five at larger
+batches) behind the C ABI of
 libdfssm_hip.so (include/dfssm.h), the SSM state is fp32, the tied head is the int8 table with
 a fused greedy argmax, and a whole decode step (embedding, all layers, head) is one HIP graph.
 Compatible extensions: generate(n_tokens, prompt=None, return_tokens=False, verbose=True) ingests
@@ -42,7 +43,7 @@ class LayerWeights:
         "in_lora_A", "in_lora_A_scale", "in_lora_B", "in_lora_B_scale",
         "out_lora_A", "out_lora_A_scale", "out_lora_B", "out_lora_B_scale",
         "conv_weight", "conv_bias", "A_log", "D", "dt_bias",
-        "norm_weight", "layer_norm_weight",
+        "norm_weight", "layer_norm_weight", "in_lora_Bq", "out_lora_Bq",
     )
 
 
@@ -89,6 +90,12 @@ class DFSSMModel:
         _C.check(_C.lib().dfssm_tile_bits(src.data_ptr(), dst.data_ptr(), rows, k, _C.stream()), "tile_bits")
         return dst
 
+    def _dequant_lora_b(self, B: torch.Tensor, Bs: torch.Tensor, k: int) -> torch.Tensor:
+        out = torch.empty(LORA_RANK, k, dtype=torch.float16, device=self.device)
+        _C.check(_C.lib().dfssm_dequant_lora_b(B.data_ptr(), Bs.data_ptr(), k, out.data_ptr(), _C.stream()),
+                 "dequant_lora_b")
+        return out
+
     def _load(self, w: DFSSMWeights):
         c = self.cfg
         dims = _C.Dims(c.n_layer, c.d_model, c.d_inner, c.d_state, c.nheads, c.p, c.ngroups,
@@ -117,6 +124,8 @@ class DFSSMModel:
             lw.A_log, lw.D, lw.dt_bias = _dev(L["A_log"], dev), _dev(L["D"], dev), _dev(L["dt_bias"], dev)
             lw.norm_weight = _dev(L["norm_w"].astype(np.float32), dev)
             lw.layer_norm_weight = _dev(L["ln_w"].astype(np.float32), dev)
+            lw.in_lora_Bq = self._dequant_lora_b(lw.in_lora_B, lw.in_lora_B_scale, D)
+            lw.out_lora_Bq = self._dequant_lora_b(lw.out_lora_B, lw.out_lora_B_scale, DI)
             self.layers.append(lw)
             d = descs[li]
             for field, t in (("in_bits", lw.in_bits), ("in_scale", lw.in_scale), ("in_lA", lw.in_lora_A),
@@ -125,7 +134,8 @@ class DFSSMModel:
                              ("out_lA_s", lw.out_lora_A_scale), ("out_lB", lw.out_lora_B),
                              ("out_lB_s", lw.out_lora_B_scale), ("conv_w", lw.conv_weight), ("conv_b", lw.conv_bias),
                              ("A_log", lw.A_log), ("D", lw.D), ("dt_bias", lw.dt_bias),
-                             ("norm_w", lw.norm_weight), ("ln_w", lw.layer_norm_weight)):
+                             ("norm_w", lw.norm_weight), ("ln_w", lw.layer_norm_weight),
+                             ("in_lBq", lw.in_lora_Bq), ("out_lBq", lw.out_lora_Bq)):
                 setattr(d, field, t.data_ptr())
         emb_src = _dev(w.emb, dev)
         self.embedding = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, D), dtype=torch.int8, device=dev)

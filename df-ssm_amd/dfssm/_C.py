@@ -28,7 +28,7 @@ class Dims(ctypes.Structure):
 
 LAYER_FIELDS = ("in_bits", "in_scale", "in_lA", "in_lA_s", "in_lB", "in_lB_s",
                 "out_bits", "out_scale", "out_lA", "out_lA_s", "out_lB", "out_lB_s",
-                "conv_w", "conv_b", "A_log", "D", "dt_bias", "norm_w", "ln_w")
+                "conv_w", "conv_b", "A_log", "D", "dt_bias", "norm_w", "ln_w", "in_lBq", "out_lBq")
 
 
 class Layer(ctypes.Structure):
@@ -52,6 +52,7 @@ _SIGS = {
     "dfssm_tiled_emb_bytes": (c_size_t, [c_int, c_int]),
     "dfssm_tile_bits": (c_int, [P, P, c_int, c_int, P]),
     "dfssm_tile_embedding": (c_int, [P, P, c_int, c_int, P]),
+    "dfssm_dequant_lora_b": (c_int, [P, P, c_int, P, P]),
     "dfssm_scaffold_gemm": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
     "dfssm_rmsnorm_quantize": (c_int, [P, P, c_int, c_int, P, P, P, P]),
     "dfssm_conv_step": (c_int, [P, P, c_int, P, P, c_int, c_int, P]),

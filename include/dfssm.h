@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 1
+#define DFSSM_ABI_VERSION 2
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
@@ -43,7 +43,9 @@ typedef struct dfssm_dims {
 
 /* Device pointers of one layer, in .dfssm order (training/export_dfssm.py:135-185). The sign bits
  * are in the tiled layout produced by dfssm_tile_bits; everything else is as stored in the file,
- * except the two norm weights, which are fp32 (fp16 files are widened at load). */
+ * except the two norm weights, which are fp32 (fp16 files are widened at load), and the two
+ * derived LoRA-B tables at the end, fp16(B_i8 * B_s) (16, K) from dfssm_dequant_lora_b -- the
+ * load-time dequantization of df_ssm_inference.py:82-83,96-97. */
 typedef struct dfssm_layer {
   const uint32_t* in_bits;   const uint16_t* in_scale;
   const int8_t* in_lA;       const uint16_t* in_lA_s;
@@ -54,6 +56,7 @@ typedef struct dfssm_layer {
   const uint16_t* conv_w;    const uint16_t* conv_b;
   const float* A_log;        const float* D;          const float* dt_bias;
   const float* norm_w;       const float* ln_w;
+  const uint16_t* in_lBq;    const uint16_t* out_lBq;
 } dfssm_layer;
 
 typedef struct dfssm_model {
@@ -83,6 +86,9 @@ size_t dfssm_tiled_emb_bytes(int vocab, int d_model);
  * scaffold kernels. Replaces the load-time unpack of df_ssm_inference.py:23-29,70-74: the copy
  * stays 1 bit per weight. k must be a multiple of 512. */
 int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* stream);
+/* LoRA-B dequantization at load: out[r][k] = fp16(B[r][k] * Bs[r]) for r < 16, k < K
+ * (df_ssm_inference.py:82-83,96-97: B_deq = (B_i8.float() * B_s.float()).half()). */
+int dfssm_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, void* stream);
 /* Re-tile the (V, D) int8 embedding for the gather and the tied head. */
 int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream);
 

@@ -49,6 +49,7 @@ def test_tiny_forward_stepwise(tiny_weights, B):
         tok = prompts[:, t + 1] if t + 1 < prompts.shape[1] else nxt
     rel = _state_rel(gpu, orc)
     print(f"B={B} worst logit err {worst:.3e} state rel {rel:.3e}")
+    assert gpu.error_flag() == 0
     assert rel <= 1e-3
     np.testing.assert_allclose(_np16(gpu.conv_state).astype(np.float32), orc.conv.astype(np.float32),
                                atol=2e-2, rtol=1e-2)
@@ -67,6 +68,7 @@ def test_tiny_generate_tokens(tiny_weights, B):
     # generating again from a reset state reproduces the same tokens
     again = gpu.generate(n_tokens=n, prompt=torch.from_numpy(prompts), return_tokens=True, verbose=False)
     np.testing.assert_array_equal(again.cpu().numpy(), ref)
+    assert gpu.error_flag() == 0
 
 
 def test_reset_state_and_token_range(tiny_weights):
@@ -104,3 +106,30 @@ def test_1p3b_greedy(w13, B, T, n):
     print(f"1.3B B={B}: state rel err {rel:.3e}, final logits max abs err {err:.3e}")
     assert rel <= 1e-3
     assert err <= 2e-2
+    assert gpu.error_flag() == 0
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
+    """dfssm_layer_step (one launch at batch <= 4) against dfssm_layer_phase 0..4 (the five-kernel
+    form) on the same inputs: x, SSM state and conv state identical bit for bit."""
+    from dfssm import _C
+    w = tiny_weights
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, 5)))  # non-trivial state
+    lib = _C.lib()
+    x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    for li in range(w.cfg.n_layer):
+        _C.check(lib.dfssm_layer_step(gpu._model, li, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
+                                      _C.stream()))
+    x1, h1, c1 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    gpu.x.copy_(x0); gpu.h_state.copy_(h0); gpu.conv_state.copy_(c0)
+    for li in range(w.cfg.n_layer):
+        for ph in range(5):
+            _C.check(lib.dfssm_layer_phase(gpu._model, li, ph, gpu.x.data_ptr(), gpu._state,
+                                           gpu.workspace.data_ptr(), _C.stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(gpu.x.view(torch.int16), x1.view(torch.int16))
+    assert torch.equal(gpu.h_state, h1)
+    assert torch.equal(gpu.conv_state.view(torch.int16), c1.view(torch.int16))
+    assert gpu.error_flag() == 0
