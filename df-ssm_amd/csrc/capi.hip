@@ -94,7 +94,7 @@ int dfssm_check_dims(const dfssm_dims* d) {
   if (!d) return DFSSM_E_NULL;
   if (d->n_layer <= 0 || d->vocab_size <= 0 || d->nheads <= 0) return DFSSM_E_DIMS;
   if (!kdim_ok(d->d_model) || !kdim_ok(d->d_inner)) return DFSSM_E_DIMS;
-  if (d->d_state != 128 || d->ngroups != 1 || d->emb_code != 1) return DFSSM_E_DIMS;
+  if (d->d_state != 128 || d->ngroups != 1 || (d->emb_code != 0 && d->emb_code != 1)) return DFSSM_E_DIMS;
   if (d->d_inner % d->nheads) return DFSSM_E_DIMS;
   const int P = d->d_inner / d->nheads;
   if (P % 16 || d->nheads % 8) return DFSSM_E_DIMS;
@@ -107,9 +107,9 @@ size_t dfssm_tiled_bits_bytes(int rows, int k) {
   return (size_t)((rows + 63) / 64 * 64) * (size_t)(k / 32) * 4;
 }
 
-size_t dfssm_tiled_emb_bytes(int vocab, int d_model) {
-  if (vocab <= 0 || d_model <= 0) return 0;
-  return (size_t)((vocab + 63) / 64 * 64) * (size_t)d_model;
+size_t dfssm_tiled_emb_bytes(int vocab, int row_bytes) {
+  if (vocab <= 0 || row_bytes <= 0) return 0;
+  return (size_t)((vocab + 63) / 64 * 64) * (size_t)row_bytes;
 }
 
 int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* stream) {
@@ -124,11 +124,11 @@ int dfssm_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* o
   return hip_status(launch_dequant_lora_b(B, Bs, K, out, as_stream(stream)));
 }
 
-int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream) {
+int dfssm_tile_embedding(const void* src, void* dst, int vocab, int row_bytes, void* stream) {
   if (!src || !dst) return DFSSM_E_NULL;
-  if (vocab <= 0 || d_model <= 0 || d_model % 64) return DFSSM_E_DIMS;
+  if (vocab <= 0 || row_bytes <= 0 || row_bytes % 64) return DFSSM_E_DIMS;
   if (((uintptr_t)src & 3u) || !aligned16(dst)) return DFSSM_E_ALIGN;
-  return hip_status(launch_tile_emb(src, dst, vocab, d_model, as_stream(stream)));
+  return hip_status(launch_tile_emb((const uint8_t*)src, (uint8_t*)dst, vocab, row_bytes, as_stream(stream)));
 }
 
 int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
@@ -216,7 +216,8 @@ int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace) {
 }
 
 static int check_model(const dfssm_model* model) {
-  if (!model || !model->layers || !model->emb || !model->emb_scale || !model->norm_f) return DFSSM_E_NULL;
+  if (!model || !model->layers || !model->emb || !model->norm_f) return DFSSM_E_NULL;
+  if (model->dims.emb_code == 1 && !model->emb_scale) return DFSSM_E_NULL;
   int rc = dfssm_check_dims(&model->dims);
   if (rc) return rc;
   if (!aligned16(model->emb)) return DFSSM_E_ALIGN;
@@ -229,7 +230,7 @@ int dfssm_embed(const dfssm_model* model, const int64_t* tokens, uint16_t* x, vo
   if (rc) return rc;
   if (!tokens || !x || !workspace) return DFSSM_E_NULL;
   const Derived r = derive(&model->dims);
-  EmbedArgs a{tokens, model->emb, model->emb_scale, x,
+  EmbedArgs a{tokens, (const uint8_t*)model->emb, model->emb_scale, model->dims.emb_code == 0 ? 1 : 0, x,
               (int*)((char*)workspace + ws_layout(&model->dims).err), r.V, r.D};
   return hip_status(launch_embed(a, r.B, as_stream(stream)));
 }
@@ -394,7 +395,8 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   char* ws = (char*)workspace;
   if (r.B > 4) {  // matrix-core head (fp32 accumulation)
     HeadArgs a{};
-    a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
+    a.x = x; a.norm_f = model->norm_f; a.emb = (const uint8_t*)model->emb; a.emb_scale = model->emb_scale;
+    a.f16 = model->dims.emb_code == 0 ? 1 : 0;
     a.V = r.V; a.D = r.D; a.logits = logits;
     a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
     a.ticket = (unsigned*)(ws + w.ticket);
@@ -403,7 +405,8 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
     return hip_status(launch_head_batched(a, r.B, as_stream(stream)));
   }
   HeadArgs a{};
-  a.x = x; a.norm_f = model->norm_f; a.emb = model->emb; a.emb_scale = model->emb_scale;
+  a.x = x; a.norm_f = model->norm_f; a.emb = (const uint8_t*)model->emb; a.emb_scale = model->emb_scale;
+    a.f16 = model->dims.emb_code == 0 ? 1 : 0;
   a.V = r.V; a.D = r.D; a.logits = logits;
   a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
   a.ticket = (unsigned*)(ws + w.ticket);

@@ -110,8 +110,9 @@ struct ConvArgs {
 struct HeadArgs {
   const uint16_t* x;         // (M, D) fp16 residual
   const float* norm_f;       // (D) fp32
-  const int8_t* emb;         // tiled int8 table
-  const uint16_t* emb_scale; // (V) fp16
+  const uint8_t* emb;        // tiled table: int8 (f16 = 0) or fp16 (f16 = 1)
+  const uint16_t* emb_scale; // (V) fp16 row scales of the int8 table
+  int f16;
   int V, D;
   uint16_t* logits;          // (M, V) fp16 or null
   float* part_val;           // (M, n_groups)
@@ -124,8 +125,9 @@ struct HeadArgs {
 
 struct EmbedArgs {
   const int64_t* tokens;     // (M)
-  const int8_t* emb;         // tiled int8 table
-  const uint16_t* emb_scale; // (V)
+  const uint8_t* emb;        // tiled table: int8 (f16 = 0) or fp16 (f16 = 1)
+  const uint16_t* emb_scale; // (V) for the int8 table
+  int f16;
   uint16_t* x;               // (M, D)
   int* err_flag;             // set to 1 if a token is out of range
   int V, D;
@@ -169,6 +171,6 @@ hipError_t launch_conv(const ConvArgs& a, int M, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
-hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStream_t s);
+hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int row_bytes, hipStream_t s);
 
 }  // namespace dfssm

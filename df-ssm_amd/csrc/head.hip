@@ -1,13 +1,14 @@
-// Embedding gather, final RMSNorm + tied int8 LM head + greedy argmax (gfx950).
+// Embedding gather, final RMSNorm + tied LM head + greedy argmax (gfx950).
 //
-// The int8 table is stored re-tiled at load time as [V_pad/64][D/16][64 lanes][16 B]: lane l of
-// a wave owns vocabulary row 64*g + l and each wave-wide 16-byte load is one contiguous 1 KiB
-// transaction. Wave w of the 256-thread workgroup covers a quarter of D.
+// The table -- int8 with an fp16 row scale (format embedding code 1), or fp16 as the exporter
+// writes it (code 0) -- is stored re-tiled at load time as [V_pad/64][row bytes/16][64 lanes]
+// [16 B]: lane l of a wave owns vocabulary row 64*g + l and each wave-wide 16-byte load is one
+// contiguous 1 KiB transaction. Wave w of the 256-thread workgroup covers a quarter of D.
 //
-// Logits (df_ssm_inference.py:210,224 with an int8 table): xf = fp16(RMSNorm(x) * norm_f),
-// logit_v = fp16(fp32(sum_k xf_k * E_i8[v,k]) * s_E[v]). The dot product is accumulated in fp64,
-// where every partial sum of fp16 x int8 products is exact, so the result does not depend on
-// the summation order. Greedy token = first index of the maximum fp16 logit (torch.argmax, :236):
+// Logits (df_ssm_inference.py:210,224): xf = fp16(RMSNorm(x) * norm_f); int8 table:
+// logit_v = fp16(fp32(sum_k xf_k * E_i8[v,k]) * s_E[v]); fp16 table: logit_v = fp16(fp32(sum_k
+// xf_k * E_16[v,k])). The dot product is accumulated in fp64, where the products (fp16 x int8,
+// fp16 x fp16) are exact, so the result does not depend on the summation order. Greedy token = first index of the maximum fp16 logit (torch.argmax, :236):
 // every workgroup writes its (max, first index) pair; the last workgroup to finish (ticket
 // counter, reset by that workgroup) reduces the pairs and may write the next token's embedding.
 #include "common.h"
@@ -15,7 +16,20 @@
 
 namespace dfssm {
 
-template <int M>
+// Element j of a 16-byte table chunk, widened: 16 int8 or 8 fp16 per chunk.
+template <bool F16>
+__device__ __forceinline__ double emb_elem(const u32x4& e4, int j) {
+  if (F16) return (double)h2f((uint16_t)(e4[j >> 1] >> (16 * (j & 1))));
+  return (double)(int)(int8_t)(e4[j >> 2] >> (8 * (j & 3)));
+}
+// Embedding value of row t (tile group tg = t / 64, lane tl = t % 64), column k, as fp16 bits.
+template <bool F16>
+__device__ __forceinline__ uint16_t emb_value(const uint8_t* emb, const uint16_t* scale, int CH, int tg, int tl, int k) {
+  if (F16) return ((const uint16_t*)(emb + (((size_t)tg * CH + (k >> 3)) * 64 + tl) * 16))[k & 7];
+  return f2h((float)(int8_t)emb[(((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16 + (k & 15)] * h2f(scale[tg * 64 + tl]));
+}
+
+template <int M, bool F16>
 __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   extern __shared__ double xf[];  // [M][D] final-normed activations as fp64
   __shared__ double part[4][M][64];
@@ -23,7 +37,8 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   __shared__ bool is_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x;
-  const int D = a.D, CH = D / 16, CPW = CH / 4;
+  constexpr int EPC = F16 ? 8 : 16;  // table elements per 16-byte chunk
+  const int D = a.D, CH = D / EPC, CPW = CH / 4;
   const u32x4* E = (const u32x4*)a.emb + ((size_t)g * CH + wave * CPW) * 64 + lane;
 
   // first group of chunks in flight before the prologue (the table does not depend on x)
@@ -54,10 +69,10 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
 #pragma unroll
     for (int c = 0; c < G; ++c) {
       const u32x4 e4 = cur[c];
-      const int k0 = (wave * CPW + c0 + c) * 16;
+      const int k0 = (wave * CPW + c0 + c) * EPC;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const double e = (double)(int)(int8_t)(e4[j >> 2] >> (8 * (j & 3)));
+      for (int j = 0; j < EPC; ++j) {
+        const double e = emb_elem<F16>(e4, j);
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[m] = __builtin_fma(xf[m * D + k0 + j], e, acc[m]);
       }
@@ -76,7 +91,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
     int bidx = 0x7fffffff;
     if (v < a.V) {
       const double s = part[0][m][lane] + part[1][m][lane] + part[2][m][lane] + part[3][m][lane];
-      const uint16_t lh = f2h((float)s * h2f(a.emb_scale[v]));
+      const uint16_t lh = F16 ? f2h((float)s) : f2h((float)s * h2f(a.emb_scale[v]));
       if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
       best = h2f(lh);
       bidx = v;
@@ -129,12 +144,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   if (a.x_next) {
     for (int m = 0; m < M; ++m) {
       const int t = next_tok[m];
-      const int tg = t >> 6, tl = t & 63;
-      const float sc = h2f(a.emb_scale[t]);
-      for (int k = tid; k < D; k += 256) {
-        const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
-        a.x_next[(size_t)m * D + k] = f2h((float)row[k & 15] * sc);
-      }
+      for (int k = tid; k < D; k += 256) a.x_next[(size_t)m * D + k] = emb_value<F16>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
     }
   }
 }
@@ -146,16 +156,13 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   if (t64 < 0 || t64 >= a.V) {
     if (threadIdx.x == 0) atomicOr(a.err_flag, 1);
   }
-  const int CH = a.D / 16, tg = t >> 6, tl = t & 63;
-  const float sc = h2f(a.emb_scale[t]);
-  for (int k = threadIdx.x; k < a.D; k += 256) {
-    const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
-    a.x[(size_t)m * a.D + k] = f2h((float)row[k & 15] * sc);
-  }
+  for (int k = threadIdx.x; k < a.D; k += 256)
+    a.x[(size_t)m * a.D + k] = a.f16 ? emb_value<true>(a.emb, a.emb_scale, a.D / 8, t >> 6, t & 63, k)
+                                     : emb_value<false>(a.emb, a.emb_scale, a.D / 16, t >> 6, t & 63, k);
 }
 
-// Re-tile a row-major (V, D) int8 table into [V_pad/64][D/16][64][16].
-__global__ void tile_emb_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int V, int D, int v_pad) {
+// Re-tile a row-major (V, D) table of D bytes per row into [V_pad/64][D/16][64][16].
+__global__ void tile_emb_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int V, int D, int v_pad) {
   const size_t total = (size_t)v_pad * D / 4;  // in 4-byte units
   const int CH = D / 16;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
@@ -171,14 +178,18 @@ __global__ void tile_emb_kernel(const int8_t* __restrict__ src, int8_t* __restri
   }
 }
 
-template <int M>
-static hipError_t launch_head_m(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
+template <int M, bool F16>
+static hipError_t launch_head_mf(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
   // dynamic LDS above 64 KiB needs an explicit opt-in (gfx950 has 160 KiB per workgroup)
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<M>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_kernel<M, F16>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(head_kernel<M>, dim3(groups), dim3(256), shm, s, a);
+  hipLaunchKernelGGL((head_kernel<M, F16>), dim3(groups), dim3(256), shm, s, a);
   return hipGetLastError();
+}
+template <int M>
+static hipError_t launch_head_m(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
+  return a.f16 ? launch_head_mf<M, true>(a, groups, shm, s) : launch_head_mf<M, false>(a, groups, shm, s);
 }
 
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
@@ -199,7 +210,7 @@ hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_tile_emb(const int8_t* src, int8_t* dst, int V, int D, hipStream_t s) {
+hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int D, hipStream_t s) {
   const int v_pad = (V + 63) / 64 * 64;
   const size_t total = (size_t)v_pad * D / 4;
   int blocks = (int)((total + 255) / 256);
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(256) void final_norm_kernel(const uint16_t* __restr
   for (int k = tid; k < D; k += 256) xf[(size_t)m * D + k] = f2h((h2f(xm[k]) * r) * norm_f[k]);
 }
 
-template <int MI>
+template <int MI, bool F16>
 __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
   constexpr int MP = MI * 16;
   __shared__ __attribute__((aligned(16))) uint16_t xs[MP][kHS];
@@ -248,7 +259,7 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
   __shared__ bool is_last;
   __shared__ int next_tok[MP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int D = a.D, CH = D / 16;
+  const int D = a.D, CH = F16 ? D / 8 : D / 16;
   const int v0 = blockIdx.x * kHV + wave * 64;
   const int vpad = (a.V + 63) / 64 * 64;
 
@@ -278,13 +289,19 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
       for (int vt = 0; vt < 4; ++vt) {
         const int v = v0 + vt * 16 + (lane & 15);
         // the tiled table holds V rounded up to 64 rows (zero padded); the last tile may pass it
-        const uint2 e8 = v < vpad ? *(const uint2*)(a.emb + (((size_t)(v >> 6) * CH + (k >> 4)) * 64 + (v & 63)) * 16 + (k & 15))
-                                  : make_uint2(0u, 0u);
         f16x8 B;
+        if (F16) {
+          const u32x4 e16 = v < vpad ? *(const u32x4*)(a.emb + (((size_t)(v >> 6) * CH + (k >> 3)) * 64 + (v & 63)) * 16)
+                                     : u32x4{0u, 0u, 0u, 0u};
+          B = __builtin_bit_cast(f16x8, e16);
+        } else {
+          const uint2 e8 = v < vpad ? *(const uint2*)(a.emb + (((size_t)(v >> 6) * CH + (k >> 4)) * 64 + (v & 63)) * 16 + (k & 15))
+                                    : make_uint2(0u, 0u);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t w = e < 4 ? e8.x : e8.y;
-          B[e] = (_Float16)(float)(int8_t)(w >> (8 * (e & 3)));
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = e < 4 ? e8.x : e8.y;
+            B[e] = (_Float16)(float)(int8_t)(w >> (8 * (e & 3)));
+          }
         }
 #pragma unroll
         for (int ib = 0; ib < MI; ++ib) acc[vt][ib] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[ib], B, acc[vt][ib], 0, 0, 0);
@@ -304,14 +321,14 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
   for (int vt = 0; vt < 4; ++vt) {
     const int v = v0 + vt * 16 + (lane & 15);
     if (v >= a.V) continue;
-    const float sc = h2f(a.emb_scale[v]);
+    const float sc = F16 ? 1.0f : h2f(a.emb_scale[v]);
 #pragma unroll
     for (int ib = 0; ib < MI; ++ib)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int m = ib * 16 + 4 * (lane >> 4) + j;
         if (m >= M) continue;
-        const uint16_t lh = f2h(acc[vt][ib][j] * sc);
+        const uint16_t lh = F16 ? f2h(acc[vt][ib][j]) : f2h(acc[vt][ib][j] * sc);
         if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
         const float lv = h2f(lh);
         if (lv > best[ib][j]) { best[ib][j] = lv; bidx[ib][j] = v; }  // v increases with vt
@@ -383,12 +400,7 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
   if (a.x_next) {
     for (int m = 0; m < M; ++m) {
       const int tk = next_tok[m];
-      const int tg = tk >> 6, tl = tk & 63;
-      const float sc = h2f(a.emb_scale[tk]);
-      for (int k = tid; k < D; k += kHT) {
-        const int8_t* row = a.emb + (((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16;
-        a.x_next[(size_t)m * D + k] = f2h((float)row[k & 15] * sc);
-      }
+      for (int k = tid; k < D; k += kHT) a.x_next[(size_t)m * D + k] = emb_value<F16>(a.emb, a.emb_scale, CH, tk >> 6, tk & 63, k);
     }
   }
 }
@@ -399,12 +411,17 @@ hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int groups = (a.V + kHV - 1) / kHV;
-  switch ((M + 15) / 16) {
-    case 1: hipLaunchKernelGGL(head_mfma_kernel<1>, dim3(groups), dim3(kHT), 0, s, a, M); break;
-    case 2: hipLaunchKernelGGL(head_mfma_kernel<2>, dim3(groups), dim3(kHT), 0, s, a, M); break;
-    case 3: hipLaunchKernelGGL(head_mfma_kernel<3>, dim3(groups), dim3(kHT), 0, s, a, M); break;
-    case 4: hipLaunchKernelGGL(head_mfma_kernel<4>, dim3(groups), dim3(kHT), 0, s, a, M); break;
+  const int mi = (M + 15) / 16;
+#define DFSSM_HEAD_MFMA(MI)                                                                        \
+  if (mi == MI) {                                                                                 \
+    if (a.f16) hipLaunchKernelGGL((head_mfma_kernel<MI, true>), dim3(groups), dim3(kHT), 0, s, a, M); \
+    else hipLaunchKernelGGL((head_mfma_kernel<MI, false>), dim3(groups), dim3(kHT), 0, s, a, M);      \
   }
+  DFSSM_HEAD_MFMA(1)
+  DFSSM_HEAD_MFMA(2)
+  DFSSM_HEAD_MFMA(3)
+  DFSSM_HEAD_MFMA(4)
+#undef DFSSM_HEAD_MFMA
   return hipGetLastError();
 }
 

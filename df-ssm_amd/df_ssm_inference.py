@@ -104,8 +104,6 @@ class DFSSMModel:
         if rc != 0:
             raise _C.DFSSMError(f"model {c} / batch {self.batch_size} not supported: "
                                 f"{_C.lib().dfssm_error_string(rc).decode()}")
-        if c.emb_code != EMB_I8:
-            raise NotImplementedError("the GPU path implements the int8 tied embedding (emb_code 1)")
         self.dims = dims
         dev = self.device
         D, DI, IPO = c.d_model, c.d_inner, c.in_proj_out
@@ -137,15 +135,19 @@ class DFSSMModel:
                              ("norm_w", lw.norm_weight), ("ln_w", lw.layer_norm_weight),
                              ("in_lBq", lw.in_lora_Bq), ("out_lBq", lw.out_lora_Bq)):
                 setattr(d, field, t.data_ptr())
+        # the table (int8 + row scale, or fp16 as the exporter writes it) re-tiled for the head
+        row_bytes = D if c.emb_code == EMB_I8 else 2 * D
         emb_src = _dev(w.emb, dev)
-        self.embedding = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, D), dtype=torch.int8, device=dev)
-        _C.check(_C.lib().dfssm_tile_embedding(emb_src.data_ptr(), self.embedding.data_ptr(), c.vocab_size, D,
-                                               _C.stream()), "tile_embedding")
+        self.embedding = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, row_bytes), dtype=torch.int8,
+                                     device=dev)
+        _C.check(_C.lib().dfssm_tile_embedding(emb_src.data_ptr(), self.embedding.data_ptr(), c.vocab_size,
+                                               row_bytes, _C.stream()), "tile_embedding")
         del emb_src
-        self.embedding_scale = _dev(w.emb_scale, dev)
+        self.embedding_scale = _dev(w.emb_scale, dev) if c.emb_code == EMB_I8 else None
         self.norm_f_weight = _dev(w.norm_f.astype(np.float32), dev)
         self._descs = descs
-        self._model = _C.Model(dims, descs, self.embedding.data_ptr(), self.embedding_scale.data_ptr(),
+        self._model = _C.Model(dims, descs, self.embedding.data_ptr(),
+                               self.embedding_scale.data_ptr() if self.embedding_scale is not None else None,
                                self.norm_f_weight.data_ptr())
         torch.cuda.synchronize(dev)
 

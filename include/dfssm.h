@@ -14,7 +14,7 @@
  *
  * Model-specific constraints (checked by dfssm_check_dims): d_state = 128, ngroups = 1,
  * LoRA rank 16, d_conv = 4, P = d_inner / nheads a multiple of 16, d_model and d_inner multiples
- * of 512 and at most 5120, nheads a multiple of 8, batch 1..64, int8 embedding (emb_code 1).
+ * of 512 and at most 5120, nheads a multiple of 8, batch 1..64.
  */
 #ifndef DFSSM_H
 #define DFSSM_H
@@ -38,7 +38,7 @@ extern "C" {
 typedef struct dfssm_dims {
   int32_t n_layer, d_model, d_inner, d_state, nheads, headdim, ngroups, vocab_size;
   int32_t batch;     /* sequences decoded together */
-  int32_t emb_code;  /* 1 = int8 table + fp16 row scale */
+  int32_t emb_code;  /* 0 = fp16 table (as the exporter writes it), 1 = int8 table + fp16 row scale */
 } dfssm_dims;
 
 /* Device pointers of one layer, in .dfssm order (training/export_dfssm.py:135-185). The sign bits
@@ -62,8 +62,8 @@ typedef struct dfssm_layer {
 typedef struct dfssm_model {
   dfssm_dims dims;
   const dfssm_layer* layers;     /* HOST array of n_layer descriptors (device pointers inside) */
-  const int8_t* emb;             /* int8 table in the tiled layout of dfssm_tile_embedding */
-  const uint16_t* emb_scale;     /* (V) fp16 row scales */
+  const void* emb;               /* table (int8 or fp16) in the tiled layout of dfssm_tile_embedding */
+  const uint16_t* emb_scale;     /* (V) fp16 row scales of an int8 table; NULL for an fp16 table */
   const float* norm_f;           /* (D) fp32 */
 } dfssm_model;
 
@@ -79,9 +79,10 @@ const char* dfssm_error_string(int code);
 int dfssm_check_dims(const dfssm_dims* dims);
 
 /* ---- load-time layout ------------------------------------------------------------------ */
-/* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, d_model) int8 table. */
+/* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, row_bytes) table
+ * (row_bytes = d_model for int8, 2 * d_model for fp16). */
 size_t dfssm_tiled_bits_bytes(int rows, int k);
-size_t dfssm_tiled_emb_bytes(int vocab, int d_model);
+size_t dfssm_tiled_emb_bytes(int vocab, int row_bytes);
 /* Re-tile row-major packed sign bits (the .dfssm int32 words, export_dfssm.py:34-42) for the
  * scaffold kernels. Replaces the load-time unpack of df_ssm_inference.py:23-29,70-74: the copy
  * stays 1 bit per weight. k must be a multiple of 512. */
@@ -89,8 +90,9 @@ int dfssm_tile_bits(const uint32_t* src, uint32_t* dst, int rows, int k, void* s
 /* LoRA-B dequantization at load: out[r][k] = fp16(B[r][k] * Bs[r]) for r < 16, k < K
  * (df_ssm_inference.py:82-83,96-97: B_deq = (B_i8.float() * B_s.float()).half()). */
 int dfssm_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, void* stream);
-/* Re-tile the (V, D) int8 embedding for the gather and the tied head. */
-int dfssm_tile_embedding(const int8_t* src, int8_t* dst, int vocab, int d_model, void* stream);
+/* Re-tile the row-major embedding table (V rows of row_bytes bytes: int8 or fp16 values) for the
+ * gather and the tied head (replaces the fp16 table kept by df_ssm_inference.py:63-64). */
+int dfssm_tile_embedding(const void* src, void* dst, int vocab, int row_bytes, void* stream);
 
 /* ---- single operators ------------------------------------------------------------------ */
 /* Scaffold GEMM: acc[m][n] = sum_k q[m][k] * (bit ? +1 : -1) (exact int32) and, if y_out is

@@ -40,7 +40,7 @@ def _dims(**kw):
 
 @pytest.mark.parametrize("kw,rc", [({}, 0), ({"batch": 4}, 0), ({"batch": 5}, 0), ({"batch": 64}, 0), ({"batch": 65}, -3), ({"batch": 0}, -3),
                                    ({"d_state": 64}, -2), ({"ngroups": 2}, -2), ({"d_model": 2000}, -2),
-                                   ({"emb_code": 0}, -2), ({"nheads": 60}, -2),
+                                   ({"emb_code": 0}, 0), ({"emb_code": 2}, -2), ({"nheads": 60}, -2),
                                    ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 0)])
 def test_check_dims(kw, rc):
     assert _C.lib().dfssm_check_dims(_dims(**kw)) == rc
@@ -51,6 +51,7 @@ def test_sizes():
     assert L.dfssm_tiled_bits_bytes(8512, 2048) == 8512 * 64 * 4
     assert L.dfssm_tiled_bits_bytes(10576, 2560) == 10624 * 80 * 4   # rows padded to 64
     assert L.dfssm_tiled_emb_bytes(50288, 2048) == 50304 * 2048
+    assert L.dfssm_tiled_emb_bytes(50288, 4096) == 50304 * 4096   # fp16 rows
     assert L.dfssm_workspace_bytes(_dims()) > 0
     assert L.dfssm_workspace_bytes(_dims(batch=65)) == 0
 

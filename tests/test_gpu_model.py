@@ -133,3 +133,34 @@ def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
     assert torch.equal(gpu.h_state, h1)
     assert torch.equal(gpu.conv_state.view(torch.int16), c1.view(torch.int16))
     assert gpu.error_flag() == 0
+
+
+@pytest.fixture(scope="module")
+def tiny_weights_f16():
+    # the exporter's fp16 embedding table (format embedding code 0)
+    return make_weights(config_tiny(n_layer=3, emb_code=0), seed=4)
+
+
+@pytest.mark.parametrize("B", [1, 3, 5])
+def test_tiny_fp16_embedding(tiny_weights_f16, B):
+    """An fp16 tied table: gather and head (fp64-exact at batch <= 4, fp16 matrix cores with fp32
+    accumulation above) against the oracle; identical greedy tokens."""
+    w = tiny_weights_f16
+    assert w.emb.dtype == np.float16 and w.emb_scale is None
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    orc = O.OracleModel(w, B)
+    prompts = make_prompts(B, w.cfg.vocab_size, 4)
+    tok = prompts[:, 0]
+    for t in range(12):
+        logits_g = _np16(gpu.forward(torch.from_numpy(tok).to(DEV))).astype(np.float32)
+        logits_o, nxt = orc.step(tok)
+        err = np.abs(logits_g - logits_o.astype(np.float32)).max()
+        if B <= 4:
+            assert err == 0.0, f"step {t}: logits differ by {err}"
+        assert err <= 2e-2
+        np.testing.assert_array_equal(logits_g.argmax(axis=1), nxt)
+        tok = prompts[:, t + 1] if t + 1 < prompts.shape[1] else nxt
+    got = gpu.generate(n_tokens=9, prompt=torch.from_numpy(prompts), return_tokens=True, verbose=False)
+    ref, _ = O.OracleModel(w, B).generate(prompts, 9)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    assert gpu.error_flag() == 0
