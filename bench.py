@@ -67,19 +67,19 @@ def algorithmic_bytes(cfg, B):
     return weights, state, per_phase
 
 
-def build_model(B, path):
+def build_model(B, path, shape="1p3b"):
     import torch
     from df_ssm_inference import DFSSMModel
     from dfssm.format import expected_size, write_dfssm
-    from dfssm.synth import config_1p3b, make_weights
-    cfg = config_1p3b()
+    from dfssm.synth import config_1p3b, config_2p7b, make_weights
+    cfg = config_1p3b() if shape == "1p3b" else config_2p7b()
     w = None
     if not (os.path.exists(path) and os.path.getsize(path) == expected_size(cfg)):
         t = time.time()
         w = make_weights(cfg, seed=0)
         write_dfssm(path + ".tmp", w)
         os.replace(path + ".tmp", path)
-        log(f"wrote synthetic 1.3B model to {path} ({time.time() - t:.1f}s)")
+        log(f"wrote synthetic {shape} model to {path} ({time.time() - t:.1f}s)")
     t = time.time()
     m = DFSSMModel(path, device="cuda:0", batch_size=B)
     torch.cuda.synchronize()
@@ -175,13 +175,13 @@ def cpu_baseline(weights, prompt, n_tokens):
                       f"AVX-512 VNNI, OpenMP {threads} threads) + NumPy fp32 head; {secs:.1f} s"}
 
 
-def measure(B, path, steps, warmup):
+def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
     """Decode throughput and per-kernel timing at batch B (one model instance)."""
     import torch
     from dfssm.synth import make_prompts
-    m, w = build_model(B, path)
+    m, w = build_model(B, path, shape)
     cfg = m.cfg
-    prompts = make_prompts(B, cfg.vocab_size, 32)
+    prompts = make_prompts(B, cfg.vocab_size, prompt_len)
     ms, nsteps = time_decode(m, prompts, steps, warmup)
     ms_per_step = ms / nsteps
     tok_s = B * nsteps / (ms / 1e3)
@@ -268,6 +268,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--model-path", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_1p3b_seed0.dfssm"))
+    ap.add_argument("--config4", type=int, default=1,
+                    help="also measure config 4: 2.7B shape, batch 64, 512-token prompt, 256 timed steps (0: skip)")
+    ap.add_argument("--model-path-2p7b", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_2p7b_seed0.dfssm"))
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 10 device-to-device copies of this many MiB (counter calibration) and exit")
     a = ap.parse_args()
@@ -283,6 +286,10 @@ def main():
     second = None
     if a.batch2 and a.batch2 != a.batch:
         second, _, _ = measure(a.batch2, a.model_path, a.steps, a.warmup)
+
+    c4 = None
+    if a.config4:
+        c4, _, _ = measure(64, a.model_path_2p7b, 256, 16, shape="2p7b", prompt_len=512)
 
     cpu = None
     if not a.no_cpu:
@@ -316,6 +323,11 @@ def main():
         out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],
                          "step_roofline": second["step_roofline"], "roofline": roofline_of(second),
                          "scaffold_roofline": roofline_of(second, "in_proj+conv"), "kernels": second["kernels"]}
+    if c4:
+        out["config4"] = {"workload": "config4: 2.7B-shape DF-SSM greedy decode, batch 64, 512-token prompt "
+                                      "ingested, 256 timed steps", "batch": 64, "tok_s": c4["tok_s"],
+                          "ms_per_step": c4["ms_per_step"], "step_roofline": c4["step_roofline"],
+                          "roofline": roofline_of(c4), "kernels": c4["kernels"]}
     print(json.dumps(out), flush=True)
 
 

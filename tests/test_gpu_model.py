@@ -164,3 +164,26 @@ def test_tiny_fp16_embedding(tiny_weights_f16, B):
     ref, _ = O.OracleModel(w, B).generate(prompts, 9)
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
     assert gpu.error_flag() == 0
+
+
+def test_2p7b_layer_shapes_batch64():
+    """Config 4's layer shapes (d_model 2560, d_inner 5120, 80 heads, in_proj 10576) at batch 64 on
+    the matrix-core path, 4 layers and a 4096-token vocabulary so that the oracle stays fast:
+    logits within 2e-2, identical greedy tokens, state within 1e-3 relative."""
+    from dfssm.format import DFSSMConfig
+    c = DFSSMConfig(n_layer=4, d_model=2560, d_inner=5120, d_state=128, nheads=80, headdim=64, ngroups=1,
+                    vocab_size=4096, kw=4)
+    w = make_weights(c, seed=5)
+    B = 64
+    print("2.7B-shape layers, batch 64", flush=True)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    orc = O.OracleModel(w, B)
+    prompts = make_prompts(B, c.vocab_size, 3)
+    ref, _ = orc.generate(prompts, 3)
+    got = gpu.generate(n_tokens=3, prompt=torch.from_numpy(prompts), return_tokens=True, verbose=False)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    assert _state_rel(gpu, orc) <= 1e-3
+    lg = _np16(gpu.forward(torch.from_numpy(ref[:, -1]).to(DEV))).astype(np.float32)
+    lo, _ = orc.step(ref[:, -1])
+    assert np.abs(lg - lo.astype(np.float32)).max() <= 2e-2
+    assert gpu.error_flag() == 0
