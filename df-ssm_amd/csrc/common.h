@@ -79,22 +79,6 @@ __device__ __forceinline__ float dev_log1pf(float y) {  // y >= 0
   return lg + (y - (u - 1.0f)) / u;
 }
 
-// Wave64 sums (xor butterfly: every lane ends with the total).
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, DFSSM_WAVE);
-  return v;
-}
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, DFSSM_WAVE);
-  return v;
-}
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, DFSSM_WAVE));
-  return v;
-}
 
 // Fast wave reductions on the DPP crossbar (a few cycles per step, against ~100 for the LDS
 // permute behind __shfl_xor). gfx9 DPP controls: quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E
@@ -151,9 +135,11 @@ __device__ __forceinline__ float wave_max_dpp_f32(float v) {
 }
 
 // Block-wide sums / max for blockDim.x == NT (multiple of 64). `red` must hold NT/64 entries.
+// Every sum reduced this way in the decode kernels is exact (fp64 sums of exactly representable
+// products, integer sums), so the reduction order does not change results.
 template <int NT>
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
-  v = wave_sum_f64(v);
+  v = wave_sum_dpp_f64(v);
   const int w = threadIdx.x / DFSSM_WAVE;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;
@@ -165,7 +151,7 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
 }
 template <int NT>
 __device__ __forceinline__ float block_max_f32(float v, float* red) {
-  v = wave_max_f32(v);
+  v = wave_max_dpp_f32(v);
   const int w = threadIdx.x / DFSSM_WAVE;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;
@@ -177,7 +163,7 @@ __device__ __forceinline__ float block_max_f32(float v, float* red) {
 }
 template <int NT>
 __device__ __forceinline__ int block_sum_i32(int v, int* red) {
-  v = wave_sum_i32(v);
+  v = wave_sum_dpp_i32(v);
   const int w = threadIdx.x / DFSSM_WAVE;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;

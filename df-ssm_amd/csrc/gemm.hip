@@ -6,8 +6,8 @@
 // four 0/1 bytes is one multiply and one mask: (nib * 0x00204081) & 0x01010101 -- the four
 // shifted copies of the nibble occupy disjoint bit ranges, so the product has no carries.
 //
-// One workgroup (1024 threads = 16 waves) owns a group of 64 output rows and up to 32 activation
-// rows (larger batches are split by the launcher). Wave w = (row tile rt = w % 4, k slot kq = w / 4).
+// One workgroup (1024 threads = 16 waves) owns a group of 64 output rows; it keeps their bits in
+// registers and walks the activation rows in blocks of 32 (16 when K > 4096). Wave w = (row tile rt = w % 4, k slot kq = w / 4).
 // The 16-byte bit chunks c of the row group (128 columns each) are dealt out as
 // c = kq + 4 j + 16 sb to lane group j = lane / 16 of wave slot kq, block sb: every lane keeps its
 // chunks in registers, loaded once, fully coalesced. Within an MFMA step lane group j supplies
@@ -27,31 +27,25 @@ constexpr int kMaxSB = 3;  // bit-chunk blocks per lane: ceil(K / 128 / 16) for 
 
 template <int MI, int MODE>
 __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
-  constexpr int MP = MI * 16;
+  constexpr int MP = MI * 16;  // activation rows per block
   extern __shared__ __attribute__((aligned(16))) int8_t qs[];  // MP rows x QS bytes; then partials
   __shared__ int Ssum[MP];
   __shared__ float hl[MP][DFSSM_LORA_R];
   __shared__ float xsl[MP];
+  __shared__ uint32_t zero_s;  // read back as 0 in every row block (see below)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rt = wave & 3, kq = wave >> 2, j = lane >> 4;
   const int g = blockIdx.x;
   const int K = a.K, CH = K / 128, M = a.M;
   const int QS = K + 16;  // padded LDS row stride
 
-  // ---- loads, all issued before any use: bits (registers), q tile (LDS), epilogue rows ----
+  // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows ----
   const int r = rt * 16 + (lane & 15);
   u32x4 wb[kMaxSB];
 #pragma unroll
   for (int sb = 0; sb < kMaxSB; ++sb) {
     const int c = kq + 4 * j + 16 * sb;
     wb[sb] = c < CH ? ld_nt((const u32x4*)a.bits + ((size_t)g * CH + c) * 64 + r) : u32x4{0u, 0u, 0u, 0u};
-  }
-  const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
-  for (int v = tid; v < nvq; v += kGT) {
-    const int row = v / (K / 16), c16 = v % (K / 16);
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (row < M) x = *(const u32x4*)(a.q + (size_t)row * a.ld_q + c16 * 16);
-    *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
   }
   const int n = g * 64 + r;
   const bool nrow = n < a.N;
@@ -73,105 +67,124 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       cb = a.conv_b[ch];
     }
   }
-  for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
-    const int m = i >> 4;
-    hl[m][i & 15] = (a.h && m < M) ? a.h[(size_t)m * DFSSM_LORA_R + (i & 15)] : 0.0f;
-  }
-  if (tid < MP) {
-    xsl[tid] = tid < M ? (a.xs ? a.xs[tid] : (a.xs16 ? h2f(a.xs16[tid]) : 0.0f)) : 0.0f;
-  }
-  __syncthreads();
-  // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
-  for (int row = wave; row < MP; row += kGT / 64) {
-    int s = 0;
-    for (int c16 = lane; c16 < K / 16; c16 += 64) {
-      const u32x4 x = *(const u32x4*)(qs + (size_t)row * QS + c16 * 16);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s += (int)(int8_t)(x[e >> 2] >> (8 * (e & 3)));
+  if (tid == 0) zero_s = 0u;
+#pragma nounroll
+  for (int m0 = 0; m0 < M; m0 += MP) {
+    const int MB = M - m0 < MP ? M - m0 : MP;  // rows in this block
+    // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
+    __syncthreads();  // the previous block's partials (in qs) have been read
+    const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
+    for (int v = tid; v < nvq; v += kGT) {
+      const int row = v / (K / 16), c16 = v % (K / 16);
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
+      *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
     }
-    s = wave_sum_i32(s);
-    if (lane == 0) Ssum[row] = s;
-  }
+    for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
+      const int m = i >> 4;
+      hl[m][i & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (i & 15)] : 0.0f;
+    }
+    if (tid < MP) {
+      xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
+    }
+    __syncthreads();
+    // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
+    for (int row = wave; row < MP; row += kGT / 64) {
+      int s = 0;
+      for (int c16 = lane; c16 < K / 16; c16 += 64) {
+        const u32x4 x = *(const u32x4*)(qs + (size_t)row * QS + c16 * 16);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += (int)(int8_t)(x[e >> 2] >> (8 * (e & 3)));
+      }
+      s = wave_sum_dpp_i32(s);
+      if (lane == 0) Ssum[row] = s;
+    }
 
-  // ---- MFMA over this wave's chunks ----
-  v4i acc[MI];
+    // ---- MFMA over this wave's chunks ----
+    // The 0/1 byte expansion of the bits does not change between row blocks; a volatile zero from
+    // LDS keeps the compiler from hoisting all 24 expanded operands (96 registers) out of the loop.
+    const uint32_t zero = *(volatile uint32_t*)&zero_s;
+    v4i acc[MI];
 #pragma unroll
-  for (int i = 0; i < MI; ++i) acc[i] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < MI; ++i) acc[i] = v4i{0, 0, 0, 0};
 #pragma unroll
-  for (int sb = 0; sb < kMaxSB; ++sb) {
-    if (kq + 16 * sb < CH) {  // wave-uniform: some lane group has a chunk in this block
-      const int c = kq + 4 * j + 16 * sb;
-      const bool valid = c < CH;
+    for (int sb = 0; sb < kMaxSB; ++sb) {
+      if (kq + 16 * sb < CH) {  // wave-uniform: some lane group has a chunk in this block
+        const int c = kq + 4 * j + 16 * sb;
+        const bool valid = c < CH;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t w = wb[sb][s >> 1];
-        const uint32_t b16 = valid ? ((s & 1) ? (w >> 16) : (w & 0xffffu)) : 0u;
-        v4i B;
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t w = wb[sb][s >> 1] ^ zero;
+          const uint32_t b16 = valid ? ((s & 1) ? (w >> 16) : (w & 0xffffu)) : 0u;
+          v4i B;
 #pragma unroll
-        for (int nib = 0; nib < 4; ++nib) B[nib] = (int)((((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u);
-        const int k = valid ? 128 * c + 16 * s : 0;
+          for (int nib = 0; nib < 4; ++nib) B[nib] = (int)((((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u);
+          const int k = valid ? 128 * c + 16 * s : 0;
 #pragma unroll
-        for (int ib = 0; ib < MI; ++ib) {
-          const v4i A = *(const v4i*)(qs + (size_t)(ib * 16 + (lane & 15)) * QS + k);
-          acc[ib] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[ib], 0, 0, 0);
+          for (int ib = 0; ib < MI; ++ib) {
+            const v4i A = *(const v4i*)(qs + (size_t)(ib * 16 + (lane & 15)) * QS + k);
+            acc[ib] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[ib], 0, 0, 0);
+          }
         }
       }
     }
-  }
-  __syncthreads();  // q tile no longer needed: reuse it for the partials
-  int* part = (int*)qs;  // [kq][rt][ib][e][lane]
+    __syncthreads();  // q tile no longer needed: reuse it for the partials
+    int* part = (int*)qs;  // [kq][rt][ib][e][lane]
 #pragma unroll
-  for (int ib = 0; ib < MI; ++ib)
+    for (int ib = 0; ib < MI; ++ib)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) part[(((kq * 4 + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
-  __syncthreads();
+      for (int e = 0; e < 4; ++e) part[(((kq * 4 + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
+    __syncthreads();
 
-  // ---- epilogue: wave (rt, kq) finishes accumulator element e = kq of each tile ----
-  if (!nrow) return;
-  double aqd[DFSSM_LORA_R];
+    // ---- epilogue: wave (rt, kq) finishes accumulator element e = kq of each tile ----
+    if (nrow) {
+      double aqd[DFSSM_LORA_R];
 #pragma unroll
-  for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
-    aqd[rr] = (double)r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * e_as);
+      for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
+        aqd[rr] = (double)r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * e_as);
 #pragma unroll
-  for (int ib = 0; ib < MI; ++ib) {
-    const int e = kq;
-    const int m = ib * 16 + 4 * j + e;
-    if (m >= M) continue;
-    int T = 0;
+      for (int ib = 0; ib < MI; ++ib) {
+        const int e = kq;
+        const int mb = ib * 16 + 4 * j + e;  // row within the block
+        if (mb >= MB) continue;
+        const int m = m0 + mb;
+        int T = 0;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
-    const int accv = 2 * T - Ssum[m];
-    if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
-    const float y = r16(r16(r16((float)accv) * xsl[m]) * e_ws);
-    if (MODE == DFSSM_MODE_SCAFFOLD) {
-      if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
-      continue;
-    }
-    double lo = 0.0;
+        for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
+        const int accv = 2 * T - Ssum[mb];
+        if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
+        const float y = r16(r16(r16((float)accv) * xsl[mb]) * e_ws);
+        if (MODE == DFSSM_MODE_SCAFFOLD) {
+          if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
+          continue;
+        }
+        double lo = 0.0;
 #pragma unroll
-    for (int rr = 0; rr < DFSSM_LORA_R; ++rr) lo += (double)hl[m][rr] * aqd[rr];
-    float out = r16((float)lo + y);
-    uint16_t* op = a.out + (size_t)m * a.ld_out + n;
-    if (MODE == DFSSM_MODE_IN) {
-      if (conv_row) {
-        uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
-        const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
-        const uint16_t xo = f2h(out);
-        cs[0] = s1;
-        cs[1] = s2;
-        cs[2] = xo;
-        const float xv = h2f(xo);
-        float o = h2f(s0) * h2f((uint16_t)cw01);
-        o = o + h2f(s1) * h2f((uint16_t)(cw01 >> 16));
-        o = o + h2f(s2) * h2f((uint16_t)cw23);
-        o = o + xv * h2f((uint16_t)(cw23 >> 16));
-        o = o + h2f(cb);
-        const float sig = 1.0f / (1.0f + dev_expf(-o));
-        out = o * sig;
+        for (int rr = 0; rr < DFSSM_LORA_R; ++rr) lo += (double)hl[mb][rr] * aqd[rr];
+        float out = r16((float)lo + y);
+        uint16_t* op = a.out + (size_t)m * a.ld_out + n;
+        if (MODE == DFSSM_MODE_IN) {
+          if (conv_row) {
+            uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
+            const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
+            const uint16_t xo = f2h(out);
+            cs[0] = s1;
+            cs[1] = s2;
+            cs[2] = xo;
+            const float xv = h2f(xo);
+            float o = h2f(s0) * h2f((uint16_t)cw01);
+            o = o + h2f(s1) * h2f((uint16_t)(cw01 >> 16));
+            o = o + h2f(s2) * h2f((uint16_t)cw23);
+            o = o + xv * h2f((uint16_t)(cw23 >> 16));
+            o = o + h2f(cb);
+            const float sig = 1.0f / (1.0f + dev_expf(-o));
+            out = o * sig;
+          }
+          *op = f2h(out);
+        } else {
+          *op = f2h(h2f(*op) + out);
+        }
       }
-      *op = f2h(out);
-    } else {
-      *op = f2h(h2f(*op) + out);
     }
   }
 }
@@ -193,23 +206,10 @@ static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
 }
 
 template <int MODE>
-static hipError_t launch_gemm_mode(const GemmArgs& a0, hipStream_t s) {
-  // rows per launch: the q tile (rows x (K + 16) bytes) must fit the 160 KiB of LDS
-  const int rows = a0.K <= 4096 ? 32 : 16;
-  for (int m0 = 0; m0 < a0.M; m0 += rows) {
-    GemmArgs a = a0;
-    a.M = a0.M - m0 < rows ? a0.M - m0 : rows;
-    a.q = a0.q + (size_t)m0 * a0.ld_q;
-    if (a0.xs) a.xs = a0.xs + m0;
-    if (a0.xs16) a.xs16 = a0.xs16 + m0;
-    if (a0.h) a.h = a0.h + (size_t)m0 * DFSSM_LORA_R;
-    if (a0.out) a.out = a0.out + (size_t)m0 * a0.ld_out;
-    if (a0.acc_out) a.acc_out = a0.acc_out + (size_t)m0 * a0.N;
-    if (a0.conv_state) a.conv_state = a0.conv_state + (size_t)m0 * a0.conv_c * 3;
-    const hipError_t e = a.M > 16 ? launch_gemm_mi<2, MODE>(a, s) : launch_gemm_mi<1, MODE>(a, s);
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
+  // one launch for all rows; the kernel walks them in blocks whose q tile (rows x (K + 16) bytes)
+  // fits the 160 KiB of LDS: 32 rows up to K = 4096, 16 above
+  return (a.M > 16 && a.K <= 4096) ? launch_gemm_mi<2, MODE>(a, s) : launch_gemm_mi<1, MODE>(a, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {

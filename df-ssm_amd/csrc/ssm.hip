@@ -50,8 +50,7 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs a) {
   }
   st_nt_f4(hp, f32x4{hv[0], hv[1], hv[2], hv[3]});
   st_nt_f4(hp + 4, f32x4{hv[4], hv[5], hv[6], hv[7]});
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
+  acc = row_sum_f64(acc);  // the 16 lanes of a row (one DPP row) share state row p
   const float y = r16((float)acc + xv * a.D[head]);
   double gsqd = 0.0;
   if ((tid & 15) == 0) {
@@ -68,9 +67,7 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs a) {
   if (a.sumsq_slots) {
     __shared__ double part[4];
     // lanes 0,16,32,48 of each wave hold the 4 rows' g^2; others hold 0
-    double s = gsqd;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const double s = wave_sum_dpp_f64(gsqd);
     if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
     if (tid == 0) a.sumsq_slots[(size_t)m * a.n_slots + blockIdx.x] = part[0] + part[1] + part[2] + part[3];
