@@ -31,7 +31,7 @@ Derived derive(const dfssm_dims* d) {
 
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, ticket, err, launches, proj_t,
-      g_t, h_t, total;
+      g_t, h_t, dt_t, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -58,6 +58,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
   w.g_t = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
   w.h_t = off;      off = align_up(off + 2 * (size_t)r.B * 16 * 4);
+  w.dt_t = off;     off = align_up(off + 2 * (size_t)r.B * r.H * 8);
   w.total = off;
   return w;
 }
@@ -277,6 +278,7 @@ static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const d
   a.projT = (uint32_t*)(ws + w.proj_t);
   a.gT = (uint32_t*)(ws + w.g_t);
   a.hT = (uint32_t*)(ws + w.h_t);
+  a.dtT = (uint64_t*)(ws + w.dt_t);
   a.launches = (uint32_t*)(ws + w.launches);
   a.err = (int*)(ws + w.err);
   a.D = r.D; a.DI = r.DI; a.N = r.N; a.H = r.H; a.P = r.P; a.IPO = r.IPO; a.C = r.C;

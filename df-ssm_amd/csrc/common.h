@@ -110,6 +110,13 @@ __device__ __forceinline__ double row_sum_f64(double v) {
   v += dpp_f64<0x128>(v);
   return v;
 }
+__device__ __forceinline__ int row_sum_i32(int v) {
+  v += dpp_i32<0xB1>(v);
+  v += dpp_i32<0x4E>(v);
+  v += dpp_i32<0x124>(v);
+  v += dpp_i32<0x128>(v);
+  return v;
+}
 __device__ __forceinline__ double wave_sum_dpp_f64(double v) {
   v = row_sum_f64(v);
   return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
@@ -181,8 +188,28 @@ __device__ __forceinline__ float quant_scale(float amax) {
   return r16(c * (1.0f / 127.0f));
 }
 __device__ __forceinline__ int quant_i8(float x, float scale) {
-  float t = __builtin_rintf(r16(x / scale));
-  t = t > 127.0f ? 127.0f : t;
-  t = t < -128.0f ? -128.0f : t;
-  return (int)t;
+  const float t = __builtin_rintf(r16(x / scale));  // finite: |x| <= amax, scale > 0
+  return (int)__builtin_amdgcn_fmed3f(t, -128.0f, 127.0f);
+}
+
+// Bit planes of 64 int8 values, one per lane (q of element k0 + lane): w[b] = bit b of elements
+// k0 .. k0 + 31, w[8 + b] = bit b of elements k0 + 32 .. k0 + 63 (one ballot per plane). The
+// words are wave-uniform (scalar registers); one lane stores them (planes_store).
+__device__ __forceinline__ void planes64(int q, uint32_t (&w)[16]) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint64_t mask = __ballot((q >> b) & 1);
+    w[b] = (uint32_t)mask;
+    w[8 + b] = (uint32_t)(mask >> 32);
+  }
+}
+// The 16 words to dst[0..15] (16-byte aligned; LDS or global), from lane 0.
+__device__ __forceinline__ void planes_store(uint32_t* dst, const uint32_t (&w)[16]) {
+  if ((threadIdx.x & 63) == 0) {
+    u32x4* d = (u32x4*)dst;
+    d[0] = u32x4{w[0], w[1], w[2], w[3]};
+    d[1] = u32x4{w[4], w[5], w[6], w[7]};
+    d[2] = u32x4{w[8], w[9], w[10], w[11]};
+    d[3] = u32x4{w[12], w[13], w[14], w[15]};
+  }
 }

@@ -147,9 +147,10 @@ struct FusedArgs {
   uint16_t* x;               // (M, D) residual, updated in place
   // words exchanged between workgroups of a launch: (tag << 16) | fp16 bits, tag = the launch's
   // epoch mod 2^16
-  uint32_t* projT;           // (M, IPO): z | conv'd xBC | dt_raw
+  uint32_t* projT;           // (M, IPO): gate z sigma(z) | conv'd xBC (dt rows unused)
   uint32_t* gT;              // (M, DI): gated SSM output
   uint32_t* hT;              // (2, M, 16): LoRA intermediates of in_proj / out_proj
+  uint64_t* dtT;             // (M, H, 2): softplus dt and exp(dt A) per head, (tag << 32) | fp32 bits
   uint32_t* launches;        // (G) launch count of each workgroup
   int* err;                  // error flags (bit 2: a wait timed out)
   int D, DI, N, H, P, IPO, C;

@@ -5,11 +5,13 @@
 // all co-resident) runs the layer in three phases:
 //   A  in_proj: workgroup w < gA = ceil(IPO/64) owns output rows 64w..64w+63: RMSNorm, int8
 //      quantizer and the activation bit planes of its own GEMV chunks (the inputs are 4 KiB of
-//      x, L2-resident), the packed-bit GEMV, dequantization, LoRA, conv + SiLU, and stores its
-//      rows. Workgroups gA..gA+15 compute the 16 LoRA intermediates (one rank each); the GEMV
+//      x, L2-resident), the packed-bit GEMV, dequantization, LoRA, and per row type: the gate
+//      z sigma(z) (z rows), conv + SiLU (x, B, C rows), softplus dt and exp(dt A) (dt rows).
+//      Workgroups gA..gA+15 compute the 16 LoRA intermediates (one rank each); the GEMV
 //      workgroups pick them up just before their epilogue.
-//   B  SSM + gate: item (sequence, head, 16-row block); a workgroup reads only the projection
-//      words the item needs (z, x, B, C, dt), updates the fp32 state and writes g.
+//   B  SSM + gate: item (sequence, head, 16-row block); two waves per item poll the words the
+//      item needs (gate, x, B, C, dt) into LDS, then every wave updates one fp32 state row and
+//      writes its g.
 //   C  out_proj: workgroup w < gC = D/64 reads all of g, runs the gated RMSNorm prologue and the
 //      GEMV and adds the residual into x; workgroups gC..gC+15 compute the out_proj LoRA
 //      intermediates as in phase A.
@@ -28,8 +30,8 @@
 // drains (the host reports the error).
 //
 // Arithmetic is that of prep_kernel + proj_kernel + ssm_kernel; every sum that the kernels
-// split differently (sum of squares, LoRA intermediate, C.h readout) is a sum of exactly
-// representable products accumulated in fp64.
+// split differently (sum of squares, LoRA intermediate and LoRA term, C.h readout) is a sum of
+// exactly representable products accumulated in fp64, and integer sums are exact.
 #include "common.h"
 #include "dfssm_kernels.h"
 
@@ -40,6 +42,7 @@ constexpr int kFW = kFT / 64;
 constexpr int kFMaxK = 5120;
 constexpr int kFMaxCPW = (kFMaxK / 128 + kFW - 1) / kFW;
 constexpr uint32_t kSpinMax = 1u << 18;
+constexpr int kMaxItems = kFW / 2;  // SSM items per workgroup (two polling waves each)
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -52,22 +55,32 @@ __device__ __forceinline__ void st_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Words of one SSM item, polled by two waves and shared through LDS.
+struct ItemLds {
+  uint32_t bc[DFSSM_WAVE * 2];  // B (pairs 0..63) and C (pairs 64..127), fp16 pairs
+  uint16_t x[16], gate[16];     // x and z sigma(z) of the item's 16 rows
+  float dt, abar;               // softplus dt and exp(dt A) of the item's head
+};
+
 template <int M>
 struct FusedLds {
   uint32_t planes[M][kFMaxK / 32][8];
-  int T[kFW][M][64];
+  int T[M][64][kFW + 1];  // per-wave GEMV partials of each row (padded against bank conflicts)
   uint16_t xn[kFMaxK];
   double rd[M][kFW];   // per-wave partial sums (squares; LoRA rank)
   float rf[M][kFW];    // per-wave partial amax
   int ri[M][kFW];      // per-wave partial sum q
   float hl[M][DFSSM_LORA_R];
   float xs[M];
+  ItemLds item[kMaxItems];
 };
 
-// Epilogue inputs of one output row, loaded ahead of the GEMV.
+// Epilogue inputs of one output row, loaded ahead of the GEMV. Thread t works on row t / 16 of
+// the group with wave partial / LoRA rank s = t % 16; threads s < M also finalize sequence s.
 struct EpiRow {
-  u32x4 la;
   uint32_t cw01, cw23;
+  float bias, A;             // dt rows: dt_bias and A = -exp(A_log) of the head
+  int8_t la;                 // LoRA A[n][s]
   uint16_t ws, as, cs0, cs1, cs2, cb, xres;
 };
 
@@ -111,24 +124,29 @@ __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t*
   }
 }
 
-// Row n = 64 grp + lane of sequence m = tid / 64 (threads tid < M * 64).
+// Row n = 64 grp + tid / 16; the sequence-specific inputs for m = tid % 16 < M.
 template <int M, bool IN>
 __device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
   EpiRow e{};
-  const int tid = threadIdx.x, m = tid >> 6, n = grp * 64 + (tid & 63);
+  const int tid = threadIdx.x, s = tid & 15, n = grp * 64 + (tid >> 4);
   const int N = IN ? a.IPO : a.D;
-  if (tid >= M * 64 || n >= N) return e;
-  e.la = *(const u32x4*)((IN ? a.in_lA : a.out_lA) + (size_t)n * DFSSM_LORA_R);
-  e.ws = (IN ? a.in_ws : a.out_ws)[n];
+  if (n >= N) return e;
+  e.la = (IN ? a.in_lA : a.out_lA)[(size_t)n * DFSSM_LORA_R + s];
   e.as = (IN ? a.in_lAs : a.out_lAs)[n];
+  if (s >= M) return e;
+  const int m = s;
+  e.ws = (IN ? a.in_ws : a.out_ws)[n];
   if (IN) {
-    const int ch = n - a.DI;
+    const int ch = n - a.DI, dtr = n - (2 * a.DI + 2 * a.N);
     if (ch >= 0 && ch < a.C) {
       const uint16_t* cs = a.conv + ((size_t)m * a.C + ch) * 3;
       e.cs0 = cs[0]; e.cs1 = cs[1]; e.cs2 = cs[2];
       const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
       e.cw01 = wc[0]; e.cw23 = wc[1];
       e.cb = a.conv_b[ch];
+    } else if (dtr >= 0) {
+      e.bias = a.dt_bias[dtr];
+      e.A = -dev_expf(a.A_log[dtr]);
     }
   } else {
     e.xres = a.x[(size_t)m * a.D + n];
@@ -257,15 +275,9 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
         const int k0 = 128 * c + 64 * hh;
         const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
         qsum += q;
-        const uint32_t qb = (uint32_t)q & 0xffu;
-        uint32_t pw = 0u;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const uint64_t mask = __ballot((qb >> b) & 1u);
-          pw = lane == b ? (uint32_t)mask : pw;
-          pw = lane == 8 + b ? (uint32_t)(mask >> 32) : pw;
-        }
-        if (lane < 16) L.planes[m][k0 / 32 + (lane >> 3)][lane & 7] = pw;
+        uint32_t pw[16];
+        planes64(q, pw);
+        planes_store(&L.planes[m][k0 / 32][0], pw);
       }
     }
     const int wq = wave_sum_dpp_i32(qsum);
@@ -347,7 +359,7 @@ __device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[
 #pragma unroll
     for (int b = 0; b < 7; ++b) t += (int)(cnt[m][b] << b);
     t -= (int)(cnt[m][7] << 7);
-    L.T[wave][m][lane] = t;
+    L.T[m][lane][wave] = t;
   }
 }
 
@@ -367,50 +379,61 @@ __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc
   }
 }
 
-// Epilogue of one 64-row group (after the barrier that publishes L.T and L.hl).
+// Epilogue of one 64-row group (after the barrier that publishes L.T and L.hl), 16 threads per
+// row: acc = sum over waves s of (2 T_s - sum q_s) and the LoRA term sum_r h_r aq_r as DPP row
+// sums (exact: integers, and exactly representable products in fp64); thread s = m then
+// finalizes sequence m. IN: z rows store the gate z sigma(z), x/B/C rows conv + SiLU, dt rows
+// softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x.
 template <int M, bool IN>
 __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag) {
   ConvPend cp{nullptr, 0, 0, 0};
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
-  const int n = grp * 64 + lane;
-  if (tid < M * 64 && n < N) {
-    const int m = tid >> 6;
-    int T = 0, S = 0;
+  const int n = grp * 64 + j;
+  const float aq = r16((float)er.la * h2f(er.as));
+  int accm = 0;
+  double lom = 0.0;
 #pragma unroll
-    for (int w = 0; w < kFW; ++w) {
-      T += L.T[w][m][lane];
-      S += L.ri[m][w];
+  for (int m = 0; m < M; ++m) {
+    const int part = row_sum_i32(2 * L.T[m][j][s] - L.ri[m][s]);
+    const double lo = row_sum_f64((double)L.hl[m][s] * (double)aq);
+    if (s == m) {
+      accm = part;
+      lom = lo;
     }
-    const int acc = 2 * T - S;
-    const float y = r16(r16(r16((float)acc) * L.xs[m]) * h2f(er.ws));
-    const float eas = h2f(er.as);
-    double lo = 0.0;
-#pragma unroll
-    for (int r = 0; r < DFSSM_LORA_R; ++r) {
-      const float aq = r16((float)(int8_t)(er.la[r >> 2] >> (8 * (r & 3))) * eas);
-      lo += (double)L.hl[m][r] * (double)aq;
+  }
+  if (s >= M || n >= N) return cp;
+  const int m = s;
+  const float y = r16(r16(r16((float)accm) * L.xs[m]) * h2f(er.ws));
+  float out = r16((float)lom + y);
+  if (IN) {
+    const int ch = n - a.DI, dtr = n - (2 * a.DI + 2 * a.N);
+    if (ch < 0) {  // z row: the gate z sigma(z)
+      const float sg = r16(1.0f / (1.0f + dev_expf(-out)));
+      out = r16(out * sg);
+    } else if (ch < a.C) {
+      // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later)
+      const uint16_t xo = f2h(out);
+      cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, er.cs1, er.cs2, xo};
+      const float xv = h2f(xo);
+      float o = h2f(er.cs0) * h2f((uint16_t)er.cw01);
+      o = o + h2f(er.cs1) * h2f((uint16_t)(er.cw01 >> 16));
+      o = o + h2f(er.cs2) * h2f((uint16_t)er.cw23);
+      o = o + xv * h2f((uint16_t)(er.cw23 >> 16));
+      o = o + h2f(er.cb);
+      const float sig = 1.0f / (1.0f + dev_expf(-o));
+      out = o * sig;
+    } else {  // dt row of head dtr
+      const float dt = dev_log1pf(dev_expf(out + er.bias));
+      const float abar = dev_expf(dt * er.A);
+      uint64_t* w = a.dtT + ((size_t)m * a.H + dtr) * 2;
+      st_dev(w, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, dt));
+      st_dev(w + 1, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, abar));
+      return cp;
     }
-    float out = r16((float)lo + y);
-    if (IN) {
-      const int ch = n - a.DI;
-      if (ch >= 0 && ch < a.C) {
-        // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later)
-        const uint16_t xo = f2h(out);
-        cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, er.cs1, er.cs2, xo};
-        const float xv = h2f(xo);
-        float o = h2f(er.cs0) * h2f((uint16_t)er.cw01);
-        o = o + h2f(er.cs1) * h2f((uint16_t)(er.cw01 >> 16));
-        o = o + h2f(er.cs2) * h2f((uint16_t)er.cw23);
-        o = o + xv * h2f((uint16_t)(er.cw23 >> 16));
-        o = o + h2f(er.cb);
-        const float sig = 1.0f / (1.0f + dev_expf(-o));
-        out = o * sig;
-      }
-      st_dev(a.projT + (size_t)m * a.IPO + n, tagged(tag, f2h(out)));
-    } else {
-      a.x[(size_t)m * a.D + n] = f2h(h2f(er.xres) + out);
-    }
+    st_dev(a.projT + (size_t)m * a.IPO + n, tagged(tag, f2h(out)));
+  } else {
+    a.x[(size_t)m * a.D + n] = f2h(h2f(er.xres) + out);
   }
   return cp;
 }
@@ -423,62 +446,82 @@ __device__ __forceinline__ void store_conv(const ConvPend& cp) {
   }
 }
 
-// SSM + gate of item `it` = (sequence m, head, 16-row block pb): wave w owns state row
-// p = 16 pb + w, lane l the state columns 2l, 2l+1. The state store of an item is deferred
-// (pend_v, pend_p) behind the next item's loads.
-template <int M>
-__device__ void ssm_item(const FusedArgs& a, int it, bool pre, f32x2 hpre, uint32_t tag, f32x2& pend_v,
-                         float*& pend_p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Item `it` = (sequence m, head, 16-row block pb); NI = H * P / 16 items per sequence.
+struct Item {
+  int m, head, pb;
+};
+__device__ __forceinline__ Item item_of(const FusedArgs& a, int it) {
   const int PB = a.P / 16, NI = a.H * PB;
-  const int m = it / NI, rem = it % NI, head = rem / PB, pb = rem % PB;
-  const int p = pb * 16 + wave;
-  const int bc0 = 2 * a.DI, dtr = 2 * a.DI + 2 * a.N + head;
-  const float A = -dev_expf(a.A_log[head]);
-  const uint32_t* pr = a.projT + (size_t)m * a.IPO;
-  float* hp = a.h + (((size_t)m * a.H + head) * a.P + p) * a.N + 2 * lane;
-  const f32x2 h0 = pre ? hpre : __builtin_nontemporal_load((const f32x2*)hp);
-  // the item's projection words, all polled together: B and C pairs of this lane, dt, x, z
+  const int m = it / NI, rem = it % NI;
+  return Item{m, rem / PB, rem % PB};
+}
+
+// This thread's two state columns of the item's row p = 16 pb + wave.
+__device__ __forceinline__ float* state_row(const FusedArgs& a, const Item& t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  return a.h + (((size_t)t.m * a.H + t.head) * a.P + t.pb * 16 + wave) * a.N + 2 * lane;
+}
+
+// Poll the words of item k (waves 2k and 2k + 1) into L.item[k]. Wave 2k: B and C (lane l:
+// words 4l .. 4l + 3 of the 256); wave 2k + 1: lanes 0..15 x, 16..31 the gate of the 16 rows,
+// lanes 32 and 33 dt and exp(dt A).
+template <int M>
+__device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, uint32_t tag) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t* pr = a.projT + (size_t)t.m * a.IPO;
   bool ok = true;
-  const uint32_t* q[5] = {pr + bc0 + 2 * lane, pr + bc0 + a.N + 2 * lane, pr + dtr, pr + a.DI + head * a.P + p,
-                          pr + head * a.P + p};
-  uint64_t v0 = ld_dev((const uint64_t*)q[0]), v1 = ld_dev((const uint64_t*)q[1]);
-  uint32_t v2 = ld_dev(q[2]), v3 = ld_dev(q[3]), v4 = ld_dev(q[4]);
-  for (uint32_t it = 0; ok; ++it) {
-    if (tag_ok2(v0, tag) && tag_ok2(v1, tag) && (v2 >> 16) == tag && (v3 >> 16) == tag && (v4 >> 16) == tag) break;
-    if (it == kSpinMax) {
-      ok = false;
-      atomicOr(a.err, 4);
-      break;
+  if (wave == 2 * k) {
+    uint32_t w[2];
+    pollv<2>(pr + 2 * a.DI + 4 * lane, tag, w, ok, a.err);
+    L.item[k].bc[2 * lane] = w[0];
+    L.item[k].bc[2 * lane + 1] = w[1];
+  } else if (wave == 2 * k + 1) {
+    const int r0 = t.head * a.P + 16 * t.pb;
+    if (lane < 32) {
+      const uint32_t* p = lane < 16 ? pr + a.DI + r0 + lane : pr + r0 + (lane - 16);
+      const uint32_t v = poll1(p, tag, ok, a.err);
+      if (lane < 16) L.item[k].x[lane] = (uint16_t)v;
+      else L.item[k].gate[lane - 16] = (uint16_t)v;
+    } else if (lane < 34) {
+      const uint64_t* p = a.dtT + ((size_t)t.m * a.H + t.head) * 2 + (lane - 32);
+      uint64_t v = ld_dev(p);
+      for (uint32_t it = 0; ok && (uint32_t)(v >> 32) != tag; ++it) {
+        if (it == kSpinMax) {
+          ok = false;
+          atomicOr(a.err, 4);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        v = ld_dev(p);
+      }
+      const float f = __builtin_bit_cast(float, (uint32_t)v);
+      if (lane == 32) L.item[k].dt = f;
+      else L.item[k].abar = f;
     }
-    __builtin_amdgcn_s_sleep(1);
-    if (!tag_ok2(v0, tag)) v0 = ld_dev((const uint64_t*)q[0]);
-    if (!tag_ok2(v1, tag)) v1 = ld_dev((const uint64_t*)q[1]);
-    if ((v2 >> 16) != tag) v2 = ld_dev(q[2]);
-    if ((v3 >> 16) != tag) v3 = ld_dev(q[3]);
-    if ((v4 >> 16) != tag) v4 = ld_dev(q[4]);
   }
-  const uint32_t bp = pack2(v0), cp = pack2(v1);
-  const uint16_t dth = (uint16_t)v2, xh = (uint16_t)v3, zh = (uint16_t)v4;
-  const float dt = dev_log1pf(dev_expf(h2f(dth) + a.dt_bias[head]));
-  const float abar = dev_expf(dt * A);
-  const float xv = h2f(xh);
-  const float X = xv * dt;
+}
+
+// SSM + gate of item k (after the barrier that publishes L.item[k]): wave w owns state row
+// p = 16 pb + w, lane l the state columns 2l, 2l+1.
+template <int M>
+__device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, f32x2 h0,
+                                         float Dh, uint32_t tag) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = t.pb * 16 + wave;
+  const ItemLds& I = L.item[k];
+  const uint32_t bp = I.bc[lane], cp = I.bc[DFSSM_WAVE + lane];
+  const float xv = h2f(I.x[wave]);
+  const float X = xv * I.dt;
   f32x2 hv;
-  hv.x = __builtin_fmaf(abar, h0.x, X * h2f((uint16_t)bp));
-  hv.y = __builtin_fmaf(abar, h0.y, X * h2f((uint16_t)(bp >> 16)));
+  hv.x = __builtin_fmaf(I.abar, h0.x, X * h2f((uint16_t)bp));
+  hv.y = __builtin_fmaf(I.abar, h0.y, X * h2f((uint16_t)(bp >> 16)));
   double acc = (double)h2f((uint16_t)cp) * (double)hv.x + (double)h2f((uint16_t)(cp >> 16)) * (double)hv.y;
-  if (pend_p) __builtin_nontemporal_store(pend_v, (f32x2*)pend_p);
-  pend_v = hv;
-  pend_p = hp;
+  __builtin_nontemporal_store(hv, (f32x2*)state_row(a, t));
   acc = wave_sum_dpp_f64(acc);
   if (lane == 0) {
-    const float y = r16((float)acc + xv * a.Dp[head]);
-    const float z = h2f(zh);
-    const float sg = r16(1.0f / (1.0f + dev_expf(-z)));
-    const float sz = r16(z * sg);
-    const float gv = r16(y * sz);
-    st_dev(a.gT + (size_t)m * a.DI + head * a.P + p, tagged(tag, f2h(gv)));
+    const float y = r16((float)acc + xv * Dh);
+    const float gv = r16(y * h2f(I.gate[wave]));
+    st_dev(a.gT + (size_t)t.m * a.DI + t.head * a.P + p, tagged(tag, f2h(gv)));
   }
 }
 
@@ -503,12 +546,9 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     ea = load_epi<M, true>(a, wg);
     load_pin<M, false>(pa, a.x, a.D, a.ln_w);
   }
-  f32x2 hpre = {0.f, 0.f};
-  if (wg < items) {
-    const int PB = a.P / 16;
-    const int m = wg / NI, rem = wg % NI, head = rem / PB, p = (rem % PB) * 16 + wave;
-    hpre = __builtin_nontemporal_load((const f32x2*)(a.h + (((size_t)m * a.H + head) * a.P + p) * a.N + 2 * lane));
-  }
+  // state row of this workgroup's first SSM item (the other items' rows load before phase B's polls)
+  f32x2 h0 = {0.f, 0.f};
+  if (wg < items) h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg)));
 
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
   if (wg < gA) {
@@ -535,10 +575,25 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     load_bits(wc, a.out_bits, wg, a.DI);
     ec = load_epi<M, false>(a, wg);
   }
-  f32x2 pend_v = {0.f, 0.f};
-  float* pend_p = nullptr;
-  for (int it = wg; it < items; it += G) ssm_item<M>(a, it, it == wg, hpre, tag, pend_v, pend_p);
-  if (pend_p) __builtin_nontemporal_store(pend_v, (f32x2*)pend_p);
+  const int nk = wg < items ? (items - 1 - wg) / G + 1 : 0;  // <= kMaxItems
+  if (nk > 0) {
+    f32x2 hk[kMaxItems];
+    float dk[kMaxItems];
+    hk[0] = h0;
+#pragma unroll
+    for (int k = 0; k < kMaxItems; ++k) {
+      if (k < nk) {
+        const Item t = item_of(a, wg + k * G);
+        if (k > 0) hk[k] = __builtin_nontemporal_load((const f32x2*)state_row(a, t));
+        dk[k] = a.Dp[t.head];
+      }
+    }
+    for (int k = 0; k < nk; ++k) poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kMaxItems; ++k)
+      if (k < nk) ssm_item<M>(L, a, k, item_of(a, wg + k * G), hk[k], dk[k], tag);
+  }
   // ---- phase C: out_proj + residual (workgroups < gC), LoRA ranks (gC .. gC + 15) ----
   if (wg < gC) {
     __syncthreads();  // LDS reuse after phase A
@@ -583,12 +638,15 @@ static int fused_grid() {
 
 // The grid must hold the phase-A and phase-C workgroups plus their 16 LoRA workgroups, and every
 // workgroup that reads x in phase A must also own an SSM item: phase C overwrites x once it has
-// seen every item's output, which then implies that all reads of x are done.
+// seen every item's output, which then implies that all reads of x are done. A workgroup polls
+// at most kMaxItems items (two waves each). The state width (d_state 128 = two columns per lane)
+// and P % 16 == 0 are checked with the model dims.
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
   const int G = fused_grid();
   const int gA = (IPO + 63) / 64, gC = D / 64, items = M * H * (P / 16);
   return G >= 1 && M >= 1 && M <= 4 && gA <= kFusedMaxGroups && D <= kFMaxK && DI <= kFMaxK &&
-         G >= gA + DFSSM_LORA_R && G >= gC + DFSSM_LORA_R && items >= gA + DFSSM_LORA_R;
+         G >= gA + DFSSM_LORA_R && G >= gC + DFSSM_LORA_R && items >= gA + DFSSM_LORA_R &&
+         items <= kMaxItems * G;
 }
 
 // out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.

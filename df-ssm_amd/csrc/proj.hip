@@ -113,16 +113,9 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
     qsum += q;
     if (k0 >= lo && k0 < hi) {
       if (a.q_out) a.q_out[(size_t)m * a.ld_q + k0 + lane] = (int8_t)q;
-      const uint32_t qb = (uint32_t)q & 0xffu;
-      uint32_t pw = 0u;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const uint64_t mask = __ballot((qb >> b) & 1u);
-        pw = lane == b ? (uint32_t)mask : pw;
-        pw = lane == 8 + b ? (uint32_t)(mask >> 32) : pw;
-      }
-      if (a.planes_out && lane < 16)
-        a.planes_out[((size_t)m * (a.ld_q / 32) + k0 / 32 + (lane >> 3)) * 8 + (lane & 7)] = pw;
+      uint32_t pw[16];
+      planes64(q, pw);
+      if (a.planes_out) planes_store(a.planes_out + ((size_t)m * (a.ld_q / 32) + k0 / 32) * 8, pw);
     }
   }
   if (rr == 0) {
