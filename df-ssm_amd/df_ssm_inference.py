@@ -83,18 +83,14 @@ class DFSSMModel:
         return cls(None, device=device, batch_size=batch_size, weights=weights)
 
     # ------------------------------------------------------------------ load
-    def _tile_bits(self, packed: np.ndarray, rows: int, k: int) -> torch.Tensor:
+    def _tile_bits(self, packed: np.ndarray, rows: int, k: int, dst: torch.Tensor) -> None:
         src = _dev(packed, self.device)
-        nbytes = _C.lib().dfssm_tiled_bits_bytes(rows, k)
-        dst = torch.empty(nbytes // 4, dtype=torch.int32, device=self.device)
+        assert dst.numel() * 4 == _C.lib().dfssm_tiled_bits_bytes(rows, k)
         _C.check(_C.lib().dfssm_tile_bits(src.data_ptr(), dst.data_ptr(), rows, k, _C.stream()), "tile_bits")
-        return dst
 
-    def _dequant_lora_b(self, B: torch.Tensor, Bs: torch.Tensor, k: int) -> torch.Tensor:
-        out = torch.empty(LORA_RANK, k, dtype=torch.float16, device=self.device)
+    def _dequant_lora_b(self, B: torch.Tensor, Bs: torch.Tensor, k: int, out: torch.Tensor) -> None:
         _C.check(_C.lib().dfssm_dequant_lora_b(B.data_ptr(), Bs.data_ptr(), k, out.data_ptr(), _C.stream()),
                  "dequant_lora_b")
-        return out
 
     def _load(self, w: DFSSMWeights):
         c = self.cfg
@@ -108,32 +104,51 @@ class DFSSMModel:
         dev = self.device
         D, DI, IPO = c.d_model, c.d_inner, c.in_proj_out
         descs = (_C.Layer * c.n_layer)()
+        # One allocation per field for all layers (layer l at a fixed stride), so that the decode
+        # step can run every layer in one launch (dfssm_decode_step checks the strides).
+        nL = c.n_layer
+
+        def stacked(key, cast=None):
+            return _dev(np.stack([cast(L[key]) if cast else L[key] for L in w.layers]), dev)
+
+        in_bits = torch.empty(nL, _C.lib().dfssm_tiled_bits_bytes(IPO, D) // 4, dtype=torch.int32, device=dev)
+        out_bits = torch.empty(nL, _C.lib().dfssm_tiled_bits_bytes(D, DI) // 4, dtype=torch.int32, device=dev)
         for li, L in enumerate(w.layers):
+            self._tile_bits(L["in_packed"], IPO, D, in_bits[li])
+            self._tile_bits(L["out_packed"], D, DI, out_bits[li])
+        f32 = lambda a: a.astype(np.float32)
+        fields = {
+            "in_scale": stacked("in_scale"), "in_lA": stacked("in_lA"), "in_lA_s": stacked("in_lA_s"),
+            "in_lB": stacked("in_lB"), "in_lB_s": stacked("in_lB_s"),
+            "out_scale": stacked("out_scale"), "out_lA": stacked("out_lA"), "out_lA_s": stacked("out_lA_s"),
+            "out_lB": stacked("out_lB"), "out_lB_s": stacked("out_lB_s"),
+            "conv_w": stacked("conv_w"), "conv_b": stacked("conv_b"),
+            "A_log": stacked("A_log"), "D": stacked("D"), "dt_bias": stacked("dt_bias"),
+            "norm_w": stacked("norm_w", f32), "ln_w": stacked("ln_w", f32),
+        }
+        in_lBq = torch.empty(nL, LORA_RANK, D, dtype=torch.float16, device=dev)
+        out_lBq = torch.empty(nL, LORA_RANK, DI, dtype=torch.float16, device=dev)
+        for li in range(nL):
+            self._dequant_lora_b(fields["in_lB"][li], fields["in_lB_s"][li], D, in_lBq[li])
+            self._dequant_lora_b(fields["out_lB"][li], fields["out_lB_s"][li], DI, out_lBq[li])
+        fields.update(in_bits=in_bits, out_bits=out_bits, in_lBq=in_lBq, out_lBq=out_lBq)
+        self._stacked = fields
+        for li in range(nL):
+            F = {k: v[li] for k, v in fields.items()}
             lw = LayerWeights()
-            lw.in_bits = self._tile_bits(L["in_packed"], IPO, D)
-            lw.in_scale = _dev(L["in_scale"], dev)
-            lw.in_lora_A, lw.in_lora_A_scale = _dev(L["in_lA"], dev), _dev(L["in_lA_s"], dev)
-            lw.in_lora_B, lw.in_lora_B_scale = _dev(L["in_lB"], dev), _dev(L["in_lB_s"], dev)
-            lw.out_bits = self._tile_bits(L["out_packed"], D, DI)
-            lw.out_scale = _dev(L["out_scale"], dev)
-            lw.out_lora_A, lw.out_lora_A_scale = _dev(L["out_lA"], dev), _dev(L["out_lA_s"], dev)
-            lw.out_lora_B, lw.out_lora_B_scale = _dev(L["out_lB"], dev), _dev(L["out_lB_s"], dev)
-            lw.conv_weight, lw.conv_bias = _dev(L["conv_w"], dev), _dev(L["conv_b"], dev)
-            lw.A_log, lw.D, lw.dt_bias = _dev(L["A_log"], dev), _dev(L["D"], dev), _dev(L["dt_bias"], dev)
-            lw.norm_weight = _dev(L["norm_w"].astype(np.float32), dev)
-            lw.layer_norm_weight = _dev(L["ln_w"].astype(np.float32), dev)
-            lw.in_lora_Bq = self._dequant_lora_b(lw.in_lora_B, lw.in_lora_B_scale, D)
-            lw.out_lora_Bq = self._dequant_lora_b(lw.out_lora_B, lw.out_lora_B_scale, DI)
+            lw.in_bits, lw.in_scale = F["in_bits"], F["in_scale"]
+            lw.in_lora_A, lw.in_lora_A_scale = F["in_lA"], F["in_lA_s"]
+            lw.in_lora_B, lw.in_lora_B_scale = F["in_lB"], F["in_lB_s"]
+            lw.out_bits, lw.out_scale = F["out_bits"], F["out_scale"]
+            lw.out_lora_A, lw.out_lora_A_scale = F["out_lA"], F["out_lA_s"]
+            lw.out_lora_B, lw.out_lora_B_scale = F["out_lB"], F["out_lB_s"]
+            lw.conv_weight, lw.conv_bias = F["conv_w"], F["conv_b"]
+            lw.A_log, lw.D, lw.dt_bias = F["A_log"], F["D"], F["dt_bias"]
+            lw.norm_weight, lw.layer_norm_weight = F["norm_w"], F["ln_w"]
+            lw.in_lora_Bq, lw.out_lora_Bq = F["in_lBq"], F["out_lBq"]
             self.layers.append(lw)
             d = descs[li]
-            for field, t in (("in_bits", lw.in_bits), ("in_scale", lw.in_scale), ("in_lA", lw.in_lora_A),
-                             ("in_lA_s", lw.in_lora_A_scale), ("in_lB", lw.in_lora_B), ("in_lB_s", lw.in_lora_B_scale),
-                             ("out_bits", lw.out_bits), ("out_scale", lw.out_scale), ("out_lA", lw.out_lora_A),
-                             ("out_lA_s", lw.out_lora_A_scale), ("out_lB", lw.out_lora_B),
-                             ("out_lB_s", lw.out_lora_B_scale), ("conv_w", lw.conv_weight), ("conv_b", lw.conv_bias),
-                             ("A_log", lw.A_log), ("D", lw.D), ("dt_bias", lw.dt_bias),
-                             ("norm_w", lw.norm_weight), ("ln_w", lw.layer_norm_weight),
-                             ("in_lBq", lw.in_lora_Bq), ("out_lBq", lw.out_lora_Bq)):
+            for field, t in F.items():
                 setattr(d, field, t.data_ptr())
         # the table (int8 + row scale, or fp16 as the exporter writes it) re-tiled for the head
         row_bytes = D if c.emb_code == EMB_I8 else 2 * D
