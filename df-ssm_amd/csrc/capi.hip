@@ -30,7 +30,7 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, ticket, err, launches, proj_t,
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, ticket, err, launches, gtick, proj_t,
       g_t, h_t, dt_t, total;
 };
 
@@ -50,11 +50,13 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.xf = off;       off = align_up(off + (size_t)r.B * r.D * 2);
   w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
+  w.hpart = off;    off = align_up(off + (r.B <= 4 ? (size_t)r.head_groups * (r.D / 512) * r.B * 64 * 8 : 0));
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
   // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by
   // dfssm_workspace_init together with the head's ticket and the error flag)
   w.launches = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
+  w.gtick = off;    off = align_up(off + (size_t)r.head_groups * 4);
   w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
   w.g_t = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
   w.h_t = off;      off = align_up(off + 2 * (size_t)r.B * 16 * 4);
@@ -413,6 +415,8 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
   a.ticket = (unsigned*)(ws + w.ticket);
   a.next = next; a.x_next = x_next;
+  a.hpart = (long long*)(ws + w.hpart);
+  a.gtick = (unsigned*)(ws + w.gtick);
   rc = hip_status(launch_head(a, r.B, as_stream(stream)));
   if (rc) return rc;
   return DFSSM_OK;

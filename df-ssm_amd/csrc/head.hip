@@ -178,6 +178,212 @@ __global__ void tile_emb_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Exact int8 head for 1..4 rows on the int8 matrix cores (int8 table). An fp16 value xf is
+// X 2^-24 with X an integer, |X| < 2^40, written as six signed base-256 digits d_b in [-128, 127]
+// (X = sum_b d_b 256^b); v_mfma_i32_16x16x64_i8 gives exact int32 sums S_b[v] = sum_k d_b[k] E[v][k],
+// and T = sum_b S_b 256^b (int64) = sum_k X_k E[v][k] exactly. The logit is fp16(fp32(T 2^-24) *
+// s_E[v]): the fp64 kernel's value whenever that one's sum is exact, and exact without condition.
+//
+// Work unit: 64 vocabulary rows (one tile group of the table) x a 512-wide k slice, i.e. 32 KiB of
+// table per workgroup and many short workgroups, which the dispatcher keeps balanced over the CUs
+// (a few long workgroups per CU left the last CUs streaming alone). Each workgroup computes the
+// final RMSNorm scale of its rows, the digits of its k slice, and 8 k steps of 64 with two MFMAs
+// each: B = the table (lane l: row 16 w + l % 16, tiled chunk 4 s + l / 16 of the slice), A = the
+// digit rows (lane l: row l % 16 of the tile, the same k block); tile 0 holds digits 0..3 of
+// sequence m at A-rows 4 m + b, tile 1 digits 4, 5 at A-rows 4 m, 4 m + 1, so lane group m = l / 16
+// ends with all six sums of (m, row l % 16) (the output layout is D[4 (l / 16) + e][l % 16]). The
+// slice's partial T goes out with write-through stores; the last of the group's slices to arrive
+// (per-group counter) adds them up, writes the logits and the group's (max, first index) pairs,
+// and the last group reduces those (the global ticket, as in the fp64 kernel).
+// ---------------------------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kHKS = 512;  // k slice per workgroup
+
+// fp16 value * 2^24 as an integer (exact for finite values).
+__device__ __forceinline__ long long fx24(uint16_t hb) {
+  const int e = (hb >> 10) & 31, mant = hb & 1023;
+  const long long X = e ? (long long)(1024 | mant) << (e - 1) : (long long)mant;
+  return (hb & 0x8000) ? -X : X;
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void head_i8_kernel(HeadArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t dg[M * 6][kHKS];  // digits of the slice
+  __shared__ double red[4][M];
+  __shared__ float pv[4][M];
+  __shared__ int pix[4][M];
+  __shared__ bool last_g, is_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int jg = lane >> 4, rl = lane & 15;
+  const int D = a.D, CH = D / 16, KP = D / kHKS;
+  const int NG = (int)gridDim.x / KP;
+  const int g = (int)blockIdx.x / KP, kp = (int)blockIdx.x % KP;
+
+  // loads: x for the sum of squares first (so that waiting for it does not wait for the table),
+  // then this slice's x and norm_f, then the 8 table chunks of this lane
+  constexpr int XR = 3;  // 8-element x chunks per thread and row: D <= 5120 = 3 * 2048 - 1024
+  u32x4 xv[M][XR];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+      const int k0 = 8 * tid + 2048 * i;
+      xv[m][i] = k0 < D ? *(const u32x4*)(a.x + (size_t)m * D + k0) : u32x4{0u, 0u, 0u, 0u};
+    }
+  const int ks = kp * kHKS + 2 * tid;  // this thread's two slice columns
+  uint32_t xs2[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xs2[m] = *(const uint32_t*)(a.x + (size_t)m * D + ks);
+  const float2 nf = *(const float2*)(a.norm_f + ks);
+  const u32x4* E = (const u32x4*)a.emb + ((size_t)g * CH + kp * (kHKS / 16) + jg) * 64 + 16 * wave + rl;
+  u32x4 buf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) buf[s] = ld_nt(E + (size_t)(4 * s) * 64);
+
+  // final RMSNorm scale of each row (fp64 sum of squares: exact)
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    double ps = 0.0;
+#pragma unroll
+    for (int i = 0; i < XR; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double v = (double)h2f((uint16_t)(xv[m][i][e >> 1] >> (16 * (e & 1))));
+        ps += v * v;
+      }
+    ps = wave_sum_dpp_f64(ps);
+    if (lane == 0) red[wave][m] = ps;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const double ss = red[0][m] + red[1][m] + red[2][m] + red[3][m];
+    const float r = 1.0f / sqrt_rn((float)ss * (1.0f / (float)D) + 1e-5f);
+    uint32_t pk[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      long long X = fx24(f2h(r16((h2f((uint16_t)(xs2[m] >> (16 * i))) * r) * (i ? nf.y : nf.x))));
+#pragma unroll
+      for (int b = 0; b < 5; ++b) {
+        const int d = (int)(int8_t)(X & 0xff);
+        X = (X - d) >> 8;
+        pk[b] |= (uint32_t)(d & 0xff) << (8 * i);
+      }
+      pk[5] |= (uint32_t)((int)X & 0xff) << (8 * i);
+    }
+#pragma unroll
+    for (int b = 0; b < 6; ++b) *(uint16_t*)&dg[m * 6 + b][2 * tid] = (uint16_t)pk[b];
+  }
+  __syncthreads();
+
+  // 8 k steps, two MFMAs each; rows without a digit read row 0 and are zeroed by a select
+  const int ma = rl >> 2, ba = rl & 3;
+  const bool a0ok = ma < M, a1ok = ma < M && ba < 2;
+  const int8_t* A0p = &dg[a0ok ? ma * 6 + ba : 0][16 * jg];
+  const int8_t* A1p = &dg[a1ok ? ma * 6 + 4 + ba : 0][16 * jg];
+  const i32x4 z4 = {0, 0, 0, 0};
+  i32x4 acc0 = z4, acc1 = z4;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const i32x4 Bv = __builtin_bit_cast(i32x4, buf[s]);
+    const i32x4 A0r = *(const i32x4*)(A0p + 64 * s);
+    const i32x4 A1r = *(const i32x4*)(A1p + 64 * s);
+    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0ok ? A0r : z4, Bv, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1ok ? A1r : z4, Bv, acc1, 0, 0, 0);
+  }
+  const int row = 16 * wave + rl;
+  if (jg < M) {
+    const long long T = (long long)acc0[0] + ((long long)acc0[1] << 8) + ((long long)acc0[2] << 16) +
+                        ((long long)acc0[3] << 24) + ((long long)acc1[0] << 32) + ((long long)acc1[1] << 40);
+    __hip_atomic_store(a.hpart + (((size_t)g * KP + kp) * M + jg) * 64 + row, T, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the partial has reached the device-coherent level
+  __syncthreads();
+  if (tid == 0) last_g = atomicAdd(a.gtick + g, 1u) == (unsigned)(KP - 1);
+  __syncthreads();
+  if (!last_g) return;
+
+  // last slice of group g: logits of its 64 rows, then the group's (max, first index) per row m
+  if (tid == 0) a.gtick[g] = 0u;
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+  const int v = g * 64 + row;
+  if (jg < M && v < a.V) {
+    long long T = 0;
+    for (int q = 0; q < KP; ++q)
+      T += __hip_atomic_load(a.hpart + (((size_t)g * KP + q) * M + jg) * 64 + row, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    const uint16_t lh = f2h((float)((double)T * 0x1p-24) * h2f(a.emb_scale[v]));
+    if (a.logits) a.logits[(size_t)jg * a.V + v] = lh;
+    best = h2f(lh);
+    bidx = v;
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) {  // within the 16 lanes of the row group
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bidx, o, 64);
+    if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+  }
+  if (rl == 0 && jg < M) {
+    pv[wave][jg] = best;
+    pix[wave][jg] = bidx;
+  }
+  __syncthreads();
+  if (tid < M) {
+    float b = pv[0][tid];
+    int bi = pix[0][tid];
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      if (pv[w][tid] > b || (pv[w][tid] == b && pix[w][tid] < bi)) { b = pv[w][tid]; bi = pix[w][tid]; }
+    __hip_atomic_store(a.part_val + (size_t)tid * NG + g, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.part_idx + (size_t)tid * NG + g, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(NG - 1);
+  __syncthreads();
+  if (!is_last) return;
+  __shared__ int next_tok[M];
+  if (wave < M) {
+    const int m = wave;
+    float b = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = lane; j < NG; j += 64) {
+      const float vv = __hip_atomic_load(a.part_val + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(b, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    if (lane == 0) {
+      if (bi < 0 || bi >= a.V) bi = 0;  // no comparable logit (all NaN): token 0
+      a.next[m] = (int64_t)bi;
+      next_tok[m] = bi;
+    }
+  }
+  if (tid == 0) *a.ticket = 0u;
+  __syncthreads();
+  if (a.x_next) {
+    for (int m = 0; m < M; ++m) {
+      const int t = next_tok[m];
+      for (int k = tid; k < D; k += 256) a.x_next[(size_t)m * D + k] = emb_value<false>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
+    }
+  }
+}
+
+template <int M>
+static hipError_t launch_head_i8(const HeadArgs& a, int groups, hipStream_t s) {
+  if (!a.hpart || !a.gtick || a.D % kHKS) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(head_i8_kernel<M>, dim3(groups * (a.D / kHKS)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int M, bool F16>
 static hipError_t launch_head_mf(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
   // dynamic LDS above 64 KiB needs an explicit opt-in (gfx950 has 160 KiB per workgroup)
@@ -189,7 +395,7 @@ static hipError_t launch_head_mf(const HeadArgs& a, int groups, size_t shm, hipS
 }
 template <int M>
 static hipError_t launch_head_m(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
-  return a.f16 ? launch_head_mf<M, true>(a, groups, shm, s) : launch_head_mf<M, false>(a, groups, shm, s);
+  return a.f16 ? launch_head_mf<M, true>(a, groups, shm, s) : launch_head_i8<M>(a, groups, s);
 }
 
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
