@@ -39,27 +39,63 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   const int K = a.K, CH = K / 128, M = a.M;
   const int QS = K + 16;  // padded LDS row stride
 
-  // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows ----
+  // ---- the first row block's q tile, issued before the bits (loads complete in issue order, so
+  // the tile does not wait for the weight stream from HBM) ----
+  constexpr int kQV = (MI == 2 ? 4096 : 5120) * MP / 16 / kGT;  // q vectors per thread, K at most
+  const int MB0 = M < MP ? M : MP;
+  u32x4 qv[kQV];
+#pragma unroll
+  for (int i = 0; i < kQV; ++i) {
+    const int v = tid + kGT * i, row = v / (K / 16), c16 = v % (K / 16);
+    qv[i] = (v < MP * (K / 16) && row < MB0) ? *(const u32x4*)(a.q + (size_t)row * a.ld_q + c16 * 16)
+                                            : u32x4{0u, 0u, 0u, 0u};
+  }
+  // its LoRA intermediates and activation scales: unconditional loads from clamped indices,
+  // selected when staged (using a loaded value waits for every load issued before it)
+  const int hi0 = tid < MB0 * DFSSM_LORA_R ? tid : MB0 * DFSSM_LORA_R - 1;
+  const int xi0 = tid < MB0 ? tid : MB0 - 1;
+  float hv0 = 0.0f, xsv0 = 0.0f;
+  uint16_t xsh0 = 0;
+  if (MODE != DFSSM_MODE_SCAFFOLD) {
+    hv0 = a.h[hi0];
+    xsv0 = a.xs[xi0];
+  } else if (a.xs16) {  // absent when only the accumulators are written
+    xsh0 = a.xs16[xi0];
+  }
+
+  // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows,
+  // kept raw until the epilogue ----
   const int r = rt * 16 + (lane & 15);
   u32x4 wb[kMaxSB];
 #pragma unroll
   for (int sb = 0; sb < kMaxSB; ++sb) {
     const int c = kq + 4 * j + 16 * sb;
-    wb[sb] = c < CH ? ld_nt((const u32x4*)a.bits + ((size_t)g * CH + c) * 64 + r) : u32x4{0u, 0u, 0u, 0u};
+    // chunks past CH re-read the last one; the MFMA loop zeroes their operands
+    wb[sb] = ld_nt((const u32x4*)a.bits + ((size_t)g * CH + (c < CH ? c : CH - 1)) * 64 + r);
+  }
+  {  // the first block's q tile into LDS (waits only for the loads issued before the bits)
+    const int nvq = MP * (K / 16);
+#pragma unroll
+    for (int i = 0; i < kQV; ++i) {
+      const int v = tid + kGT * i, row = v / (K / 16), c16 = v % (K / 16);
+      if (v < nvq) *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = qv[i];
+    }
+    if (tid < MP * DFSSM_LORA_R) hl[tid >> 4][tid & 15] = tid < MB0 * DFSSM_LORA_R ? hv0 : 0.0f;
+    if (tid < MP) xsl[tid] = tid < MB0 ? (MODE != DFSSM_MODE_SCAFFOLD ? xsv0 : h2f(xsh0)) : 0.0f;
   }
   const int n = g * 64 + r;
   const bool nrow = n < a.N;
   u32x4 la = {0u, 0u, 0u, 0u};
-  float e_ws = 0.0f, e_as = 0.0f;
+  uint16_t ws_raw = 0, as_raw = 0;
   uint32_t cw01 = 0, cw23 = 0;
   uint16_t cb = 0;
   const int ch = n - a.conv_lo;
   const bool conv_row = MODE == DFSSM_MODE_IN && nrow && ch >= 0 && ch < a.conv_c;
   if (nrow) {
-    if (a.wscale) e_ws = h2f(a.wscale[n]);
+    if (a.wscale) ws_raw = a.wscale[n];
     if (MODE != DFSSM_MODE_SCAFFOLD) {
       la = *(const u32x4*)(a.lA + (size_t)n * DFSSM_LORA_R);
-      e_as = h2f(a.lAs[n]);
+      as_raw = a.lAs[n];
     }
     if (conv_row) {
       const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
@@ -73,19 +109,23 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
     const int MB = M - m0 < MP ? M - m0 : MP;  // rows in this block
     // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
     __syncthreads();  // the previous block's partials (in qs) have been read
-    const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
-    for (int v = tid; v < nvq; v += kGT) {
-      const int row = v / (K / 16), c16 = v % (K / 16);
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
-      *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
+    if (m0 > 0) {  // the first block's tile was staged before the loop
+      const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
+      for (int v = tid; v < nvq; v += kGT) {
+        const int row = v / (K / 16), c16 = v % (K / 16);
+        u32x4 x = {0u, 0u, 0u, 0u};
+        if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
+        *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
+      }
     }
-    for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
-      const int m = i >> 4;
-      hl[m][i & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (i & 15)] : 0.0f;
-    }
-    if (tid < MP) {
-      xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
+    if (m0 > 0) {
+      for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
+        const int m = i >> 4;
+        hl[m][i & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (i & 15)] : 0.0f;
+      }
+      if (tid < MP) {
+        xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
+      }
     }
     __syncthreads();
     // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
@@ -141,7 +181,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       double aqd[DFSSM_LORA_R];
 #pragma unroll
       for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
-        aqd[rr] = (double)r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * e_as);
+        aqd[rr] = (double)r16((float)(int8_t)((la[rr >> 2] ^ zero) >> (8 * (rr & 3))) * h2f(as_raw ^ (uint16_t)zero));
 #pragma unroll
       for (int ib = 0; ib < MI; ++ib) {
         const int e = kq;
@@ -153,7 +193,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
         const int accv = 2 * T - Ssum[mb];
         if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
-        const float y = r16(r16(r16((float)accv) * xsl[mb]) * e_ws);
+        const float y = r16(r16(r16((float)accv) * xsl[mb]) * h2f(ws_raw ^ (uint16_t)zero));
         if (MODE == DFSSM_MODE_SCAFFOLD) {
           if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
           continue;
@@ -172,11 +212,12 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
             cs[1] = s2;
             cs[2] = xo;
             const float xv = h2f(xo);
-            float o = h2f(s0) * h2f((uint16_t)cw01);
-            o = o + h2f(s1) * h2f((uint16_t)(cw01 >> 16));
-            o = o + h2f(s2) * h2f((uint16_t)cw23);
-            o = o + xv * h2f((uint16_t)(cw23 >> 16));
-            o = o + h2f(cb);
+            const uint32_t c01 = cw01 ^ zero, c23 = cw23 ^ zero;
+            float o = h2f(s0) * h2f((uint16_t)c01);
+            o = o + h2f(s1) * h2f((uint16_t)(c01 >> 16));
+            o = o + h2f(s2) * h2f((uint16_t)c23);
+            o = o + xv * h2f((uint16_t)(c23 >> 16));
+            o = o + h2f(cb ^ (uint16_t)zero);
             const float sig = 1.0f / (1.0f + dev_expf(-o));
             out = o * sig;
           }
