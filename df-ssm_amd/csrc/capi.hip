@@ -313,9 +313,11 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
     p.lB = in ? Lw.in_lB : Lw.out_lB;
     p.lBs = in ? Lw.in_lB_s : Lw.out_lB_s;
     p.q_out = (int8_t*)(ws + w.q);
-    p.planes_out = (uint32_t*)(ws + w.planes);
     p.ld_q = kq;
-    p.s_out = (int*)(ws + w.qsum);
+    if (r.B <= 4) {  // the bit-plane GEMV reads planes and sum q; the matrix-core GEMM neither
+      p.planes_out = (uint32_t*)(ws + w.planes);
+      p.s_out = (int*)(ws + w.qsum);
+    }
     p.xs_out = (float*)(ws + w.xs);
     p.h_out = (float*)(ws + w.h);
     p.K = in ? r.D : r.DI;

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   for (int m0 = 0; m0 < M; m0 += MP) {
     const int MB = M - m0 < MP ? M - m0 : MP;  // rows in this block
     // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
-    __syncthreads();  // the previous block's partials (in qs) have been read
+    lds_barrier();  // the previous block's partials (in qs) have been read
     if (m0 > 0) {  // the first block's tile was staged before the loop
       const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
       for (int v = tid; v < nvq; v += kGT) {
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
     for (int row = wave; row < MP; row += kGT / 64) {
       int s = 0;
@@ -168,13 +168,13 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         }
       }
     }
-    __syncthreads();  // q tile no longer needed: reuse it for the partials
+    lds_barrier();  // q tile no longer needed: reuse it for the partials
     int* part = (int*)qs;  // [kq][rt][ib][e][lane]
 #pragma unroll
     for (int ib = 0; ib < MI; ++ib)
 #pragma unroll
       for (int e = 0; e < 4; ++e) part[(((kq * 4 + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
-    __syncthreads();
+    lds_barrier();
 
     // ---- epilogue: wave (rt, kq) finishes accumulator element e = kq of each tile ----
     if (nrow) {

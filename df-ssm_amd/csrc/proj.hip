@@ -51,7 +51,16 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
   const int K = a.K;
   const bool has_v = tid < K / 8;
   const uint16_t* act = a.act + (size_t)m * a.ld_act;
-  // loads first: the activation vector, norm weights, LoRA-B row r, the partials
+  // Loads first, in the order they are needed (loads complete in issue order, so waiting for one
+  // waits for all issued before it): the sum-of-squares partials (MODE_OUT), the activation
+  // vector, norm weights, LoRA-B row r and its scale. Raw values are converted where used.
+  double slot = 0.0;
+  if (MODE == DFSSM_MODE_OUT) {  // n_slots <= kPT (d_inner <= 16 * kPT); clamped, then selected
+    const int j = tid < a.n_slots ? tid : a.n_slots - 1;
+    slot = a.sumsq_slots[(size_t)m * a.n_slots + j];
+  }
+  // Threads past K/8 (whole waves: K is a multiple of 512) skip the vector work; the LoRA scale
+  // is loaded unconditionally, from a valid stand-in address when there is no LoRA.
   const u32x4 av = has_v ? *(const u32x4*)(act + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
   f32x4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = {0.f, 0.f, 0.f, 0.f};
   uint2 b8 = make_uint2(0u, 0u);
@@ -60,7 +69,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
     w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
     if (a.lB) b8 = *(const uint2*)(a.lB + (size_t)rr * K + 8 * tid);
   }
-  const float bs = a.lB ? h2f(a.lBs[rr]) : 0.0f;
+  const uint16_t bs_raw = *(a.lB ? a.lBs + rr : act);
   double part = 0.0;
   if (MODE == DFSSM_MODE_IN) {
     if (has_v) {
@@ -71,15 +80,17 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
       }
     }
   } else {
-    for (int j = tid; j < a.n_slots; j += kPT) part += a.sumsq_slots[(size_t)m * a.n_slots + j];
+    part = tid < a.n_slots ? slot : 0.0;
   }
   const double ss = block_sum_f64<kPT>(part, L.red_d);
   // xn into LDS, amax
   const float var = (float)ss * (1.0f / (float)K);
   const float r = 1.0f / sqrt_rn(var + 1e-5f);
   const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+  const float bs = a.lB ? h2f(bs_raw) : 0.0f;
   float mx = 0.0f;
   double hacc = 0.0;
+  u32x4 ov = {0u, 0u, 0u, 0u};
   if (has_v) {
     uint32_t o[4];
     const uint32_t bw[2] = {b8.x, b8.y};
@@ -95,20 +106,20 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
       hacc += (double)(x0 * b0);
       hacc += (double)(x1 * b1);
     }
-    const u32x4 ov = {o[0], o[1], o[2], o[3]};
+    ov = u32x4{o[0], o[1], o[2], o[3]};
     *(u32x4*)&L.xn[8 * tid] = ov;
-    if (a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = ov;
   }
-  if (a.lB) {
-    const double ht = block_sum_f64<kPT>(hacc, L.red_d);
-    if (tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + rr] = r16((float)ht);
-  }
+  // Global stores wait until the end: a wave with a store outstanding waits for its
+  // acknowledgement wherever the compiler needs a load complete (the counter is in order).
+  const double ht = a.lB ? block_sum_f64<kPT>(hacc, L.red_d) : 0.0;
   const float amax = block_max_f32<kPT>(mx, L.red_f);  // also publishes xn to the block
   const float xs = quant_scale(amax);
-  // q over all columns (for sum q); bytes and bit planes written for slice rr only
+  // q over all columns when sum q is wanted, else over slice rr only; bytes and bit planes are
+  // written for slice rr
   const int lo = rr * (K / 16), hi = lo + K / 16;
+  const bool want_sum = a.s_out != nullptr;
   int qsum = 0;
-  for (int k0 = (tid & ~63); k0 < K; k0 += kPT) {
+  for (int k0 = (tid & ~63) + (want_sum ? 0 : lo); k0 < (want_sum ? K : hi); k0 += kPT) {
     const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
     qsum += q;
     if (k0 >= lo && k0 < hi) {
@@ -118,8 +129,10 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
       if (a.planes_out) planes_store(a.planes_out + ((size_t)m * (a.ld_q / 32) + k0 / 32) * 8, pw);
     }
   }
+  if (has_v && a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = ov;
+  if (a.lB && tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + rr] = r16((float)ht);
   if (rr == 0) {
-    const int S = block_sum_i32<kPT>(qsum, L.red_i);
+    const int S = want_sum ? block_sum_i32<kPT>(qsum, L.red_i) : 0;
     if (tid == 0) {
       if (a.s_out) a.s_out[m] = S;
       if (a.xs_out) a.xs_out[m] = xs;
@@ -382,6 +395,10 @@ hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s) {
 }
 
 hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
+  // the kernel reads one sum-of-squares slot per thread and the LoRA scale with its table
+  if (mode == DFSSM_MODE_OUT && (!a.sumsq_slots || a.n_slots < 1 || a.n_slots > kPT)) return hipErrorInvalidValue;
+  if (a.lB && !a.lBs) return hipErrorInvalidValue;
+  if (a.K > kMaxK || a.K % 128) return hipErrorInvalidValue;
   if (mode == DFSSM_MODE_IN)
     hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(kPT), 0, s, a);
   else

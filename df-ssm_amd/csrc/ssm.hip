@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs a) {
     // lanes 0 and 32 of each wave hold their two rows' g^2; the others hold 0
     const double s = wave_sum_dpp_f64(gsqd);
     if (lane == 0) part[tid >> 6] = s;
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) a.sumsq_slots[(size_t)m * a.n_slots + blockIdx.x] = part[0] + part[1] + part[2] + part[3];
   }
 }
