@@ -30,8 +30,8 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, ticket, err, launches, gtick, proj_t,
-      g_t, h_t, dt_t, total;
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, ticket, err, launches, gtick,
+      proj_t, g_t, h_t, dt_t, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -51,6 +51,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.hpart = off;    off = align_up(off + (r.B <= 4 ? (size_t)r.head_groups * (r.D / 512) * r.B * 64 * 8 : 0));
+  w.hdig = off;     off = align_up(off + (r.B > 4 ? head_digit_bytes(r.B, r.D) : 0));  // batched int8 head
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
   // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by
@@ -399,7 +400,7 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   const Derived r = derive(&model->dims);
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
-  if (r.B > 4) {  // matrix-core head (fp32 accumulation)
+  if (r.B > 4) {  // matrix-core head: exact on the int8 table, fp32 accumulation on an fp16 table
     HeadArgs a{};
     a.x = x; a.norm_f = model->norm_f; a.emb = (const uint8_t*)model->emb; a.emb_scale = model->emb_scale;
     a.f16 = model->dims.emb_code == 0 ? 1 : 0;
@@ -408,6 +409,7 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
     a.ticket = (unsigned*)(ws + w.ticket);
     a.next = next; a.x_next = x_next;
     a.xf = (const uint16_t*)(ws + w.xf);
+    a.hdig = (const int8_t*)(ws + w.hdig);
     return hip_status(launch_head_batched(a, r.B, as_stream(stream)));
   }
   HeadArgs a{};

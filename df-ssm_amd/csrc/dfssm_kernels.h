@@ -123,6 +123,7 @@ struct HeadArgs {
   const uint16_t* xf;        // batched head: (M, D) scratch for the final-normed rows
   long long* hpart;          // int8 head at M <= 4: (groups, D / 512, M, 64) exact partial dot products
   unsigned* gtick;           // (groups) arrival counters, zero before the first launch, left zero
+  const int8_t* hdig;        // int8 head at M >= 5: digit planes, head_digit_bytes(M, D) bytes
 };
 
 struct EmbedArgs {
@@ -173,6 +174,7 @@ hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);
 hipError_t launch_conv(const ConvArgs& a, int M, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
+size_t head_digit_bytes(int M, int D);  // HeadArgs::hdig size for the batched int8 head
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
 hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int row_bytes, hipStream_t s);
 

@@ -427,6 +427,270 @@ hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int D, hipSt
 
 
 // ---------------------------------------------------------------------------------------------
+// Exact int8 head for 5..64 rows (int8 table): the digit decomposition of the 1..4-row kernel as
+// a tiled GEMM. head_digits_kernel computes the final RMSNorm of every row once and writes the
+// six base-256 digit planes of X = xf 2^24, tiled for the A operand: tile t = b NH + h holds
+// digit b of rows 16 h .. 16 h + 15, laid out [tile][16-byte k chunk][16 rows][16 bytes]
+// (NH = ceil(M / 16); rows M .. 16 NH - 1 and the chunks past D are zero).
+// head_i8b_kernel<NH, KP>: a workgroup of 2 NH KP waves owns two table groups (128 vocabulary
+// rows). Wave w takes k part w / (2 NH) (the k steps are split in KP parts so that more waves
+// keep loads in flight; part 0 adds the others' exact partials from LDS), row block h and table
+// group from w % (2 NH) = 2 h + group. Per 64-wide k step a lane loads its 16 bytes of the 6
+// digit tiles of h (A: row l % 16, k block l / 16) and of the group's 4 fragments of 16 rows (B:
+// row 16 f + l % 16, same k block); the loads of the next two steps are in flight during a
+// step's 24 MFMAs. The accumulator layout D[4 (l / 16) + e][l % 16] leaves lane l with all six
+// digit sums S_b of (m = 16 h + 4 (l / 16) + e, v = 64 g + 16 f + l % 16) in its own registers:
+// T = sum_b S_b 256^b (int64) = sum_k X_k E[v][k] exactly, the logit fp16(fp32(T 2^-24) *
+// s_E[v]) as in the 1..4-row kernel. The table streams from HBM once; the digit planes
+// (6 * 16 NH * D bytes) stay in L2. Argmax: per-workgroup (max, first index) pairs written
+// through to the coherent level, the last workgroup (arrival ticket) reduces them and writes the
+// next tokens and their embedding.
+// ---------------------------------------------------------------------------------------------
+// 16-byte k chunks per digit-plane row: D / 16 rounded up to whole groups of three 64-wide k steps
+// (the three-stage ring runs without a tail; the padding is zero)
+__host__ __device__ inline int digit_chunks(int D) { return (D / 64 + 2) / 3 * 3 * 4; }
+size_t head_digit_bytes(int M, int D) { return (size_t)6 * 16 * ((M + 15) / 16) * digit_chunks(D) * 16; }
+
+__global__ __launch_bounds__(256) void head_digits_kernel(const uint16_t* __restrict__ x,
+                                                         const float* __restrict__ norm_f,
+                                                         int8_t* __restrict__ dig, int M, int NH, int D) {
+  __shared__ double red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;  // grid: 16 NH rows
+  const int CH = D / 16, h = m >> 4, rr = m & 15;
+  const int CHp = digit_chunks(D);  // the planes are zero past column D
+  const uint16_t* xm = x + (size_t)(m < M ? m : 0) * D;
+  float r = 0.0f;
+  if (m < M) {  // uniform over the workgroup
+    double ps = 0.0;
+    for (int k = 8 * tid; k < D; k += 8 * 256) {
+      const u32x4 xv = *(const u32x4*)(xm + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double v = (double)h2f((uint16_t)(xv[e >> 1] >> (16 * (e & 1))));
+        ps += v * v;
+      }
+    }
+    const double ss = block_sum_f64<256>(ps, red);
+    r = 1.0f / sqrt_rn((float)ss * (1.0f / (float)D) + 1e-5f);
+  }
+  for (int c = tid; c < CHp; c += 256) {  // one 16-column chunk per thread
+    uint32_t pk[6][4];
+#pragma unroll
+    for (int b = 0; b < 6; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pk[b][j] = 0u;
+    if (m < M && c < CH) {
+      const u32x4 x0 = *(const u32x4*)(xm + 16 * c), x1 = *(const u32x4*)(xm + 16 * c + 8);
+      const f32x4* nfp = (const f32x4*)(norm_f + 16 * c);
+      const f32x4 n4[4] = {nfp[0], nfp[1], nfp[2], nfp[3]};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = i < 8 ? x0[i >> 1] : x1[(i - 8) >> 1];
+        const float xv = h2f((uint16_t)(w >> (16 * (i & 1))));
+        long long X = fx24(f2h(r16((xv * r) * n4[i >> 2][i & 3])));
+#pragma unroll
+        for (int b = 0; b < 5; ++b) {
+          const int d = (int)(int8_t)(X & 0xff);
+          X = (X - d) >> 8;
+          pk[b][i >> 2] |= (uint32_t)(d & 0xff) << (8 * (i & 3));
+        }
+        pk[5][i >> 2] |= (uint32_t)((int)X & 0xff) << (8 * (i & 3));
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 6; ++b)
+      *(u32x4*)(dig + (((size_t)(b * NH + h) * CHp + c) * 16 + rr) * 16) = u32x4{pk[b][0], pk[b][1], pk[b][2], pk[b][3]};
+  }
+}
+
+// (at most 256 registers per lane: with more, the accumulators move through AGPR copies)
+// KP: k parts (waves) per (row block, table group); 128 NH KP <= 512 threads keeps 2 waves per SIMD
+template <int NH, int KP>
+__global__ __launch_bounds__(128 * NH * KP) __attribute__((amdgpu_waves_per_eu(2))) void head_i8b_kernel(HeadArgs a, int M) {
+  constexpr int MP = 16 * NH, NWP = 2 * NH;  // waves per k part
+  __shared__ long long tpart[KP > 1 ? KP - 1 : 1][NWP][16][64];
+  __shared__ float wbest[2][MP];
+  __shared__ int widx[2][MP];
+  __shared__ bool is_last;
+  __shared__ int next_tok[MP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: operand bases in SGPRs
+  const int kp = wave / NWP, wl = wave % NWP;
+  const int h = wl >> 1, vh = wl & 1, jg = lane >> 4, rl = lane & 15;
+  const int D = a.D, CH = D / 16, KS = D / 64;
+  const int ngrp = (a.V + 63) / 64;
+  const int g = 2 * (int)blockIdx.x + vh;
+  const bool gok = g < ngrp;           // wave-uniform; a wave past the table computes on group
+  const int gc = gok ? g : ngrp - 1;   // ngrp - 1 (in bounds) and discards the result
+  // row scales of this lane's 4 vocabulary rows: loaded first, used at the end
+  uint16_t sc[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int v = gc * 64 + 16 * f + rl;
+    sc[f] = a.emb_scale[v < a.V ? v : a.V - 1];
+  }
+  // operand addresses: a workgroup-uniform base plus a 32-bit lane offset (scalar-base loads)
+  const char* Eb = (const char*)a.emb + (size_t)gc * CH * 1024;   // table group gc
+  const int CHp = digit_chunks(D), KSp = CHp / 4;                 // k steps incl. zero padding
+  const char* Ab = (const char*)a.hdig + (size_t)h * CHp * 256;   // row block h of digit plane 0
+  const uint32_t eo = (uint32_t)(jg * 64 + rl) * 16;              // + 1024 (4 s) + 256 f
+  const uint32_t ao = (uint32_t)(jg * 16 + rl) * 16;              // + b * plane + 256 (4 s)
+  const uint32_t plane = (uint32_t)NH * CHp * 256;                // one digit plane, bytes
+  i32x4 acc[6][4];
+#pragma unroll
+  for (int b = 0; b < 6; ++b)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[b][f] = i32x4{0, 0, 0, 0};
+  // three-stage ring: the loads of steps s + 1 and s + 2 are in flight during step s's MFMAs
+  // (loads complete in issue order, so a step's operands are waited for with 20 loads pending)
+  u32x4 A[3][6], Bf[3][4];
+  auto load = [&](int st, int step) {
+    // steps KS .. KSp - 1 multiply zero digits with a re-read of the last table step; loads past
+    // KSp (the ring's last two) re-read step KSp - 1 and are not used
+    const uint32_t oa = (uint32_t)(4 * (step < KSp ? step : KSp - 1));
+    const uint32_t oe = (uint32_t)(4 * (step < KS ? step : KS - 1));
+#pragma unroll
+    for (int b = 0; b < 6; ++b) A[st][b] = *(const u32x4*)(Ab + (ao + b * plane + oa * 256));
+#pragma unroll
+    for (int f = 0; f < 4; ++f) Bf[st][f] = ld_nt((const u32x4*)(Eb + (eo + oe * 1024 + 256 * f)));
+  };
+  auto mma = [&](int st) {
+#pragma unroll
+    for (int b = 0; b < 6; ++b)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        acc[b][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, A[st][b]),
+                                                          __builtin_bit_cast(i32x4, Bf[st][f]), acc[b][f], 0, 0, 0);
+  };
+  // this wave's k part: whole groups of three steps, the last part the shortest
+  const int Q = (KSp / 3 + KP - 1) / KP * 3;
+  const int s0 = kp * Q < KSp ? kp * Q : KSp, s1 = s0 + Q < KSp ? s0 + Q : KSp;
+  load(0, s0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(1, s0 + 1);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int s = s0; s < s1; s += 3) {
+    // sched_barrier keeps each step's loads ahead of the previous step's MFMAs (the scheduler
+    // would otherwise sink them to their uses and expose the load latency at every step)
+    load(2, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    load(0, s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1);
+    load(1, s + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(2);
+  }
+
+  // exact partial dot products of this k part; parts 1.. hand theirs to part 0 through LDS
+  long long T[4][4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      long long t = 0;
+#pragma unroll
+      for (int b = 0; b < 6; ++b) t += (long long)acc[b][f][e] << (8 * b);
+      T[f][e] = t;
+    }
+  if (kp > 0) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tpart[kp - 1][wl][4 * f + e][lane] = T[f][e];
+  }
+  lds_barrier();
+  if (kp == 0) {
+#pragma unroll
+    for (int q = 0; q < KP - 1; ++q)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) T[f][e] += tpart[q][wl][4 * f + e][lane];
+  }
+
+  // logits (part 0) and the best of this lane per row e (vocabulary rows increase with f)
+  float best[4];
+  int bidx[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { best[e] = -INFINITY; bidx[e] = 0x7fffffff; }
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int v = g * 64 + 16 * f + rl;
+    const float sv = h2f(sc[f]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * h + 4 * jg + e;
+      const long long T_ = T[f][e];
+      if (kp == 0 && gok && m < M && v < a.V) {
+        const uint16_t lh = f2h((float)((double)T_ * 0x1p-24) * sv);
+        if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
+        const float lv = h2f(lh);
+        if (lv > best[e]) { best[e] = lv; bidx[e] = v; }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float b = best[e];
+    int bi = bidx[e];
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {  // the 16 lanes of row group jg
+      const float ob = __shfl_xor(b, o, 16);
+      const int oi = __shfl_xor(bi, o, 16);
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    if (kp == 0 && rl == 0) {
+      wbest[vh][16 * h + 4 * jg + e] = b;
+      widx[vh][16 * h + 4 * jg + e] = bi;
+    }
+  }
+  __syncthreads();
+  const int NGW = (int)gridDim.x;
+  if (tid < M) {
+    float b = wbest[0][tid];
+    int bi = widx[0][tid];
+    if (wbest[1][tid] > b || (wbest[1][tid] == b && widx[1][tid] < bi)) { b = wbest[1][tid]; bi = widx[1][tid]; }
+    __hip_atomic_store(a.part_val + (size_t)tid * NGW + blockIdx.x, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.part_idx + (size_t)tid * NGW + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the pairs have reached the device-coherent level
+  __syncthreads();
+  if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(NGW - 1);
+  __syncthreads();
+  if (!is_last) return;
+  for (int m = wave; m < M; m += NWP * KP) {
+    float b = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = lane; j < NGW; j += 64) {
+      const float vv = __hip_atomic_load(a.part_val + (size_t)m * NGW + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * NGW + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(b, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    if (lane == 0) {
+      if (bi < 0 || bi >= a.V) bi = 0;  // no comparable logit (all NaN): token 0
+      a.next[m] = (int64_t)bi;
+      next_tok[m] = bi;
+    }
+  }
+  if (tid == 0) *a.ticket = 0u;
+  __syncthreads();
+  if (a.x_next) {
+    for (int m = 0; m < M; ++m) {
+      const int t = next_tok[m];
+      for (int k = tid; k < D; k += 128 * NH * KP) a.x_next[(size_t)m * D + k] = emb_value<false>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Batched head (M = 5..64): logits on the fp16 matrix cores, v_mfma_f32_16x16x32_f16. A = xf
 // (fp16, 16 rows x 32 k), B = 16 vocabulary rows of the int8 table converted exactly to fp16 in
 // registers. Products are exact; the sum is accumulated in fp32 (not exact -- the 1..4-row kernel
@@ -612,7 +876,23 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
 }
 
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s) {
-  if (M < 1 || M > 64 || a.D % kHK || !a.xf) return hipErrorInvalidValue;
+  if (M < 1 || M > 64 || a.D % kHK) return hipErrorInvalidValue;
+  if (!a.f16) {  // int8 table: exact digit-plane GEMM
+    if (!a.hdig) return hipErrorInvalidValue;
+    const int nh = (M + 15) / 16;
+    hipLaunchKernelGGL(head_digits_kernel, dim3(16 * nh), dim3(256), 0, s, a.x, a.norm_f, (int8_t*)a.hdig, M, nh, a.D);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int grid = ((a.V + 63) / 64 + 1) / 2;
+    switch (nh) {
+      case 1: hipLaunchKernelGGL((head_i8b_kernel<1, 4>), dim3(grid), dim3(512), 0, s, a, M); break;
+      case 2: hipLaunchKernelGGL((head_i8b_kernel<2, 2>), dim3(grid), dim3(512), 0, s, a, M); break;
+      case 3: hipLaunchKernelGGL((head_i8b_kernel<3, 1>), dim3(grid), dim3(384), 0, s, a, M); break;
+      default: hipLaunchKernelGGL((head_i8b_kernel<4, 1>), dim3(grid), dim3(512), 0, s, a, M); break;
+    }
+    return hipGetLastError();
+  }
+  if (!a.xf) return hipErrorInvalidValue;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(256), 0, s, a.x, a.norm_f, (uint16_t*)a.xf, a.D);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

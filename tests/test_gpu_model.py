@@ -1,7 +1,8 @@
 """End-to-end GPU decode parity against the oracle on seeded random-init models.
 
-Per step: fp16 logits within 2e-2 absolute, identical greedy tokens; after the run the fp32 SSM
-state within 1e-3 max relative error and the conv state close. The north-star tolerances.
+Per step: fp16 logits identical to the oracle's on the int8 table (the north star allows 2e-2
+absolute), identical greedy tokens; after the run the fp32 SSM state within 1e-3 max relative
+error and the conv state close.
 """
 import numpy as np
 import pytest
@@ -43,9 +44,7 @@ def test_tiny_forward_stepwise(tiny_weights, B):
         logits_o, nxt = orc.step(tok)
         err = np.abs(logits_g - logits_o.astype(np.float32)).max()
         worst = max(worst, err)
-        if B <= 4:  # the exact int8 head: identical logits
-            assert err == 0.0, f"step {t}: logits differ by {err}"
-        assert err <= 2e-2, f"step {t}: logits max abs err {err}"
+        assert err == 0.0, f"step {t}: logits differ by {err}"  # the exact int8 head, every batch
         g_next = logits_g.argmax(axis=1)
         np.testing.assert_array_equal(g_next, nxt)
         tok = prompts[:, t + 1] if t + 1 < prompts.shape[1] else nxt
@@ -90,8 +89,8 @@ def w13():
 
 @pytest.mark.parametrize("B,T,n", [(1, 32, 128), (4, 8, 8), (8, 4, 4)])
 def test_1p3b_greedy(w13, B, T, n):
-    """Config 3 at batch 1 (32-token seeded prompt, 128 generated) and a short batch-4 run:
-    identical greedy tokens, state within 1e-3 after the run, final logits within 2e-2."""
+    """Config 3 at batch 1 (32-token seeded prompt, 128 generated) and short batch-4 and batch-8
+    runs: identical greedy tokens, state within 1e-3 after the run, identical final logits."""
     w = w13
     print(f"1.3B B={B} T={T} n={n}", flush=True)
     prompts = make_prompts(B, w.cfg.vocab_size, T)
@@ -107,7 +106,7 @@ def test_1p3b_greedy(w13, B, T, n):
     err = np.abs(lg - lo.astype(np.float32)).max()
     print(f"1.3B B={B}: state rel err {rel:.3e}, final logits max abs err {err:.3e}")
     assert rel <= 1e-3
-    assert err <= 2e-2
+    assert err == 0.0
     assert gpu.error_flag() == 0
 
 
@@ -171,7 +170,7 @@ def test_tiny_fp16_embedding(tiny_weights_f16, B):
 def test_2p7b_layer_shapes_batch64():
     """Config 4's layer shapes (d_model 2560, d_inner 5120, 80 heads, in_proj 10576) at batch 64 on
     the matrix-core path, 4 layers and a 4096-token vocabulary so that the oracle stays fast:
-    logits within 2e-2, identical greedy tokens, state within 1e-3 relative."""
+    identical logits and greedy tokens, state within 1e-3 relative."""
     from dfssm.format import DFSSMConfig
     c = DFSSMConfig(n_layer=4, d_model=2560, d_inner=5120, d_state=128, nheads=80, headdim=64, ngroups=1,
                     vocab_size=4096, kw=4)
@@ -187,5 +186,5 @@ def test_2p7b_layer_shapes_batch64():
     assert _state_rel(gpu, orc) <= 1e-3
     lg = _np16(gpu.forward(torch.from_numpy(ref[:, -1]).to(DEV))).astype(np.float32)
     lo, _ = orc.step(ref[:, -1])
-    assert np.abs(lg - lo.astype(np.float32)).max() <= 2e-2
+    assert np.abs(lg - lo.astype(np.float32)).max() == 0.0
     assert gpu.error_flag() == 0
