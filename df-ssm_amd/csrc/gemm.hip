@@ -41,14 +41,22 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 
   // ---- the first row block's q tile, issued before the bits (loads complete in issue order, so
   // the tile does not wait for the weight stream from HBM) ----
-  constexpr int kQV = (MI == 2 ? 4096 : 5120) * MP / 16 / kGT;  // q vectors per thread, K at most
+  // Wave w copies rows w + 16 jr, lane l the 16-byte vectors l + 64 i of a row: no index division,
+  // row addresses are scalar. Loads are unconditional from clamped indices (a load inside a branch
+  // makes the compiler wait for all loads where the paths join); staging selects.
+  constexpr int kQI = (MI == 2 ? 4096 : 5120) / 16 / 64;  // vectors per lane and row, K at most
   const int MB0 = M < MP ? M : MP;
-  u32x4 qv[kQV];
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  u32x4 qv[MI][kQI];
 #pragma unroll
-  for (int i = 0; i < kQV; ++i) {
-    const int v = tid + kGT * i, row = v / (K / 16), c16 = v % (K / 16);
-    qv[i] = (v < MP * (K / 16) && row < MB0) ? *(const u32x4*)(a.q + (size_t)row * a.ld_q + c16 * 16)
-                                            : u32x4{0u, 0u, 0u, 0u};
+  for (int jr = 0; jr < MI; ++jr) {
+    const int row = wv + 16 * jr;
+    const int8_t* qrow = a.q + (size_t)(row < MB0 ? row : MB0 - 1) * a.ld_q;
+#pragma unroll
+    for (int i = 0; i < kQI; ++i) {
+      const int c16 = lane + 64 * i;  // lanes past the row load nothing (exec-masked)
+      qv[jr][i] = c16 < K / 16 ? *(const u32x4*)(qrow + c16 * 16) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
   // its LoRA intermediates and activation scales: unconditional loads from clamped indices,
   // selected when staged (using a loaded value waits for every load issued before it)
@@ -74,11 +82,14 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
     wb[sb] = ld_nt((const u32x4*)a.bits + ((size_t)g * CH + (c < CH ? c : CH - 1)) * 64 + r);
   }
   {  // the first block's q tile into LDS (waits only for the loads issued before the bits)
-    const int nvq = MP * (K / 16);
 #pragma unroll
-    for (int i = 0; i < kQV; ++i) {
-      const int v = tid + kGT * i, row = v / (K / 16), c16 = v % (K / 16);
-      if (v < nvq) *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = qv[i];
+    for (int jr = 0; jr < MI; ++jr) {
+      const int row = wv + 16 * jr;
+#pragma unroll
+      for (int i = 0; i < kQI; ++i) {
+        const int c16 = lane + 64 * i;
+        if (c16 < K / 16) *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = row < MB0 ? qv[jr][i] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
     if (tid < MP * DFSSM_LORA_R) hl[tid >> 4][tid & 15] = tid < MB0 * DFSSM_LORA_R ? hv0 : 0.0f;
     if (tid < MP) xsl[tid] = tid < MB0 ? (MODE != DFSSM_MODE_SCAFFOLD ? xsv0 : h2f(xsh0)) : 0.0f;
@@ -110,12 +121,13 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
     // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
     lds_barrier();  // the previous block's partials (in qs) have been read
     if (m0 > 0) {  // the first block's tile was staged before the loop
-      const int nvq = MP * (K / 16);  // 16-byte vectors of the q tile
-      for (int v = tid; v < nvq; v += kGT) {
-        const int row = v / (K / 16), c16 = v % (K / 16);
-        u32x4 x = {0u, 0u, 0u, 0u};
-        if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
-        *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
+      for (int jr = 0; jr < MI; ++jr) {
+        const int row = wv + 16 * jr;
+        for (int c16 = lane; c16 < K / 16; c16 += 64) {
+          u32x4 x = {0u, 0u, 0u, 0u};
+          if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
+          *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
+        }
       }
     }
     if (m0 > 0) {

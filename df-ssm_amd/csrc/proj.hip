@@ -114,15 +114,18 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
   const double ht = a.lB ? block_sum_f64<kPT>(hacc, L.red_d) : 0.0;
   const float amax = block_max_f32<kPT>(mx, L.red_f);  // also publishes xn to the block
   const float xs = quant_scale(amax);
-  // q over all columns when sum q is wanted, else over slice rr only; bytes and bit planes are
-  // written for slice rr
+  // q over all columns when sum q is wanted, else only where written: the bytes and bit planes
+  // of the 64-column wave blocks that start in slice rr (slices narrower than 64 columns, K < 1024,
+  // leave every other workgroup nothing to write)
   const int lo = rr * (K / 16), hi = lo + K / 16;
   const bool want_sum = a.s_out != nullptr;
   int qsum = 0;
-  for (int k0 = (tid & ~63) + (want_sum ? 0 : lo); k0 < (want_sum ? K : hi); k0 += kPT) {
+  for (int k0 = (tid & ~63); k0 < K; k0 += kPT) {
+    const bool mine = k0 >= lo && k0 < hi;  // wave-uniform
+    if (!want_sum && !mine) continue;
     const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
     qsum += q;
-    if (k0 >= lo && k0 < hi) {
+    if (mine) {
       if (a.q_out) a.q_out[(size_t)m * a.ld_q + k0 + lane] = (int8_t)q;
       uint32_t pw[16];
       planes64(q, pw);
