@@ -1,10 +1,14 @@
 // Batched scaffold projection (M = 5..64 activation rows) on the int8 matrix cores (gfx950).
 //
-// T[m][n] = sum_k q[m][k] * bit[n][k] is computed with v_mfma_i32_16x16x64_i8: A = q (16 rows x
-// 64 k, int8), B = the sign bits of 16 output rows expanded in registers to 0/1 bytes, and
-// acc = 2 T - sum_k q[m][k] (exact int32; acc = sum_k q * (2 bit - 1)). Expansion of a nibble to
-// four 0/1 bytes is one multiply and one mask: (nib * 0x00204081) & 0x01010101 -- the four
-// shifted copies of the nibble occupy disjoint bit ranges, so the product has no carries.
+// acc[m][n] = sum_k q[m][k] * (2 bit[n][k] - 1) (exact int32) is computed with
+// v_mfma_i32_16x16x64_i8: A = q (16 rows x 64 k, int8), B = the sign bits of 16 output rows
+// expanded in registers to bytes. Expansion of a nibble to four 0/1 bytes is one multiply and one
+// mask: (nib * 0x00204081) & 0x01010101 -- the four shifted copies of the nibble occupy disjoint
+// bit ranges, so the product has no carries. With 32-row blocks (MI = 2) ~(x * 0xfe) then turns
+// each 0/1 byte into -1/+1 (each byte product is at most 0xfe: again no carries) and the MFMA
+// sums are acc itself; with 16-row blocks (MI = 1: K > 4096 or M <= 16, where the expansion is
+// redone for up to four blocks) B stays 0/1 and acc = 2 T - sum_k q[m][k], the row sums taken
+// from the q tile in LDS.
 //
 // One workgroup (1024 threads = 16 waves) owns a group of 64 output rows; it keeps their bits in
 // registers and walks the activation rows in blocks of 32 (16 when K > 4096). Wave w = (row tile rt = w % 4, k slot kq = w / 4).
@@ -140,20 +144,21 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       }
     }
     lds_barrier();
-    // sum q per row: wave w sums rows w, w + 16 (exact integer reduction)
-    for (int row = wave; row < MP; row += kGT / 64) {
-      int s = 0;
-      for (int c16 = lane; c16 < K / 16; c16 += 64) {
-        const u32x4 x = *(const u32x4*)(qs + (size_t)row * QS + c16 * 16);
+    if (MI == 1) {  // sum q per row: wave w sums row w (exact integer reduction)
+      for (int row = wave; row < MP; row += kGT / 64) {
+        int sq = 0;
+        for (int c16 = lane; c16 < K / 16; c16 += 64) {
+          const u32x4 x = *(const u32x4*)(qs + (size_t)row * QS + c16 * 16);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s += (int)(int8_t)(x[e >> 2] >> (8 * (e & 3)));
+          for (int e = 0; e < 16; ++e) sq += (int)(int8_t)(x[e >> 2] >> (8 * (e & 3)));
+        }
+        sq = wave_sum_dpp_i32(sq);
+        if (lane == 0) Ssum[row] = sq;
       }
-      s = wave_sum_dpp_i32(s);
-      if (lane == 0) Ssum[row] = s;
     }
 
     // ---- MFMA over this wave's chunks ----
-    // The 0/1 byte expansion of the bits does not change between row blocks; a volatile zero from
+    // The byte expansion of the bits does not change between row blocks; a volatile zero from
     // LDS keeps the compiler from hoisting all 24 expanded operands (96 registers) out of the loop.
     const uint32_t zero = *(volatile uint32_t*)&zero_s;
     v4i acc[MI];
@@ -167,10 +172,14 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const uint32_t w = wb[sb][s >> 1] ^ zero;
-          const uint32_t b16 = valid ? ((s & 1) ? (w >> 16) : (w & 0xffffu)) : 0u;
+          const uint32_t b16 = (s & 1) ? (w >> 16) : (w & 0xffffu);
           v4i B;
 #pragma unroll
-          for (int nib = 0; nib < 4; ++nib) B[nib] = (int)((((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u);
+          for (int nib = 0; nib < 4; ++nib) {
+            // four 0/1 bytes; for MI = 2 +-1 bytes: ~(x * 0xfe) maps byte 1 -> 0x01, 0 -> 0xff
+            const uint32_t x = (((b16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u;
+            B[nib] = valid ? (int)(MI == 2 ? ~(x * 0xfeu) : x) : 0;
+          }
           const int k = valid ? 128 * c + 16 * s : 0;
 #pragma unroll
           for (int ib = 0; ib < MI; ++ib) {
@@ -203,7 +212,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         int T = 0;
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
-        const int accv = 2 * T - Ssum[mb];
+        const int accv = MI == 2 ? T : 2 * T - Ssum[mb];
         if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
         const float y = r16(r16(r16((float)accv) * xsl[mb]) * h2f(ws_raw ^ (uint16_t)zero));
         if (MODE == DFSSM_MODE_SCAFFOLD) {
