@@ -23,7 +23,7 @@ namespace dfssm {
 constexpr int kMaxK = 5120;          // largest d_model / d_inner supported
 
 // ------------------------------------------------------------------------------------------
-// prep_kernel: the per-projection prologue, computed once per sequence (16 workgroups of 1024
+// prep_kernel: the per-projection prologue, computed once per sequence (16 workgroups of K/8
 // threads per activation row m):
 //   MODE_IN : xn = fp16((x * r) * ln_w), r = 1/sqrt(sum(x^2)/K + 1e-5)  (df_ssm_inference.py:141-145)
 //   MODE_OUT: the same on the gated g with sum(g^2) from the SSM kernel's per-block partials
@@ -31,7 +31,7 @@ constexpr int kMaxK = 5120;          // largest d_model / d_inner supported
 //   planes[m][word][b] = bit b of q for the 32 columns of `word`; S = sum q
 //   h[m][r] = fp16(sum_k xn_k * fp16(B_i8[r,k] * B_s[r]))                   (:83,173,204)
 // ------------------------------------------------------------------------------------------
-constexpr int kPT = 1024;
+constexpr int kPT = 1024;       // threads per workgroup at most (K / 8 for K <= 5120)
 constexpr int kPW = kPT / 64;
 
 struct PrepLds {
@@ -41,58 +41,54 @@ struct PrepLds {
   int red_i[kPW];
 };
 
-// Grid (16, M): workgroup (r, m) recomputes the normalization and quantization of row m (K
-// elements, a few per thread), writes the q bytes and bit planes of column slice r (K/16 columns),
-// and the LoRA intermediate h[m][r]; workgroup (0, m) also writes sum q and the scale.
+// Grid (16, M) x K/8 threads (8 columns each; K is a multiple of 512, so whole waves): workgroup
+// (r, m) recomputes the normalization and quantization of row m, writes the q bytes (and for the
+// bit-plane GEMV the planes) of column slice r (K/16 columns) and the LoRA intermediate h[m][r];
+// workgroup (0, m) also writes sum q (when asked) and the scale. Three LDS reductions: the sum of
+// squares, then the LoRA sum and the maximum together, then (workgroup 0, when asked) sum q.
 template <int MODE>
 __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
   __shared__ PrepLds L;
-  const int rr = blockIdx.x, m = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  const int K = a.K;
-  const bool has_v = tid < K / 8;
+  const int rr = blockIdx.x, m = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int K = a.K, NT = (int)blockDim.x, nw = NT >> 6;
   const uint16_t* act = a.act + (size_t)m * a.ld_act;
   // Loads first, in the order they are needed (loads complete in issue order, so waiting for one
-  // waits for all issued before it): the sum-of-squares partials (MODE_OUT), the activation
-  // vector, norm weights, LoRA-B row r and its scale. Raw values are converted where used.
+  // waits for all issued before it): the sum-of-squares partials (MODE_OUT, n_slots < K / 8), the
+  // activation vector, norm weights, LoRA-B row r and its scale (from a valid stand-in address
+  // when there is no LoRA). Raw values are converted where used.
   double slot = 0.0;
-  if (MODE == DFSSM_MODE_OUT) {  // n_slots <= kPT (d_inner <= 16 * kPT); clamped, then selected
-    const int j = tid < a.n_slots ? tid : a.n_slots - 1;
-    slot = a.sumsq_slots[(size_t)m * a.n_slots + j];
-  }
-  // Threads past K/8 (whole waves: K is a multiple of 512) skip the vector work; the LoRA scale
-  // is loaded unconditionally, from a valid stand-in address when there is no LoRA.
-  const u32x4 av = has_v ? *(const u32x4*)(act + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
-  f32x4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = {0.f, 0.f, 0.f, 0.f};
-  uint2 b8 = make_uint2(0u, 0u);
-  if (has_v) {
-    w0 = *(const f32x4*)(a.norm_w + 8 * tid);
-    w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
-    if (a.lB) b8 = *(const uint2*)(a.lB + (size_t)rr * K + 8 * tid);
-  }
+  if (MODE == DFSSM_MODE_OUT) slot = a.sumsq_slots[(size_t)m * a.n_slots + (tid < a.n_slots ? tid : a.n_slots - 1)];
+  const u32x4 av = *(const u32x4*)(act + 8 * tid);
+  const f32x4 w0 = *(const f32x4*)(a.norm_w + 8 * tid);
+  const f32x4 w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
+  const uint2 b8 = *(const uint2*)((a.lB ? a.lB + (size_t)rr * K : (const int8_t*)act) + 8 * tid);
   const uint16_t bs_raw = *(a.lB ? a.lBs + rr : act);
   double part = 0.0;
   if (MODE == DFSSM_MODE_IN) {
-    if (has_v) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const double xv = (double)h2f((uint16_t)(av[e >> 1] >> (16 * (e & 1))));
-        part += xv * xv;
-      }
+    for (int e = 0; e < 8; ++e) {
+      const double xv = (double)h2f((uint16_t)(av[e >> 1] >> (16 * (e & 1))));
+      part += xv * xv;
     }
   } else {
     part = tid < a.n_slots ? slot : 0.0;
   }
-  const double ss = block_sum_f64<kPT>(part, L.red_d);
-  // xn into LDS, amax
+  {  // sum of squares (fp64: the sums are exact)
+    const double pw = wave_sum_dpp_f64(part);
+    if (lane == 0) L.red_d[w] = pw;
+  }
+  lds_barrier();
+  double ss = 0.0;
+  for (int i = 0; i < nw; ++i) ss += L.red_d[i];
+  // xn into LDS, this thread's max |xn| and LoRA partial
   const float var = (float)ss * (1.0f / (float)K);
   const float r = 1.0f / sqrt_rn(var + 1e-5f);
   const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
   const float bs = a.lB ? h2f(bs_raw) : 0.0f;
   float mx = 0.0f;
   double hacc = 0.0;
-  u32x4 ov = {0u, 0u, 0u, 0u};
-  if (has_v) {
-    uint32_t o[4];
+  uint32_t o[4];
+  {
     const uint32_t bw[2] = {b8.x, b8.y};
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -106,36 +102,57 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
       hacc += (double)(x0 * b0);
       hacc += (double)(x1 * b1);
     }
-    ov = u32x4{o[0], o[1], o[2], o[3]};
-    *(u32x4*)&L.xn[8 * tid] = ov;
+    *(u32x4*)&L.xn[8 * tid] = u32x4{o[0], o[1], o[2], o[3]};
   }
-  // Global stores wait until the end: a wave with a store outstanding waits for its
-  // acknowledgement wherever the compiler needs a load complete (the counter is in order).
-  const double ht = a.lB ? block_sum_f64<kPT>(hacc, L.red_d) : 0.0;
-  const float amax = block_max_f32<kPT>(mx, L.red_f);  // also publishes xn to the block
+  {  // LoRA sum and maximum in one exchange (the first barrier: every wave has read the squares)
+    const double hw = wave_sum_dpp_f64(hacc);
+    const float mw = wave_max_dpp_f32(mx);
+    lds_barrier();
+    if (lane == 0) {
+      L.red_d[w] = hw;
+      L.red_f[w] = mw;
+    }
+  }
+  lds_barrier();  // also publishes xn
+  double ht = 0.0;
+  float amax = L.red_f[0];
+  for (int i = 0; i < nw; ++i) {
+    ht += L.red_d[i];
+    amax = fmaxf(amax, L.red_f[i]);
+  }
   const float xs = quant_scale(amax);
   // q over all columns when sum q is wanted, else only where written: the bytes and bit planes
   // of the 64-column wave blocks that start in slice rr (slices narrower than 64 columns, K < 1024,
-  // leave every other workgroup nothing to write)
+  // leave every other workgroup nothing to write). Global stores come last: a wave with a store
+  // outstanding waits for its acknowledgement wherever a later load must be complete.
   const int lo = rr * (K / 16), hi = lo + K / 16;
   const bool want_sum = a.s_out != nullptr;
   int qsum = 0;
-  for (int k0 = (tid & ~63); k0 < K; k0 += kPT) {
+  for (int k0 = 64 * w; k0 < K; k0 += NT) {
     const bool mine = k0 >= lo && k0 < hi;  // wave-uniform
     if (!want_sum && !mine) continue;
     const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
     qsum += q;
     if (mine) {
       if (a.q_out) a.q_out[(size_t)m * a.ld_q + k0 + lane] = (int8_t)q;
-      uint32_t pw[16];
-      planes64(q, pw);
-      if (a.planes_out) planes_store(a.planes_out + ((size_t)m * (a.ld_q / 32) + k0 / 32) * 8, pw);
+      if (a.planes_out) {
+        uint32_t pw[16];
+        planes64(q, pw);
+        planes_store(a.planes_out + ((size_t)m * (a.ld_q / 32) + k0 / 32) * 8, pw);
+      }
     }
   }
-  if (has_v && a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = ov;
+  if (a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = u32x4{o[0], o[1], o[2], o[3]};
   if (a.lB && tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + rr] = r16((float)ht);
   if (rr == 0) {
-    const int S = want_sum ? block_sum_i32<kPT>(qsum, L.red_i) : 0;
+    int S = 0;
+    if (want_sum) {
+      const int qw = wave_sum_dpp_i32(qsum);
+      lds_barrier();  // every wave has read the LoRA sums
+      if (lane == 0) L.red_i[w] = qw;
+      lds_barrier();
+      for (int i = 0; i < nw; ++i) S += L.red_i[i];
+    }
     if (tid == 0) {
       if (a.s_out) a.s_out[m] = S;
       if (a.xs_out) a.xs_out[m] = xs;
@@ -399,13 +416,13 @@ hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s) {
 
 hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
   // the kernel reads one sum-of-squares slot per thread and the LoRA scale with its table
-  if (mode == DFSSM_MODE_OUT && (!a.sumsq_slots || a.n_slots < 1 || a.n_slots > kPT)) return hipErrorInvalidValue;
+  if (mode == DFSSM_MODE_OUT && (!a.sumsq_slots || a.n_slots < 1 || a.n_slots > a.K / 8)) return hipErrorInvalidValue;
   if (a.lB && !a.lBs) return hipErrorInvalidValue;
-  if (a.K > kMaxK || a.K % 128) return hipErrorInvalidValue;
+  if (a.K > kMaxK || a.K % 512) return hipErrorInvalidValue;  // K / 8 threads: whole waves
   if (mode == DFSSM_MODE_IN)
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(kPT), 0, s, a);
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
   else
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(DFSSM_LORA_R, M), dim3(kPT), 0, s, a);
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
   return hipGetLastError();
 }
 
