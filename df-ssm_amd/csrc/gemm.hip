@@ -10,15 +10,16 @@
 // redone for up to four blocks) B stays 0/1 and acc = 2 T - sum_k q[m][k], the row sums taken
 // from the q tile in LDS.
 //
-// One workgroup (1024 threads = 16 waves) owns a group of 64 output rows; it keeps their bits in
-// registers and walks the activation rows in blocks of 32 (16 when K > 4096). Wave w = (row tile rt = w % 4, k slot kq = w / 4).
-// The 16-byte bit chunks c of the row group (128 columns each) are dealt out as
-// c = kq + 4 j + 16 sb to lane group j = lane / 16 of wave slot kq, block sb: every lane keeps its
-// chunks in registers, loaded once, fully coalesced. Within an MFMA step lane group j supplies
-// columns 128 c + 16 s .. +15 of both operands; a consistent permutation of the k index between
-// A and B leaves the dot product unchanged. The q tile of all rows sits in LDS (one batch of
-// loads); the four k slots' int32 partials are added through LDS (exact), and the epilogue is
-// shared by all 16 waves.
+// One workgroup (1024 threads = 16 waves) owns 16 RT output rows (RT = 1, 2 or 4 row tiles: the
+// fewest that keep the grid within one workgroup per CU); it keeps their bits in registers and walks the activation
+// rows in blocks of 32 (16 when K > 4096). Wave w = (row tile rt = w % RT, k slot kq = w / RT),
+// KQ = 16 / RT k slots. The 16-byte bit chunks c of a row tile (128 columns each) are dealt out as
+// c = kq + KQ j + 4 KQ sb to lane group j = lane / 16 of wave slot kq, block sb: every lane keeps
+// its chunks in registers, loaded once, fully coalesced. Within an MFMA step lane group j
+// supplies columns 128 c + 16 s .. +15 of both operands; a consistent permutation of the k index
+// between A and B leaves the dot product unchanged. The q tile of all rows sits in LDS (one
+// batch of loads); the k slots' int32 partials are added through LDS (exact), and the epilogue
+// is shared by the waves (element i of a lane's 4 MI accumulators by wave slot i % KQ).
 #include "common.h"
 #include "dfssm_kernels.h"
 
@@ -27,18 +28,19 @@ namespace dfssm {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGT = 1024;
-constexpr int kMaxSB = 3;  // bit-chunk blocks per lane: ceil(K / 128 / 16) for K <= 5120
 
-template <int MI, int MODE>
+template <int MI, int RT, int MODE>
 __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   constexpr int MP = MI * 16;  // activation rows per block
+  constexpr int KQ = 16 / RT;  // k slots
+  constexpr int kSB = (5120 / 128 + 4 * KQ - 1) / (4 * KQ);  // bit-chunk blocks per lane, K <= 5120
   extern __shared__ __attribute__((aligned(16))) int8_t qs[];  // MP rows x QS bytes; then partials
   __shared__ int Ssum[MP];
   __shared__ float hl[MP][DFSSM_LORA_R];
   __shared__ float xsl[MP];
   __shared__ uint32_t zero_s;  // read back as 0 in every row block (see below)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rt = wave & 3, kq = wave >> 2, j = lane >> 4;
+  const int rt = wave % RT, kq = wave / RT, j = lane >> 4;
   const int g = blockIdx.x;
   const int K = a.K, CH = K / 128, M = a.M;
   const int QS = K + 16;  // padded LDS row stride
@@ -77,13 +79,15 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 
   // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows,
   // kept raw until the epilogue ----
-  const int r = rt * 16 + (lane & 15);
-  u32x4 wb[kMaxSB];
+  const int r = rt * 16 + (lane & 15);  // output row within the workgroup's 16 RT
+  // the bits are tiled in groups of 64 rows: [group][chunk][64 rows][16 bytes]
+  const int g64 = g * RT / 4, r64 = (g * RT % 4) * 16 + r;
+  u32x4 wb[kSB];
 #pragma unroll
-  for (int sb = 0; sb < kMaxSB; ++sb) {
-    const int c = kq + 4 * j + 16 * sb;
+  for (int sb = 0; sb < kSB; ++sb) {
+    const int c = kq + KQ * j + 4 * KQ * sb;
     // chunks past CH re-read the last one; the MFMA loop zeroes their operands
-    wb[sb] = ld_nt((const u32x4*)a.bits + ((size_t)g * CH + (c < CH ? c : CH - 1)) * 64 + r);
+    wb[sb] = ld_nt((const u32x4*)a.bits + ((size_t)g64 * CH + (c < CH ? c : CH - 1)) * 64 + r64);
   }
   {  // the first block's q tile into LDS (waits only for the loads issued before the bits)
 #pragma unroll
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
     if (tid < MP * DFSSM_LORA_R) hl[tid >> 4][tid & 15] = tid < MB0 * DFSSM_LORA_R ? hv0 : 0.0f;
     if (tid < MP) xsl[tid] = tid < MB0 ? (MODE != DFSSM_MODE_SCAFFOLD ? xsv0 : h2f(xsh0)) : 0.0f;
   }
-  const int n = g * 64 + r;
+  const int n = g * 16 * RT + r;
   const bool nrow = n < a.N;
   u32x4 la = {0u, 0u, 0u, 0u};
   uint16_t ws_raw = 0, as_raw = 0;
@@ -165,9 +169,9 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[i] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int sb = 0; sb < kMaxSB; ++sb) {
-      if (kq + 16 * sb < CH) {  // wave-uniform: some lane group has a chunk in this block
-        const int c = kq + 4 * j + 16 * sb;
+    for (int sb = 0; sb < kSB; ++sb) {
+      if (kq + 4 * KQ * sb < CH) {  // wave-uniform: some lane group has a chunk in this block
+        const int c = kq + KQ * j + 4 * KQ * sb;
         const bool valid = c < CH;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -194,24 +198,26 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int ib = 0; ib < MI; ++ib)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part[(((kq * 4 + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
+      for (int e = 0; e < 4; ++e) part[(((kq * RT + rt) * MI + ib) * 4 + e) * 64 + lane] = acc[ib][e];
     lds_barrier();
 
-    // ---- epilogue: wave (rt, kq) finishes accumulator element e = kq of each tile ----
-    if (nrow) {
+    // ---- epilogue: wave (rt, kq) finishes accumulator elements i = kq, kq + KQ, ... < 4 MI ----
+    if (nrow && kq < 4 * MI) {
       double aqd[DFSSM_LORA_R];
 #pragma unroll
       for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
         aqd[rr] = (double)r16((float)(int8_t)((la[rr >> 2] ^ zero) >> (8 * (rr & 3))) * h2f(as_raw ^ (uint16_t)zero));
 #pragma unroll
-      for (int ib = 0; ib < MI; ++ib) {
-        const int e = kq;
+      for (int ii = 0; ii < (4 * MI + KQ - 1) / KQ; ++ii) {
+        const int i = kq + KQ * ii;
+        if (i >= 4 * MI) break;
+        const int ib = i >> 2, e = i & 3;
         const int mb = ib * 16 + 4 * j + e;  // row within the block
         if (mb >= MB) continue;
         const int m = m0 + mb;
         int T = 0;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) T += part[(((q4 * 4 + rt) * MI + ib) * 4 + e) * 64 + lane];
+        for (int q = 0; q < KQ; ++q) T += part[(((q * RT + rt) * MI + ib) * 4 + e) * 64 + lane];
         const int accv = MI == 2 ? T : 2 * T - Ssum[mb];
         if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
         const float y = r16(r16(r16((float)accv) * xsl[mb]) * h2f(ws_raw ^ (uint16_t)zero));
@@ -257,21 +263,30 @@ static size_t gemm_lds_bytes(int MI, int K) {
   return tile > part ? tile : part;
 }
 
-template <int MI, int MODE>
+template <int MI, int RT, int MODE>
 static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
   const size_t shm = gemm_lds_bytes(MI, a.K);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, MODE>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, RT, MODE>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gemm_kernel<MI, MODE>), dim3((a.N + 63) / 64), dim3(kGT), shm, s, a);
+  hipLaunchKernelGGL((gemm_kernel<MI, RT, MODE>), dim3((a.N + 16 * RT - 1) / (16 * RT)), dim3(kGT), shm, s, a);
   return hipGetLastError();
+}
+
+template <int MI, int MODE>
+static hipError_t launch_gemm_rt(const GemmArgs& a, hipStream_t s) {
+  // the fewest output rows per workgroup (16, 32 or 64) that keep the grid within one workgroup
+  // per CU (256): a workgroup fills its CU, so a grid beyond 256 runs a second round
+  if (a.N <= 256 * 16) return launch_gemm_mi<MI, 1, MODE>(a, s);
+  if (a.N <= 256 * 32) return launch_gemm_mi<MI, 2, MODE>(a, s);
+  return launch_gemm_mi<MI, 4, MODE>(a, s);
 }
 
 template <int MODE>
 static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
   // one launch for all rows; the kernel walks them in blocks whose q tile (rows x (K + 16) bytes)
   // fits the 160 KiB of LDS: 32 rows up to K = 4096, 16 above
-  return (a.M > 16 && a.K <= 4096) ? launch_gemm_mi<2, MODE>(a, s) : launch_gemm_mi<1, MODE>(a, s);
+  return (a.M > 16 && a.K <= 4096) ? launch_gemm_rt<2, MODE>(a, s) : launch_gemm_rt<1, MODE>(a, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {
