@@ -248,6 +248,27 @@ def measured_traffic(batch, phase):
     return None
 
 
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+
+
+def mfma_use(res, cfg):
+    """int8 matrix-core rate of the batched scaffold GEMMs (2 B N K ops per launch, the
+    algorithmic count: padding rows and the +-1 expansion are not counted) against the dense
+    int8 peak; batch > 4 only (the one-launch layer at batch <= 4 uses no matrix cores)."""
+    B = res["batch"]
+    if B <= 4:
+        return None
+    dims = {"in_proj+conv": (cfg.in_proj_out, cfg.d_model), "out_proj+residual": (cfg.d_model, cfg.d_inner)}
+    out = {}
+    for name, (N, K) in dims.items():
+        us = res["kernels"][name]["us_per_launch"]
+        ops = 2 * B * N * K
+        tops = ops / (us * 1e-6) / 1e12
+        out[name] = {"ops_per_launch": ops, "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 5)}
+    return out
+
+
 def roofline_of(res, name=None):
     ks = res["kernels"]
     dom = name or max(ks, key=lambda k: ks[k]["us_per_step"])
@@ -299,7 +320,7 @@ def main():
         if cpu:
             log(f"reference CPU: {cpu['value']} tok/s on {cpu['cores']} threads")
 
-    from dfssm.synth import config_1p3b
+    from dfssm.synth import config_1p3b, config_2p7b
     cfg = config_1p3b()
     B = a.batch
     out = {
@@ -322,12 +343,13 @@ def main():
     if second:
         out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],
                          "step_roofline": second["step_roofline"], "roofline": roofline_of(second),
-                         "scaffold_roofline": roofline_of(second, "in_proj+conv"), "kernels": second["kernels"]}
+                         "scaffold_roofline": roofline_of(second, "in_proj+conv"), "mfma": mfma_use(second, cfg),
+                         "kernels": second["kernels"]}
     if c4:
         out["config4"] = {"workload": "config4: 2.7B-shape DF-SSM greedy decode, batch 64, 512-token prompt "
                                       "ingested, 256 timed steps", "batch": 64, "tok_s": c4["tok_s"],
                           "ms_per_step": c4["ms_per_step"], "step_roofline": c4["step_roofline"],
-                          "roofline": roofline_of(c4), "kernels": c4["kernels"]}
+                          "roofline": roofline_of(c4), "mfma": mfma_use(c4, config_2p7b()), "kernels": c4["kernels"]}
     print(json.dumps(out), flush=True)
 
 

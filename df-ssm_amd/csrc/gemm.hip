@@ -33,7 +33,8 @@ template <int MI, int RT, int MODE>
 __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   constexpr int MP = MI * 16;  // activation rows per block
   constexpr int KQ = 16 / RT;  // k slots
-  constexpr int kSB = (5120 / 128 + 4 * KQ - 1) / (4 * KQ);  // bit-chunk blocks per lane, K <= 5120
+  constexpr int kKMax = MI == 2 ? 4096 : 5120;  // the host picks MI = 2 only for K <= 4096
+  constexpr int kSB = (kKMax / 128 + 4 * KQ - 1) / (4 * KQ);  // bit-chunk blocks per lane
   extern __shared__ __attribute__((aligned(16))) int8_t qs[];  // MP rows x QS bytes; then partials
   __shared__ int Ssum[MP];
   __shared__ float hl[MP][DFSSM_LORA_R];
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   // Wave w copies rows w + 16 jr, lane l the 16-byte vectors l + 64 i of a row: no index division,
   // row addresses are scalar. Loads are unconditional from clamped indices (a load inside a branch
   // makes the compiler wait for all loads where the paths join); staging selects.
-  constexpr int kQI = (MI == 2 ? 4096 : 5120) / 16 / 64;  // vectors per lane and row, K at most
+  constexpr int kQI = kKMax / 16 / 64;  // vectors per lane and row, K at most
   const int MB0 = M < MP ? M : MP;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   u32x4 qv[MI][kQI];
@@ -122,6 +123,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       cb = a.conv_b[ch];
     }
   }
+  constexpr int kEI = (4 * MI + KQ - 1) / KQ;  // epilogue elements per lane
   if (tid == 0) zero_s = 0u;
 #pragma nounroll
   for (int m0 = 0; m0 < M; m0 += MP) {
@@ -208,7 +210,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
         aqd[rr] = (double)r16((float)(int8_t)((la[rr >> 2] ^ zero) >> (8 * (rr & 3))) * h2f(as_raw ^ (uint16_t)zero));
 #pragma unroll
-      for (int ii = 0; ii < (4 * MI + KQ - 1) / KQ; ++ii) {
+      for (int ii = 0; ii < kEI; ++ii) {
         const int i = kq + KQ * ii;
         if (i >= 4 * MI) break;
         const int ib = i >> 2, e = i & 3;
