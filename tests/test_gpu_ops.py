@@ -28,7 +28,8 @@ def _tiled(bits_np, N, K):
     return ops.tile_bits(torch.from_numpy(bits_np.view(np.int32)).to(DEV), N, K)
 
 
-@pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096), (10576, 2560), (2048, 5120), (2320, 512)])
+# N picks 16, 32 or 64 output rows per matrix-core workgroup (N <= 4096, <= 8192, above)
+@pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096), (10576, 2560), (2048, 5120), (2320, 512), (6144, 1024)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16, 32, 64])
 def test_scaffold_acc_bit_exact(N, K, M):
     """Config 1: in_proj 2048->8512, out_proj 4096->2048 (+2.7B and tiny shapes), int8 ~N(0,40)."""
