@@ -66,6 +66,28 @@ WsLayout ws_layout(const dfssm_dims* d) {
   return w;
 }
 
+// Prompt prefill workspace for up to `rows` = batch x tokens-per-chunk activation rows: the
+// residual stream of every row, the projection rows, g, the sum(g^2) slots and the prologue
+// outputs (q, scale, LoRA intermediate).
+struct PfLayout {
+  size_t x, proj, g, slots, q, xs, h, total;
+};
+
+PfLayout pf_layout(const Derived& r, int rows) {
+  PfLayout w;
+  size_t off = 0;
+  const int kq = r.D > r.DI ? r.D : r.DI;
+  w.x = off;     off = align_up(off + (size_t)rows * r.D * 2);
+  w.proj = off;  off = align_up(off + (size_t)rows * r.IPO * 2);
+  w.g = off;     off = align_up(off + (size_t)rows * r.DI * 2);
+  w.slots = off; off = align_up(off + (size_t)rows * r.n_slots * 8);
+  w.q = off;     off = align_up(off + (size_t)rows * kq);
+  w.xs = off;    off = align_up(off + (size_t)rows * 4);
+  w.h = off;     off = align_up(off + (size_t)rows * 16 * 4);
+  w.total = off;
+  return w;
+}
+
 inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -440,6 +462,113 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
     rc = dfssm_layer_step(model, l, x, state, workspace, stream);
     if (rc) return rc;
   }
+  return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
+}
+
+size_t dfssm_prefill_workspace_bytes(const dfssm_dims* dims, int max_rows) {
+  if (!dims || dfssm_check_dims(dims) != DFSSM_OK) return 0;
+  if (max_rows < dims->batch || max_rows > kGemmMaxRows) return 0;
+  return pf_layout(derive(dims), max_rows).total;
+}
+
+// One chunk of the prefill: tokens t0 .. t0 + tc - 1 of every sequence through all layers.
+static int prefill_chunk(const dfssm_model* model, const int64_t* tokens, int n_tokens, int t0, int tc,
+                         const dfssm_state* state, void* workspace, char* pw, hipStream_t s) {
+  const Derived r = derive(&model->dims);
+  const PfLayout w = pf_layout(r, r.B * tc);
+  const int R = r.B * tc;
+  const int kq = r.D > r.DI ? r.D : r.DI;
+  uint16_t* xr = (uint16_t*)(pw + w.x);
+  uint16_t* proj = (uint16_t*)(pw + w.proj);
+  uint16_t* g = (uint16_t*)(pw + w.g);
+  double* slots = (double*)(pw + w.slots);
+  EmbedArgs e{tokens, (const uint8_t*)model->emb, model->emb_scale, model->dims.emb_code == 0 ? 1 : 0, xr,
+              (int*)((char*)workspace + ws_layout(&model->dims).err), r.V, r.D, n_tokens, t0, tc};
+  hipError_t st = launch_embed(e, R, s);
+  if (st != hipSuccess) return hip_status(st);
+  for (int l = 0; l < r.L; ++l) {
+    const dfssm_layer& Lw = model->layers[l];
+    float* h = state->h + (size_t)l * r.B * r.H * r.P * r.N;
+    uint16_t* conv = state->conv + (size_t)l * r.B * r.C * 3;
+    for (int ph = 0; ph < 2; ++ph) {  // in_proj, then out_proj
+      const bool in = ph == 0;
+      PrepArgs p{};
+      p.act = in ? xr : g;
+      p.ld_act = in ? r.D : r.DI;
+      p.norm_w = in ? Lw.ln_w : Lw.norm_w;
+      p.sumsq_slots = in ? nullptr : slots;
+      p.n_slots = in ? 0 : r.n_slots;
+      p.lB = in ? Lw.in_lB : Lw.out_lB;
+      p.lBs = in ? Lw.in_lB_s : Lw.out_lB_s;
+      p.q_out = (int8_t*)(pw + w.q);
+      p.ld_q = kq;
+      p.xs_out = (float*)(pw + w.xs);
+      p.h_out = (float*)(pw + w.h);
+      p.K = in ? r.D : r.DI;
+      st = launch_prep(p, R, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s);
+      if (st != hipSuccess) return hip_status(st);
+      GemmArgs a{};
+      a.q = (const int8_t*)(pw + w.q); a.ld_q = kq; a.M = R;
+      a.xs = (const float*)(pw + w.xs);
+      a.h = (const float*)(pw + w.h);
+      if (in) {  // raw projection rows: the conv runs over the tokens below
+        a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
+        a.out = proj; a.ld_out = r.IPO;
+        a.N = r.IPO; a.K = r.D;
+      } else {
+        a.bits = Lw.out_bits; a.wscale = Lw.out_scale; a.lA = Lw.out_lA; a.lAs = Lw.out_lA_s;
+        a.out = xr; a.ld_out = r.D;
+        a.N = r.D; a.K = r.DI;
+      }
+      st = launch_gemm(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s);
+      if (st != hipSuccess) return hip_status(st);
+      if (!in) break;
+      ConvSeqArgs c{conv, proj + r.DI, r.IPO, Lw.conv_w, Lw.conv_b, r.C, tc};
+      st = launch_conv_seq(c, r.B, s);
+      if (st != hipSuccess) return hip_status(st);
+      ScanArgs sc{};
+      sc.h = h;
+      sc.xbc = proj + r.DI; sc.ld_xbc = r.IPO;
+      sc.dt = proj + r.DI + r.C; sc.ld_dt = r.IPO;
+      sc.z = proj; sc.ld_z = r.IPO;
+      sc.dt_bias = Lw.dt_bias; sc.A_log = Lw.A_log; sc.D = Lw.D;
+      sc.y_out = g; sc.ld_y = r.DI;
+      sc.sumsq_slots = slots; sc.n_slots = r.n_slots;
+      sc.H = r.H; sc.P = r.P; sc.N = r.N; sc.T = tc;
+      st = launch_ssm_scan(sc, r.B, s);
+      if (st != hipSuccess) return hip_status(st);
+    }
+  }
+  return DFSSM_OK;
+}
+
+int dfssm_prefill(const dfssm_model* model, const int64_t* tokens, int n_tokens, uint16_t* x,
+                  const dfssm_state* state, void* workspace, void* prefill_workspace, int max_rows,
+                  uint16_t* logits, int64_t* next, int fuse_next_embed, void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!tokens || !x || !state || !state->h || !state->conv || !workspace || !prefill_workspace || !next)
+    return DFSSM_E_NULL;
+  const Derived r = derive(&model->dims);
+  if (n_tokens < 1 || max_rows < r.B || max_rows > kGemmMaxRows) return DFSSM_E_RANGE;
+  if (!aligned16(prefill_workspace) || !aligned16(workspace) || !aligned16(x) || !aligned16(state->h))
+    return DFSSM_E_ALIGN;
+  for (int l = 0; l < r.L; ++l) {
+    rc = check_layer_args(model, l, x, state, workspace);
+    if (rc) return rc;
+  }
+  hipStream_t s = as_stream(stream);
+  char* pw = (char*)prefill_workspace;
+  const int T = max_rows / r.B;  // tokens per chunk
+  int tc = 0;
+  for (int t0 = 0; t0 < n_tokens; t0 += tc) {
+    tc = n_tokens - t0 < T ? n_tokens - t0 : T;
+    rc = prefill_chunk(model, tokens, n_tokens, t0, tc, state, workspace, pw, s);
+    if (rc) return rc;
+  }
+  // the last token's residual row of every sequence, then the head as after a decode step
+  rc = hip_status(launch_last_rows((const uint16_t*)(pw + pf_layout(r, r.B * tc).x), x, r.B, tc, r.D, s));
+  if (rc) return rc;
   return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
 }
 

@@ -64,12 +64,13 @@ struct GemmArgs {
   uint16_t* out;             // IN: proj; OUT: residual x (in place); SCAFFOLD: y (may be null)
   int ld_out;
   int32_t* acc_out;          // optional (M, N) accumulators
-  uint16_t* conv_state;      // IN: (M, conv_c, 3)
+  uint16_t* conv_state;      // IN: (M, conv_c, 3); null: the conv rows are written raw (prefill)
   const uint16_t* conv_w;
   const uint16_t* conv_b;
   int conv_lo, conv_c;
   int N, K;
 };
+constexpr int kGemmMaxRows = 32768;  // activation rows of one gemm_kernel launch (prefill)
 
 struct ScaffoldArgs {
   const uint32_t* bits;      // tiled sign bits
@@ -107,6 +108,37 @@ struct ConvArgs {
   int ld, C;
 };
 
+// Prompt prefill (prefill.hip): conv over the tokens of each sequence, rows (b, t) at b * T + t.
+struct ConvSeqArgs {
+  uint16_t* state;           // (batch, C, 3) fp16, advanced by T tokens
+  uint16_t* x;               // rows (batch * T, ld): raw xBC in, conv'd + SiLU out (in place)
+  int ld;
+  const uint16_t* w;         // (C, 4)
+  const uint16_t* b;         // (C)
+  int C, T;
+};
+
+// Prompt prefill: SSM + gate over T tokens per sequence (rows (b, t) at b * T + t), state in
+// registers; the fields mean what they mean in SsmArgs, with z and the slots required.
+struct ScanArgs {
+  float* h;                  // (batch, H, P, N) fp32 state, advanced by T tokens
+  const uint16_t* xbc;       // rows x | B | C (after the conv)
+  int ld_xbc;
+  const uint16_t* dt;        // raw dt rows
+  int ld_dt;
+  const uint16_t* z;         // gate input rows
+  int ld_z;
+  const float* dt_bias;
+  const float* A_log;
+  const float* D;
+  uint16_t* y_out;           // (batch * T, ld_y) gated g
+  int ld_y;
+  double* sumsq_slots;       // (batch * T, n_slots) per-block sum(g^2)
+  int n_slots;
+  int H, P, N, T;
+  int pb0;                   // set by the kernel
+};
+
 struct HeadArgs {
   const uint16_t* x;         // (M, D) fp16 residual
   const float* norm_f;       // (D) fp32
@@ -134,6 +166,9 @@ struct EmbedArgs {
   uint16_t* x;               // (M, D)
   int* err_flag;             // set to 1 if a token is out of range
   int V, D;
+  // tok_tc > 0: row m reads tokens[(m / tok_tc) * tok_ld + tok_t0 + m % tok_tc] (a window of
+  // tok_tc tokens of every sequence of a row-major (batch, tok_ld) prompt); else tokens[m]
+  int tok_ld, tok_t0, tok_tc;
 };
 
 // One whole layer for 1..4 sequences in a single launch (fused.hip).
@@ -176,6 +211,9 @@ hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
 size_t head_digit_bytes(int M, int D);  // HeadArgs::hdig size for the batched int8 head
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
+hipError_t launch_conv_seq(const ConvSeqArgs& a, int batch, hipStream_t s);
+hipError_t launch_ssm_scan(const ScanArgs& a, int batch, hipStream_t s);
+hipError_t launch_last_rows(const uint16_t* src, uint16_t* dst, int batch, int T, int D, hipStream_t s);
 hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int row_bytes, hipStream_t s);
 
 }  // namespace dfssm

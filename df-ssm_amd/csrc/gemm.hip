@@ -110,7 +110,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   uint32_t cw01 = 0, cw23 = 0;
   uint16_t cb = 0;
   const int ch = n - a.conv_lo;
-  const bool conv_row = MODE == DFSSM_MODE_IN && nrow && ch >= 0 && ch < a.conv_c;
+  const bool conv_row = MODE == DFSSM_MODE_IN && a.conv_state && nrow && ch >= 0 && ch < a.conv_c;
   if (nrow) {
     if (a.wscale) ws_raw = a.wscale[n];
     if (MODE != DFSSM_MODE_SCAFFOLD) {
@@ -128,6 +128,22 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma nounroll
   for (int m0 = 0; m0 < M; m0 += MP) {
     const int MB = M - m0 < MP ? M - m0 : MP;  // rows in this block
+    // ---- the epilogue's read-modify-write operands of this block (conv state / residual x),
+    // issued now so that their round trip overlaps the MFMAs; unconditional loads from clamped
+    // addresses, selected in the epilogue ----
+    uint16_t pre[kEI][3];
+#pragma unroll
+    for (int ii = 0; ii < kEI; ++ii) {
+      const int i = kq + KQ * ii;
+      const int mb = (i < 4 * MI ? (i >> 2) * 16 + 4 * j + (i & 3) : 0);
+      const int m = m0 + (mb < MB ? mb : 0);
+      if (MODE == DFSSM_MODE_IN && a.conv_state) {
+        const uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + (conv_row ? ch : 0)) * 3;
+        pre[ii][0] = cs[0]; pre[ii][1] = cs[1]; pre[ii][2] = cs[2];
+      } else if (MODE == DFSSM_MODE_OUT) {
+        pre[ii][0] = a.out[(size_t)m * a.ld_out + (nrow ? n : 0)];
+      }
+    }
     // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
     lds_barrier();  // the previous block's partials (in qs) have been read
     if (m0 > 0) {  // the first block's tile was staged before the loop
@@ -235,7 +251,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         if (MODE == DFSSM_MODE_IN) {
           if (conv_row) {
             uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
-            const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
+            const uint16_t s0 = pre[ii][0], s1 = pre[ii][1], s2 = pre[ii][2];
             const uint16_t xo = f2h(out);
             cs[0] = s1;
             cs[1] = s2;
@@ -252,7 +268,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
           }
           *op = f2h(out);
         } else {
-          *op = f2h(h2f(*op) + out);
+          *op = f2h(h2f(pre[ii][0]) + out);
         }
       }
     }
@@ -292,7 +308,7 @@ static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {
-  if (a.M < 1 || a.M > 64 || a.K % 512 || a.K > 5120) return hipErrorInvalidValue;
+  if (a.M < 1 || a.M > kGemmMaxRows || a.K % 512 || a.K > 5120) return hipErrorInvalidValue;
   switch (mode) {
     case DFSSM_MODE_IN: return launch_gemm_mode<DFSSM_MODE_IN>(a, s);
     case DFSSM_MODE_OUT: return launch_gemm_mode<DFSSM_MODE_OUT>(a, s);

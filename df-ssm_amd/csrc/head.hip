@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   const int m = blockIdx.x;
-  const int64_t t64 = a.tokens[m];
+  const int64_t t64 = a.tok_tc > 0 ? a.tokens[(size_t)(m / a.tok_tc) * a.tok_ld + a.tok_t0 + m % a.tok_tc] : a.tokens[m];
   const int t = (t64 < 0 || t64 >= a.V) ? 0 : (int)t64;
   if (t64 < 0 || t64 >= a.V) {
     if (threadIdx.x == 0) atomicOr(a.err_flag, 1);

@@ -1,0 +1,254 @@
+// Prompt prefill, layer-major (gfx950): the n prompt tokens of every sequence go through one
+// layer together, then the next layer. The projections and their prologues are row-independent,
+// so the decode kernels run them on all batch x n rows at once (prep_kernel, gemm_kernel); only
+// the two recurrences walk the tokens in order, here:
+//
+//   conv_seq_kernel  one thread per (sequence, conv channel): the fp16 shift register stays in
+//                    registers while the thread walks the tokens; out = s0 w0 + s1 w1 + s2 w2 +
+//                    x w3 + b (left to right, fp32), x <- fp16(out sigmoid(out)), in place on the
+//                    projection rows, whose raw values the in_proj GEMM wrote (no conv there).
+//   ssm_scan_kernel  one workgroup per (sequence, head, up to 4 blocks of 16 state rows): the fp32
+//                    state of the rows stays in registers for all n tokens (read and written
+//                    once per layer instead of once per token). Per token the arithmetic, the
+//                    thread -> state-element map and every reduction tree are those of
+//                    ssm_kernel<true>, so state, g and the per-block sum(g^2) slots are bit-for-bit
+//                    what n decode steps produce. The tokens' operands (B | C, x, z, dt) are staged
+//                    in LDS kTT tokens at a time, double-buffered, with softplus dt, exp(dt A) and
+//                    the gate factor z sigma(z) computed once per token (per row) while staging.
+//
+// Together with the row-wise kernels this makes the prefill equal, bit for bit, to n calls of the
+// decode step (Mamba-2 recurrence of df_ssm_kernels.cu:53-103 / training/
+// df_ssm_mamba2_distill_dfw.py:346-381, evaluated token by token as the reference's
+// cpu_inference_driver.py:186-204 ingests a prompt).
+#include "common.h"
+#include "dfssm_kernels.h"
+
+namespace dfssm {
+
+__global__ __launch_bounds__(256) void conv_seq_kernel(ConvSeqArgs a) {
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (ch >= a.C) return;
+  uint16_t* cs = a.state + ((size_t)b * a.C + ch) * 3;
+  uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
+  const uint16_t* wc = a.w + (size_t)ch * 4;
+  const float w0 = h2f(wc[0]), w1 = h2f(wc[1]), w2 = h2f(wc[2]), w3 = h2f(wc[3]);
+  const float cb = h2f(a.b[ch]);
+  uint16_t* col = a.x + (size_t)b * a.T * a.ld + ch;  // token t of sequence b: col[t * ld]
+  constexpr int U = 8;
+  for (int t0 = 0; t0 < a.T; t0 += U) {
+    uint16_t raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) raw[u] = col[(size_t)(t0 + u < a.T ? t0 + u : a.T - 1) * a.ld];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t0 + u >= a.T) break;
+      const uint16_t xo = raw[u];
+      float o = h2f(s0) * w0;
+      o = o + h2f(s1) * w1;
+      o = o + h2f(s2) * w2;
+      o = o + h2f(xo) * w3;
+      o = o + cb;
+      const float sig = 1.0f / (1.0f + dev_expf(-o));
+      col[(size_t)(t0 + u) * a.ld] = f2h(o * sig);
+      s0 = s1;
+      s1 = s2;
+      s2 = xo;
+    }
+  }
+  cs[0] = s0;
+  cs[1] = s1;
+  cs[2] = s2;
+}
+
+constexpr int kTT = 16;    // tokens staged per round
+constexpr int kPGMax = 4;  // 16-row state blocks per workgroup
+
+struct ScanBuf {
+  uint16_t bc[kTT][256];           // B (0..127) | C (128..255) of each token
+  uint16_t x[kTT][16 * kPGMax];    // x of the workgroup's rows
+  float sz[kTT][16 * kPGMax];      // gate factor fp16(z sigma(z)) of the workgroup's rows
+  float dt[kTT], abar[kTT];        // softplus dt and exp(dt A) of the head
+  double gpart[kTT][4 * kPGMax];   // per-wave partial sum(g^2), reduced per block after the round
+};
+
+// Raw operands of one round, loaded into registers one round ahead.
+template <int PG>
+struct ScanRaw {
+  static constexpr int KB = (kTT * 32 + 256 * PG - 1) / (256 * PG);
+  u32x4 bc[KB];    // 8 halves of B | C: chunk i = tid + 256 PG k, token i / 32, halves 8 (i % 32) ..
+  uint16_t x, z;   // token tid / (16 PG), row tid % (16 PG) (tid < kTT * 16 PG = blockDim)
+  uint16_t dt;     // token tid (tid < kTT)
+};
+
+template <int PG>
+__device__ __forceinline__ ScanRaw<PG> scan_load(const ScanArgs& a, int b, int head, int t0) {
+  const int tid = threadIdx.x;
+  constexpr int NT = 256 * PG, RW = 16 * PG;
+  ScanRaw<PG> r{};
+  const size_t row0 = (size_t)b * a.T;
+  // clamped token indices: rows past the end re-read the last token (never consumed)
+#pragma unroll
+  for (int k = 0; k < ScanRaw<PG>::KB; ++k) {
+    const int i = tid + NT * k;
+    const int t = t0 + i / 32;
+    const uint16_t* p = a.xbc + (row0 + (t < a.T ? t : a.T - 1)) * a.ld_xbc + a.H * a.P + 8 * (i % 32);
+    if (i < kTT * 32) r.bc[k] = *(const u32x4*)p;
+  }
+  if (tid < kTT * RW) {
+    const int t = t0 + tid / RW;
+    const size_t row = row0 + (t < a.T ? t : a.T - 1);
+    const int col = head * a.P + a.pb0 * 16 + tid % RW;
+    r.x = a.xbc[row * a.ld_xbc + col];
+    r.z = a.z[row * a.ld_z + col];
+  }
+  if (tid < kTT) {
+    const int t = t0 + tid;
+    r.dt = a.dt[(row0 + (t < a.T ? t : a.T - 1)) * a.ld_dt + head];
+  }
+  return r;
+}
+
+template <int PG>
+__device__ __forceinline__ void scan_stage(ScanBuf& S, const ScanRaw<PG>& r, float dtb, float nA) {
+  const int tid = threadIdx.x;
+  constexpr int NT = 256 * PG, RW = 16 * PG;
+#pragma unroll
+  for (int k = 0; k < ScanRaw<PG>::KB; ++k) {
+    const int i = tid + NT * k;
+    if (i < kTT * 32) *(u32x4*)&S.bc[i / 32][8 * (i % 32)] = r.bc[k];
+  }
+  if (tid < kTT * RW) {
+    const int t = tid / RW, i = tid % RW;
+    S.x[t][i] = r.x;
+    const float z = h2f(r.z);
+    S.sz[t][i] = r16(z * r16(1.0f / (1.0f + dev_expf(-z))));
+  }
+  if (tid < kTT) {
+    const float dt = dev_log1pf(dev_expf(h2f(r.dt) + dtb));
+    S.dt[tid] = dt;
+    S.abar[tid] = dev_expf(dt * nA);
+  }
+}
+
+template <int PG>
+__global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
+  __shared__ ScanBuf buf[2];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int grp = tid >> 8;            // 16-row block of this thread within the workgroup
+  const int gt = tid & 255;            // thread within its block: the ssm_kernel map
+  const int b = blockIdx.y;
+  const int wg_per_head = a.P / (16 * PG);
+  const int head = blockIdx.x / wg_per_head;
+  const int pb = (blockIdx.x % wg_per_head) * PG + grp;  // state block of this thread
+  ScanArgs aa = a;
+  aa.pb0 = (blockIdx.x % wg_per_head) * PG;
+  const int n0 = 4 * (gt & 31);
+  const int pr = gt >> 5;              // rows pr and pr + 8 of the block
+  const int p = pb * 16 + pr;
+  const int rl = grp * 16 + pr;        // row index within the workgroup's staged x / sz
+  const float Dh = a.D[head], dtb = a.dt_bias[head];
+  const float nA = -dev_expf(a.A_log[head]);
+
+  ScanRaw<PG> raw = scan_load<PG>(aa, b, head, 0);
+  float* hp = a.h + (((size_t)b * a.H + head) * a.P + p) * a.N + n0;
+  const f32x4 s0 = ld_nt_f4(hp);
+  const f32x4 s1 = ld_nt_f4(hp + 8 * a.N);
+  float h0[4] = {s0.x, s0.y, s0.z, s0.w}, h1[4] = {s1.x, s1.y, s1.z, s1.w};
+  scan_stage<PG>(buf[0], raw, dtb, nA);
+  lds_barrier();
+
+  const int rounds = (a.T + kTT - 1) / kTT;
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int t0 = rd * kTT;
+    ScanBuf& S = buf[rd & 1];
+    if (rd + 1 < rounds) raw = scan_load<PG>(aa, b, head, t0 + kTT);
+    const int nt = a.T - t0 < kTT ? a.T - t0 : kTT;
+    for (int t = 0; t < nt; ++t) {
+      const uint2 b4 = *(const uint2*)&S.bc[t][n0];
+      const uint2 c4 = *(const uint2*)&S.bc[t][128 + n0];
+      const float dt = S.dt[t], abar = S.abar[t];
+      const float xv0 = h2f(S.x[t][rl]), xv1 = h2f(S.x[t][rl + 8]);
+      const float X0 = xv0 * dt, X1 = xv1 * dt;
+      const uint32_t bw[2] = {b4.x, b4.y}, cw[2] = {c4.x, c4.y};
+      double acc0 = 0.0, acc1 = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float bn = h2f((uint16_t)(bw[j >> 1] >> (16 * (j & 1))));
+        const float cn = h2f((uint16_t)(cw[j >> 1] >> (16 * (j & 1))));
+        h0[j] = __builtin_fmaf(abar, h0[j], X0 * bn);
+        h1[j] = __builtin_fmaf(abar, h1[j], X1 * bn);
+        acc0 += (double)cn * (double)h0[j];
+        acc1 += (double)cn * (double)h1[j];
+      }
+      acc0 = row_sum_f64(acc0);
+      acc1 = row_sum_f64(acc1);
+      const double t0a = readlane_f64(acc0, 0) + readlane_f64(acc0, 16);
+      const double t0b = readlane_f64(acc0, 32) + readlane_f64(acc0, 48);
+      const double t1a = readlane_f64(acc1, 0) + readlane_f64(acc1, 16);
+      const double t1b = readlane_f64(acc1, 32) + readlane_f64(acc1, 48);
+      double gsqd = 0.0;
+      if ((gt & 31) == 0) {
+        const bool hi = lane >= 32;
+        const float y0 = r16((float)(hi ? t0b : t0a) + xv0 * Dh);
+        const float y1 = r16((float)(hi ? t1b : t1a) + xv1 * Dh);
+        const float o0 = r16(y0 * S.sz[t][rl]);
+        const float o1 = r16(y1 * S.sz[t][rl + 8]);
+        gsqd = (double)o0 * (double)o0 + (double)o1 * (double)o1;
+        uint16_t* yp = a.y_out + ((size_t)b * a.T + t0 + t) * a.ld_y + head * a.P + p;
+        yp[0] = f2h(o0);
+        yp[8] = f2h(o1);
+      }
+      const double s = wave_sum_dpp_f64(gsqd);
+      if (lane == 0) S.gpart[t][w] = s;
+    }
+    if (rd + 1 < rounds) scan_stage<PG>(buf[(rd + 1) & 1], raw, dtb, nA);
+    lds_barrier();
+    // per-block sum(g^2) of this round's tokens, in ssm_kernel's order (waves 0 + 1 + 2 + 3)
+    if (tid < nt * PG) {
+      const int t = tid / PG, g = tid % PG;
+      const double* gp = &S.gpart[t][4 * g];
+      const int slot = head * (a.P / 16) + aa.pb0 + g;
+      a.sumsq_slots[((size_t)b * a.T + t0 + t) * a.n_slots + slot] = gp[0] + gp[1] + gp[2] + gp[3];
+    }
+  }
+  st_nt_f4(hp, f32x4{h0[0], h0[1], h0[2], h0[3]});
+  st_nt_f4(hp + 8 * a.N, f32x4{h1[0], h1[1], h1[2], h1[3]});
+}
+
+// dst[b] = src[b * T + T - 1]: the last token's row of every sequence.
+__global__ __launch_bounds__(256) void last_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                        int T, int D) {
+  const int b = blockIdx.x;
+  const uint16_t* s = src + ((size_t)b * T + T - 1) * D;
+  for (int k = threadIdx.x; k < D; k += 256) dst[(size_t)b * D + k] = s[k];
+}
+
+hipError_t launch_conv_seq(const ConvSeqArgs& a, int batch, hipStream_t s) {
+  hipLaunchKernelGGL(conv_seq_kernel, dim3((a.C + 255) / 256, batch), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+int scan_groups(int P) {
+  const int pbs = P / 16;
+  return pbs % 4 == 0 ? 4 : (pbs % 2 == 0 ? 2 : 1);
+}
+
+hipError_t launch_ssm_scan(const ScanArgs& a, int batch, hipStream_t s) {
+  if (a.T < 1 || a.P % 16 || a.N != 128) return hipErrorInvalidValue;
+  const int PG = scan_groups(a.P);
+  const dim3 grid(a.H * (a.P / (16 * PG)), batch);
+  switch (PG) {
+    case 4: hipLaunchKernelGGL(ssm_scan_kernel<4>, grid, dim3(1024), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(ssm_scan_kernel<2>, grid, dim3(512), 0, s, a); break;
+    default: hipLaunchKernelGGL(ssm_scan_kernel<1>, grid, dim3(256), 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_last_rows(const uint16_t* src, uint16_t* dst, int batch, int T, int D, hipStream_t s) {
+  hipLaunchKernelGGL(last_rows_kernel, dim3(batch), dim3(256), 0, s, src, dst, T, D);
+  return hipGetLastError();
+}
+
+}  // namespace dfssm

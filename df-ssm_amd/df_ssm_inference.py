@@ -240,12 +240,45 @@ class DFSSMModel:
             self._gen_graphs[S] = (self._capture(body), hist)
         return self._gen_graphs[S]
 
-    def ingest(self, prompt: torch.Tensor) -> None:
-        """Consume a (batch, T) prompt token by token; afterwards self._next holds the greedy
-        token after the prompt and self.x its embedding."""
+    PREFILL_MAX_ROWS = 16384  # batch x tokens per prefill chunk (workspace ~ rows x 38 KB at 1.3B)
+
+    def prefill(self, prompt: torch.Tensor, want_logits: bool = False) -> torch.Tensor:
+        """Consume a (batch, T) prompt in one layer-major pass (dfssm_prefill): bit-for-bit the
+        result of T decode steps. Afterwards self._next holds the greedy token after the prompt
+        and self.x its embedding; returns the last token's logits if want_logits, else None."""
+        prompt = torch.as_tensor(prompt)
+        if prompt.dim() == 1:
+            prompt = prompt.view(-1, 1)
+        if prompt.shape[0] != self.batch_size or prompt.shape[1] < 1:
+            raise ValueError(f"prompt must be (batch={self.batch_size}, T >= 1), got {tuple(prompt.shape)}")
+        if prompt.device.type == "cpu" and (int(prompt.min()) < 0 or int(prompt.max()) >= self.cfg.vocab_size):
+            raise IndexError("token id out of range")
+        prompt = prompt.to(self.device, torch.int64).contiguous()
+        rows = min(self.PREFILL_MAX_ROWS, self.batch_size * prompt.shape[1])
+        rows = max(rows, self.batch_size)
+        if getattr(self, "_pf_rows", 0) < rows:
+            nbytes = _C.lib().dfssm_prefill_workspace_bytes(self.dims, rows)
+            if nbytes == 0:
+                raise _C.DFSSMError(f"prefill of {rows} rows not supported")
+            self._pf_ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self._pf_rows = rows
+        _C.check(_C.lib().dfssm_prefill(
+            self._model, prompt.data_ptr(), prompt.shape[1], self.x.data_ptr(), self._state,
+            self.workspace.data_ptr(), self._pf_ws.data_ptr(), self._pf_rows,
+            self.logits.data_ptr() if want_logits else None, self._next.data_ptr(), 1, _C.stream()), "prefill")
+        self._tok.copy_(prompt[:, -1])
+        return self.logits.clone() if want_logits else None
+
+    def ingest(self, prompt: torch.Tensor, step_by_step: bool = False) -> None:
+        """Consume a (batch, T) prompt; afterwards self._next holds the greedy token after the
+        prompt and self.x its embedding. By default one layer-major prefill pass; with
+        step_by_step, T decode steps (graph replays), which give the same bits."""
         prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
         if prompt.dim() == 1:
             prompt = prompt.view(-1, 1)
+        if not step_by_step:
+            self.prefill(prompt)
+            return
         if self._graph is None:
             self._capture_graph()
         for t in range(prompt.shape[1]):

@@ -163,6 +163,26 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
                       const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
                       int fuse_next_embed, void* stream);
 
+/* ---- prompt prefill ------------------------------------------------------------------- */
+/* Workspace of dfssm_prefill for chunks of up to max_rows = batch x tokens-per-chunk rows
+ * (batch <= max_rows <= 32768); 0 if the arguments are not supported. */
+size_t dfssm_prefill_workspace_bytes(const dfssm_dims* dims, int max_rows);
+
+/* Ingest a prompt of n_tokens tokens per sequence, tokens (batch, n_tokens) int64 row-major: the
+ * result -- state, logits, next and x -- is bit-for-bit that of n_tokens dfssm_decode_step calls
+ * with tokens[:, t] (the reference ingests prompts token by token, cpu_inference_driver.py:
+ * 186-204; its GPU generate() has no prompt, df_ssm_inference.py:226-243). Layer-major: the
+ * prompt rows of all sequences go through a layer together (prologues and scaffold GEMMs over
+ * batch x n_tokens rows on the int8 matrix cores), the conv and the SSM recurrence walk the
+ * tokens with their state in registers, so weights and state are read once per layer and chunk
+ * instead of once per token. The prompt is processed in chunks of max_rows / batch tokens;
+ * prefill_workspace holds dfssm_prefill_workspace_bytes(dims, max_rows) bytes, workspace is the
+ * decode workspace (the head and the error flag). logits (batch, V) may be NULL; x receives the
+ * embedding of `next` if fuse_next_embed, else the last token's residual row. */
+int dfssm_prefill(const dfssm_model* model, const int64_t* tokens, int n_tokens, uint16_t* x,
+                  const dfssm_state* state, void* workspace, void* prefill_workspace, int max_rows,
+                  uint16_t* logits, int64_t* next, int fuse_next_embed, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
