@@ -43,8 +43,15 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rt = wave % RT, kq = wave / RT, j = lane >> 4;
   const int g = blockIdx.x;
-  const int K = a.K, CH = K / 128, M = a.M;
+  const int K = a.K, CH = K / 128;
   const int QS = K + 16;  // padded LDS row stride
+  // rows of this workgroup: blocks [blockIdx.y * bpw, +bpw) of the activation rows (one range
+  // in decode; the prompt prefill spreads its thousands of rows over gridDim.y ranges)
+  const int nblk = (a.M + MP - 1) / MP, bpw = (nblk + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int m_begin = (int)blockIdx.y * bpw * MP;
+  if (m_begin >= a.M) return;
+  const int m_end = m_begin + bpw * MP < a.M ? m_begin + bpw * MP : a.M;
+  const int M = m_end - m_begin;  // rows of this workgroup, from m_begin
 
   // ---- the first row block's q tile, issued before the bits (loads complete in issue order, so
   // the tile does not wait for the weight stream from HBM) ----
@@ -58,7 +65,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int jr = 0; jr < MI; ++jr) {
     const int row = wv + 16 * jr;
-    const int8_t* qrow = a.q + (size_t)(row < MB0 ? row : MB0 - 1) * a.ld_q;
+    const int8_t* qrow = a.q + (size_t)(m_begin + (row < MB0 ? row : MB0 - 1)) * a.ld_q;
 #pragma unroll
     for (int i = 0; i < kQI; ++i) {
       const int c16 = lane + 64 * i;  // lanes past the row load nothing (exec-masked)
@@ -72,10 +79,10 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   float hv0 = 0.0f, xsv0 = 0.0f;
   uint16_t xsh0 = 0;
   if (MODE != DFSSM_MODE_SCAFFOLD) {
-    hv0 = a.h[hi0];
-    xsv0 = a.xs[xi0];
+    hv0 = a.h[(size_t)m_begin * DFSSM_LORA_R + hi0];
+    xsv0 = a.xs[m_begin + xi0];
   } else if (a.xs16) {  // absent when only the accumulators are written
-    xsh0 = a.xs16[xi0];
+    xsh0 = a.xs16[m_begin + xi0];
   }
 
   // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows,
@@ -126,44 +133,64 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   constexpr int kEI = (4 * MI + KQ - 1) / KQ;  // epilogue elements per lane
   if (tid == 0) zero_s = 0u;
 #pragma nounroll
-  for (int m0 = 0; m0 < M; m0 += MP) {
-    const int MB = M - m0 < MP ? M - m0 : MP;  // rows in this block
-    // ---- the epilogue's read-modify-write operands of this block (conv state / residual x),
-    // issued now so that their round trip overlaps the MFMAs; unconditional loads from clamped
-    // addresses, selected in the epilogue ----
-    uint16_t pre[kEI][3];
-#pragma unroll
-    for (int ii = 0; ii < kEI; ++ii) {
-      const int i = kq + KQ * ii;
-      const int mb = (i < 4 * MI ? (i >> 2) * 16 + 4 * j + (i & 3) : 0);
-      const int m = m0 + (mb < MB ? mb : 0);
-      if (MODE == DFSSM_MODE_IN && a.conv_state) {
-        const uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + (conv_row ? ch : 0)) * 3;
-        pre[ii][0] = cs[0]; pre[ii][1] = cs[1]; pre[ii][2] = cs[2];
-      } else if (MODE == DFSSM_MODE_OUT) {
-        pre[ii][0] = a.out[(size_t)m * a.ld_out + (nrow ? n : 0)];
+  for (int m0 = m_begin; m0 < m_end; m0 += MP) {
+    const int MB = m_end - m0 < MP ? m_end - m0 : MP;  // rows in this block
+    // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 (the first block's
+    // were staged before the loop): every load is issued before the first LDS store, from
+    // clamped rows, so the tile costs one memory round trip, overlapping the barrier ----
+    if (RT == 4 && MI == 1 && m0 > m_begin) {
+      // in_proj at 64 output rows with 16-row blocks reaches here only for d_model > 4096; the
+      // unrolled copy below would raise this variant's peak registers past 128, so it copies
+      // with a loop (a load round trip per vector)
+      lds_barrier();  // the previous block's partials (in qs) have been read
+      for (int c16 = lane; c16 < K / 16; c16 += 64) {
+        u32x4 x = {0u, 0u, 0u, 0u};
+        if (wv < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + wv) * a.ld_q + c16 * 16);
+        *(u32x4*)(qs + (size_t)wv * QS + c16 * 16) = x;
       }
-    }
-    // ---- q tile, LoRA intermediates and scales of rows m0 .. m0 + MB - 1 ----
-    lds_barrier();  // the previous block's partials (in qs) have been read
-    if (m0 > 0) {  // the first block's tile was staged before the loop
-      for (int jr = 0; jr < MI; ++jr) {
-        const int row = wv + 16 * jr;
-        for (int c16 = lane; c16 < K / 16; c16 += 64) {
-          u32x4 x = {0u, 0u, 0u, 0u};
-          if (row < MB) x = *(const u32x4*)(a.q + (size_t)(m0 + row) * a.ld_q + c16 * 16);
-          *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = x;
+      if (tid < MP * DFSSM_LORA_R) {
+        const int m = tid >> 4;
+        hl[m][tid & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (tid & 15)] : 0.0f;
+      }
+      if (tid < MP) xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
+    } else if (m0 > m_begin) {
+      // at most 4 vectors per lane and row in flight (a fifth, K > 4096, in a second round)
+      constexpr int kQR = kQI > 4 ? 4 : kQI;
+      const int hi = tid < MB * DFSSM_LORA_R ? tid : MB * DFSSM_LORA_R - 1;
+      const int xi = tid < MB ? tid : MB - 1;
+      float hv = 0.0f, xsv = 0.0f;
+#pragma unroll
+      for (int i0 = 0; i0 < kQI; i0 += kQR) {
+        u32x4 qn[MI][kQR];
+#pragma unroll
+        for (int jr = 0; jr < MI; ++jr) {
+          const int row = wv + 16 * jr;
+          const int8_t* qrow = a.q + (size_t)(m0 + (row < MB ? row : MB - 1)) * a.ld_q;
+#pragma unroll
+          for (int i = 0; i < kQR; ++i) {
+            const int c16 = lane + 64 * (i0 + i);
+            qn[jr][i] = (i0 + i < kQI && c16 < K / 16) ? *(const u32x4*)(qrow + c16 * 16) : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+        if (i0 == 0) {
+          if (a.h) hv = a.h[(size_t)m0 * DFSSM_LORA_R + hi];
+          if (a.xs) xsv = a.xs[m0 + xi];
+          else if (a.xs16) xsv = h2f(a.xs16[m0 + xi]);
+          lds_barrier();  // the previous block's partials (in qs) have been read
+        }
+#pragma unroll
+        for (int jr = 0; jr < MI; ++jr) {
+          const int row = wv + 16 * jr;
+#pragma unroll
+          for (int i = 0; i < kQR; ++i) {
+            const int c16 = lane + 64 * (i0 + i);
+            if (i0 + i < kQI && c16 < K / 16)
+              *(u32x4*)(qs + (size_t)row * QS + c16 * 16) = row < MB ? qn[jr][i] : u32x4{0u, 0u, 0u, 0u};
+          }
         }
       }
-    }
-    if (m0 > 0) {
-      for (int i = tid; i < MP * DFSSM_LORA_R; i += kGT) {
-        const int m = i >> 4;
-        hl[m][i & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (i & 15)] : 0.0f;
-      }
-      if (tid < MP) {
-        xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
-      }
+      if (tid < MP * DFSSM_LORA_R) hl[tid >> 4][tid & 15] = tid < MB * DFSSM_LORA_R ? hv : 0.0f;
+      if (tid < MP) xsl[tid] = tid < MB ? xsv : 0.0f;
     }
     lds_barrier();
     if (MI == 1) {  // sum q per row: wave w sums row w (exact integer reduction)
@@ -251,7 +278,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         if (MODE == DFSSM_MODE_IN) {
           if (conv_row) {
             uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
-            const uint16_t s0 = pre[ii][0], s1 = pre[ii][1], s2 = pre[ii][2];
+            const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
             const uint16_t xo = f2h(out);
             cs[0] = s1;
             cs[1] = s2;
@@ -268,7 +295,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
           }
           *op = f2h(out);
         } else {
-          *op = f2h(h2f(pre[ii][0]) + out);
+          *op = f2h(h2f(*op) + out);
         }
       }
     }
@@ -287,7 +314,13 @@ static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, RT, MODE>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gemm_kernel<MI, RT, MODE>), dim3((a.N + 16 * RT - 1) / (16 * RT)), dim3(kGT), shm, s, a);
+  // one workgroup per CU (registers and LDS): decode batches run one row range; many rows
+  // (prefill) are split into ranges so that the grid fills about two rounds of the CUs
+  const int gx = (a.N + 16 * RT - 1) / (16 * RT);
+  const int nblk = (a.M + MI * 16 - 1) / (MI * 16);
+  int gy = a.M > 64 ? (512 + gx / 2) / gx : 1;
+  gy = gy < 1 ? 1 : (gy > nblk ? nblk : gy);
+  hipLaunchKernelGGL((gemm_kernel<MI, RT, MODE>), dim3(gx, gy), dim3(kGT), shm, s, a);
   return hipGetLastError();
 }
 

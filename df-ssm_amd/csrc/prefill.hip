@@ -63,6 +63,7 @@ __global__ __launch_bounds__(256) void conv_seq_kernel(ConvSeqArgs a) {
 
 constexpr int kTT = 16;    // tokens staged per round
 constexpr int kPGMax = 4;  // 16-row state blocks per workgroup
+constexpr int kTG = 4;     // tokens whose reductions run together
 
 struct ScanBuf {
   uint16_t bc[kTT][256];           // B (0..127) | C (128..255) of each token
@@ -164,43 +165,67 @@ __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
     ScanBuf& S = buf[rd & 1];
     if (rd + 1 < rounds) raw = scan_load<PG>(aa, b, head, t0 + kTT);
     const int nt = a.T - t0 < kTT ? a.T - t0 : kTT;
-    for (int t = 0; t < nt; ++t) {
-      const uint2 b4 = *(const uint2*)&S.bc[t][n0];
-      const uint2 c4 = *(const uint2*)&S.bc[t][128 + n0];
-      const float dt = S.dt[t], abar = S.abar[t];
-      const float xv0 = h2f(S.x[t][rl]), xv1 = h2f(S.x[t][rl + 8]);
-      const float X0 = xv0 * dt, X1 = xv1 * dt;
-      const uint32_t bw[2] = {b4.x, b4.y}, cw[2] = {c4.x, c4.y};
-      double acc0 = 0.0, acc1 = 0.0;
+    // Tokens in groups of kTG: the state updates are a chain of fmas, but a token's readout and
+    // sum(g^2) reductions feed nothing later, so a group's reductions are independent chains the
+    // compiler interleaves. Slots of a group past nt update nothing and store nothing.
+    for (int t = 0; t < nt; t += kTG) {
+      double acc0[kTG], acc1[kTG];
+      float xv0[kTG], xv1[kTG];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float bn = h2f((uint16_t)(bw[j >> 1] >> (16 * (j & 1))));
-        const float cn = h2f((uint16_t)(cw[j >> 1] >> (16 * (j & 1))));
-        h0[j] = __builtin_fmaf(abar, h0[j], X0 * bn);
-        h1[j] = __builtin_fmaf(abar, h1[j], X1 * bn);
-        acc0 += (double)cn * (double)h0[j];
-        acc1 += (double)cn * (double)h1[j];
+      for (int j = 0; j < kTG; ++j) {
+        const int tt = t + j < nt ? t + j : t;
+        const uint2 b4 = *(const uint2*)&S.bc[tt][n0];
+        const uint2 c4 = *(const uint2*)&S.bc[tt][128 + n0];
+        const float dt = S.dt[tt], abar = S.abar[tt];
+        xv0[j] = h2f(S.x[tt][rl]);
+        xv1[j] = h2f(S.x[tt][rl + 8]);
+        const float X0 = xv0[j] * dt, X1 = xv1[j] * dt;
+        const uint32_t bw[2] = {b4.x, b4.y}, cw[2] = {c4.x, c4.y};
+        const bool valid = t + j < nt;
+        acc0[j] = 0.0;
+        acc1[j] = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float bn = h2f((uint16_t)(bw[q >> 1] >> (16 * (q & 1))));
+          const float cn = h2f((uint16_t)(cw[q >> 1] >> (16 * (q & 1))));
+          const float n0v = __builtin_fmaf(abar, h0[q], X0 * bn);
+          const float n1v = __builtin_fmaf(abar, h1[q], X1 * bn);
+          h0[q] = valid ? n0v : h0[q];
+          h1[q] = valid ? n1v : h1[q];
+          acc0[j] += (double)cn * (double)h0[q];
+          acc1[j] += (double)cn * (double)h1[q];
+        }
       }
-      acc0 = row_sum_f64(acc0);
-      acc1 = row_sum_f64(acc1);
-      const double t0a = readlane_f64(acc0, 0) + readlane_f64(acc0, 16);
-      const double t0b = readlane_f64(acc0, 32) + readlane_f64(acc0, 48);
-      const double t1a = readlane_f64(acc1, 0) + readlane_f64(acc1, 16);
-      const double t1b = readlane_f64(acc1, 32) + readlane_f64(acc1, 48);
-      double gsqd = 0.0;
-      if ((gt & 31) == 0) {
-        const bool hi = lane >= 32;
-        const float y0 = r16((float)(hi ? t0b : t0a) + xv0 * Dh);
-        const float y1 = r16((float)(hi ? t1b : t1a) + xv1 * Dh);
-        const float o0 = r16(y0 * S.sz[t][rl]);
-        const float o1 = r16(y1 * S.sz[t][rl + 8]);
-        gsqd = (double)o0 * (double)o0 + (double)o1 * (double)o1;
-        uint16_t* yp = a.y_out + ((size_t)b * a.T + t0 + t) * a.ld_y + head * a.P + p;
-        yp[0] = f2h(o0);
-        yp[8] = f2h(o1);
+#pragma unroll
+      for (int j = 0; j < kTG; ++j) {
+        acc0[j] = row_sum_f64(acc0[j]);
+        acc1[j] = row_sum_f64(acc1[j]);
       }
-      const double s = wave_sum_dpp_f64(gsqd);
-      if (lane == 0) S.gpart[t][w] = s;
+      double gsqd[kTG];
+#pragma unroll
+      for (int j = 0; j < kTG; ++j) {
+        const double t0a = readlane_f64(acc0[j], 0) + readlane_f64(acc0[j], 16);
+        const double t0b = readlane_f64(acc0[j], 32) + readlane_f64(acc0[j], 48);
+        const double t1a = readlane_f64(acc1[j], 0) + readlane_f64(acc1[j], 16);
+        const double t1b = readlane_f64(acc1[j], 32) + readlane_f64(acc1[j], 48);
+        gsqd[j] = 0.0;
+        if ((gt & 31) == 0 && t + j < nt) {
+          const bool hi = lane >= 32;
+          const float y0 = r16((float)(hi ? t0b : t0a) + xv0[j] * Dh);
+          const float y1 = r16((float)(hi ? t1b : t1a) + xv1[j] * Dh);
+          const float o0 = r16(y0 * S.sz[t + j][rl]);
+          const float o1 = r16(y1 * S.sz[t + j][rl + 8]);
+          gsqd[j] = (double)o0 * (double)o0 + (double)o1 * (double)o1;
+          uint16_t* yp = a.y_out + ((size_t)b * a.T + t0 + t + j) * a.ld_y + head * a.P + p;
+          yp[0] = f2h(o0);
+          yp[8] = f2h(o1);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kTG; ++j) {
+        const double s = wave_sum_dpp_f64(gsqd[j]);
+        if (lane == 0 && t + j < nt) S.gpart[t + j][w] = s;
+      }
     }
     if (rd + 1 < rounds) scan_stage<PG>(buf[(rd + 1) & 1], raw, dtb, nA);
     lds_barrier();
