@@ -4,7 +4,8 @@
 Workload: the 1.3B-shaped DF-SSM (d_model 2048, 48 layers, d_inner 4096,
 64 heads x 64, d_state 128, vocab 50288, rank-16 int8 LoRA, int8 tied embedding) with seeded
 random-init weights, written to and loaded from a .dfssm file; a seeded 32-token prompt per
-sequence is ingested step by step, then greedy decode steps are timed. One step = one token for
+sequence is ingested (dfssm_prefill, bit-identical to step-by-step ingestion; its time is reported
+under "prefill"), then greedy decode steps are timed. One step = one token for
 every sequence of the batch: embedding, 48 layers, final norm, tied head, argmax, with the
 greedy token fed back on the device (HIP graph of 8 steps per replay). value = batch * steps /
 seconds over the timed steps, inputs resident in HBM.
@@ -85,6 +86,24 @@ def build_model(B, path, shape="1p3b"):
     torch.cuda.synchronize()
     log(f"loaded {path} for batch {B} ({time.time() - t:.1f}s)")
     return m, w
+
+
+def time_prefill(m, prompts):
+    """Prompt ingestion by dfssm_prefill (layer-major, bit-identical to step-by-step decode): one
+    untimed call (workspace allocation), then one timed with HIP events from a reset state.
+    Leaves the state after the prompt."""
+    import torch
+    p = torch.from_numpy(prompts).to("cuda:0")
+    m.reset_state()
+    m.prefill(p)
+    m.reset_state()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    m.prefill(p)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1)
 
 
 def time_decode(m, prompts, steps, warmup):
@@ -182,6 +201,13 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
     m, w = build_model(B, path, shape)
     cfg = m.cfg
     prompts = make_prompts(B, cfg.vocab_size, prompt_len)
+    pf_ms = time_prefill(m, prompts)
+    L, R = cfg.n_layer, B * prompt_len
+    pf_ops = 2 * R * L * (cfg.in_proj_out * cfg.d_model + cfg.d_model * cfg.d_inner)
+    prefill = {"batch": B, "prompt_tokens": prompt_len, "ms": round(pf_ms, 3),
+               "tok_s": round(R / (pf_ms * 1e-3), 1),
+               "gemm_ops": pf_ops, "gemm_tops_whole_prefill": round(pf_ops / (pf_ms * 1e-3) / 1e12, 2)}
+    log(f"prefill batch {B} x {prompt_len} tokens: {pf_ms:.1f} ms, {prefill['tok_s']:.0f} tok/s")
     ms, nsteps = time_decode(m, prompts, steps, warmup)
     ms_per_step = ms / nsteps
     tok_s = B * nsteps / (ms / 1e3)
@@ -209,7 +235,7 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
            "step_roofline": {"bytes_per_step": step_bytes, "weights": weights, "state": state,
                              "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
                              "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
-           "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2)}
+           "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2), "prefill": prefill}
     del m
     torch.cuda.empty_cache()
     return res, w, prompts
@@ -339,17 +365,19 @@ def main():
         "step_roofline": main_res["step_roofline"],
         "kernels": main_res["kernels"],
         "cpu_baseline": cpu,
+        "prefill": main_res["prefill"],
     }
     if second:
         out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],
                          "step_roofline": second["step_roofline"], "roofline": roofline_of(second),
                          "scaffold_roofline": roofline_of(second, "in_proj+conv"), "mfma": mfma_use(second, cfg),
-                         "kernels": second["kernels"]}
+                         "kernels": second["kernels"], "prefill": second["prefill"]}
     if c4:
         out["config4"] = {"workload": "config4: 2.7B-shape DF-SSM greedy decode, batch 64, 512-token prompt "
                                       "ingested, 256 timed steps", "batch": 64, "tok_s": c4["tok_s"],
                           "ms_per_step": c4["ms_per_step"], "step_roofline": c4["step_roofline"],
-                          "roofline": roofline_of(c4), "mfma": mfma_use(c4, config_2p7b()), "kernels": c4["kernels"]}
+                          "roofline": roofline_of(c4), "mfma": mfma_use(c4, config_2p7b()), "kernels": c4["kernels"],
+                          "prefill": c4["prefill"]}
     print(json.dumps(out), flush=True)
 
 

@@ -221,9 +221,11 @@ __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
           yp[8] = f2h(o1);
         }
       }
+      // the wave's sum(g^2): only lanes 0 and 32 hold non-zero values, so ssm_kernel's
+      // wave_sum_dpp_f64 adds exact zeros to them and equals (lane 0) + (lane 32)
 #pragma unroll
       for (int j = 0; j < kTG; ++j) {
-        const double s = wave_sum_dpp_f64(gsqd[j]);
+        const double s = readlane_f64(gsqd[j], 0) + readlane_f64(gsqd[j], 32);
         if (lane == 0 && t + j < nt) S.gpart[t + j][w] = s;
       }
     }
