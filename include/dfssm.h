@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 2
+#define DFSSM_ABI_VERSION 3
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
