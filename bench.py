@@ -20,6 +20,7 @@ reference's cpu_inference.c, HEADDIM 64, compiled in oracle/_ref) on a bounded s
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -125,6 +126,47 @@ def time_decode(m, prompts, steps, warmup):
     return ms, reps * STEPS_PER_GRAPH
 
 
+def time_sampled(m, prompts, steps, warmup, T=0.7, top_p=0.9, penalty=1.2):
+    """Decode with the sampling head (gen_test.py's settings: temperature 0.7, top-p 0.9,
+    repetition penalty 1.2) instead of the argmax: graphs of 8 steps, HIP events. Returns ms
+    per step and the sampler kernel's own time per launch (graph of 48 launches on fixed logits)."""
+    import torch
+    from dfssm import _C
+    m.reset_state()
+    params = m._sampler(T, top_p, penalty, 0, 1234)
+    m._counts.zero_()
+    m._sstep.zero_()
+    m.ingest(torch.from_numpy(prompts))
+    g, _ = m._sample_graph(STEPS_PER_GRAPH, params)
+    for _ in range(max(1, warmup // STEPS_PER_GRAPH)):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // STEPS_PER_GRAPH)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * STEPS_PER_GRAPH)
+    lib = _C.lib()
+    out = torch.zeros(m.batch_size, dtype=torch.int64, device="cuda:0")
+    ks = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ks):
+        for _ in range(48):
+            _C.check(lib.dfssm_sample(m._model, m.logits.data_ptr(), m._counts.data_ptr(), m._sstep.data_ptr(),
+                                      ctypes.byref(params), out.data_ptr(), None, m.workspace.data_ptr(),
+                                      _C.stream()))
+    ks.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        ks.replay()
+    e1.record()
+    e1.synchronize()
+    return ms, e0.elapsed_time(e1) * 1e3 / (5 * 48)
+
+
 def time_kernels(m, reps=10):
     """Per-launch time of each layer kernel and of the head: HIP events on the launch stream around
     `reps` replays of a graph of 48 back-to-back launches of that kernel alone, divided by the
@@ -218,6 +260,12 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / PEAK_GBS:.1f}% of HBM peak)")
     if m.error_flag():
         raise RuntimeError(f"decode reported error flag {m.error_flag():#x}")
+    samp_ms, samp_us = time_sampled(m, prompts, steps, warmup)
+    sampled = {"settings": "temperature 0.7, top-p 0.9, repetition penalty 1.2 (gen_test.py)",
+               "ms_per_step": round(samp_ms, 4), "tok_s": round(B / (samp_ms * 1e-3), 1),
+               "sample_kernel_us_per_launch": round(samp_us, 2)}
+    log(f"sampled decode batch {B}: {samp_ms * 1e3:.1f} us/step, {sampled['tok_s']:.0f} tok/s "
+        f"(sampler {samp_us:.1f} us/launch)")
     kt = time_kernels(m)
     phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
                 "head+argmax": 3, "layer (one launch)": 4}
@@ -235,7 +283,8 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
            "step_roofline": {"bytes_per_step": step_bytes, "weights": weights, "state": state,
                              "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
                              "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
-           "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2), "prefill": prefill}
+           "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2), "prefill": prefill,
+           "sampled": sampled}
     del m
     torch.cuda.empty_cache()
     return res, w, prompts
@@ -366,12 +415,13 @@ def main():
         "kernels": main_res["kernels"],
         "cpu_baseline": cpu,
         "prefill": main_res["prefill"],
+        "sampled": main_res["sampled"],
     }
     if second:
         out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],
                          "step_roofline": second["step_roofline"], "roofline": roofline_of(second),
                          "scaffold_roofline": roofline_of(second, "in_proj+conv"), "mfma": mfma_use(second, cfg),
-                         "kernels": second["kernels"], "prefill": second["prefill"]}
+                         "kernels": second["kernels"], "prefill": second["prefill"], "sampled": second["sampled"]}
     if c4:
         out["config4"] = {"workload": "config4: 2.7B-shape DF-SSM greedy decode, batch 64, 512-token prompt "
                                       "ingested, 256 timed steps", "batch": 64, "tok_s": c4["tok_s"],

@@ -30,7 +30,7 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, ticket, err, launches, gtick,
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
       proj_t, g_t, h_t, dt_t, total;
 };
 
@@ -52,6 +52,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.hpart = off;    off = align_up(off + (r.B <= 4 ? (size_t)r.head_groups * (r.D / 512) * r.B * 64 * 8 : 0));
   w.hdig = off;     off = align_up(off + (r.B > 4 ? head_digit_bytes(r.B, r.D) : 0));  // batched int8 head
+  w.samp = off;     off = align_up(off + (size_t)r.B * 2 * ((r.V + 3) / 4 * 4) * 4);  // sampler rows z | e
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
   // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by
@@ -463,6 +464,29 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
     if (rc) return rc;
   }
   return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
+}
+
+int dfssm_sample(const dfssm_model* model, const uint16_t* logits, int32_t* counts, uint32_t* step,
+                 const dfssm_sample_params* params, int64_t* next, uint16_t* x_next, void* workspace,
+                 void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!logits || !counts || !step || !params || !next) return DFSSM_E_NULL;
+  const Derived r = derive(&model->dims);
+  if (r.V > kSampleMaxVocab) return DFSSM_E_DIMS;
+  const dfssm_sample_params& p = *params;
+  if (!(p.temperature > 0.0f) || !(p.penalty > 0.0f) || !(p.top_p >= 0.0f) || (p.mode != 0 && p.mode != 1))
+    return DFSSM_E_RANGE;
+  SampleArgs a{};
+  a.logits = logits; a.counts = counts; a.step = step; a.next = next;
+  a.temperature = p.temperature; a.top_p = p.top_p; a.penalty = p.penalty; a.mode = p.mode; a.seed = p.seed;
+  a.V = r.V;
+  if (!workspace) return DFSSM_E_NULL;
+  a.escratch = (float*)((char*)workspace + ws_layout(&model->dims).samp);
+  hipStream_t s = as_stream(stream);
+  rc = hip_status(launch_sample(a, r.B, s));
+  if (rc || !x_next) return rc;
+  return dfssm_embed(model, next, x_next, workspace, stream);
 }
 
 size_t dfssm_prefill_workspace_bytes(const dfssm_dims* dims, int max_rows) {

@@ -139,6 +139,20 @@ struct ScanArgs {
   int pb0;                   // set by the kernel
 };
 
+// Sampling head (sample.hip): one workgroup per sequence.
+constexpr int kSampleMaxVocab = 65536;
+struct SampleArgs {
+  const uint16_t* logits;    // (M, V) fp16
+  int* counts;               // (M, V) occurrences of each token so far; the drawn token is counted
+  uint32_t* step;            // (M) draw counter of each sequence (RNG stream position), advanced
+  int64_t* next;             // (M) drawn tokens
+  float temperature, top_p, penalty;
+  int mode;                  // 0: gen_test.py order, 1: training-script order (see sample.hip)
+  uint64_t seed;
+  int V;
+  float* escratch;           // (M, 2, ld) workspace rows z | exp(z - max z), ld = V rounded up to 4
+};
+
 struct HeadArgs {
   const uint16_t* x;         // (M, D) fp16 residual
   const float* norm_f;       // (D) fp32
@@ -211,6 +225,7 @@ hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s);
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
 size_t head_digit_bytes(int M, int D);  // HeadArgs::hdig size for the batched int8 head
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
+hipError_t launch_sample(const SampleArgs& a, int batch, hipStream_t s);
 hipError_t launch_conv_seq(const ConvSeqArgs& a, int batch, hipStream_t s);
 hipError_t launch_ssm_scan(const ScanArgs& a, int batch, hipStream_t s);
 hipError_t launch_last_rows(const uint16_t* src, uint16_t* dst, int batch, int T, int D, hipStream_t s);

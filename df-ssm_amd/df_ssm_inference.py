@@ -20,6 +20,7 @@ cpu_inference_driver.py:191-192).
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import sys
 import time
@@ -300,13 +301,79 @@ class DFSSMModel:
             done += s
         return torch.cat(out, dim=1)[:, :n_steps]
 
-    def generate(self, n_tokens=128, prompt=None, return_tokens=False, verbose=True):
+    # ------------------------------------------------------------------ sampling
+    def _sampler(self, temperature, top_p, penalty, mode, seed):
+        if getattr(self, "_counts", None) is None:
+            V = self.cfg.vocab_size
+            self._counts = torch.zeros(self.batch_size, V, dtype=torch.int32, device=self.device)
+            self._sstep = torch.zeros(self.batch_size, dtype=torch.int32, device=self.device)
+            self._gnext = torch.zeros(self.batch_size, dtype=torch.int64, device=self.device)
+        return _C.SampleParams(float(temperature), float(top_p), float(penalty), int(mode), int(seed) & (2**64 - 1))
+
+    def _sample_step(self, params, tokens: Optional[torch.Tensor], out: torch.Tensor) -> None:
+        """One decode step whose next token is drawn by dfssm_sample instead of the argmax;
+        x receives the drawn token's embedding."""
+        self._decode(tokens, self.logits, self._gnext, fuse=False)
+        _C.check(_C.lib().dfssm_sample(self._model, self.logits.data_ptr(), self._counts.data_ptr(),
+                                       self._sstep.data_ptr(), ctypes.byref(params), out.data_ptr(),
+                                       self.x.data_ptr(), self.workspace.data_ptr(), _C.stream()), "sample")
+
+    def _sample_graph(self, S: int, params):
+        key = (S, params.temperature, params.top_p, params.penalty, params.mode, params.seed)
+        graphs = self.__dict__.setdefault("_sample_graphs", {})
+        if key not in graphs:
+            hist = torch.zeros(S, self.batch_size, dtype=torch.int64, device=self.device)
+
+            def body():
+                for i in range(S):
+                    self._sample_step(params, None, hist[i])
+            graphs[key] = (self._capture(body), hist)
+        return graphs[key]
+
+    def _generate_sampled(self, n_tokens, prompt, temperature, top_p, penalty, mode, seed):
+        """Sampled decode (eval/gen_test.py:54-95 semantics, see dfssm_sample): the prompt is
+        counted as seen, ingested, then n_tokens draws; returns (tokens (B, n), seconds)."""
+        params = self._sampler(temperature, top_p, penalty, mode, seed)
+        self._counts.zero_()
+        self._sstep.zero_()
+        self._counts.scatter_add_(1, prompt, torch.ones_like(prompt, dtype=torch.int32))
+        S = 8 if n_tokens > 8 else 1
+        g, hist = self._sample_graph(S, params)
+        g1, hist1 = self._sample_graph(1, params)
+        if prompt.shape[1] > 1:
+            self.ingest(prompt[:, :-1])
+        first = torch.empty(self.batch_size, dtype=torch.int64, device=self.device)
+        torch.cuda.synchronize(self.device)
+        start = time.perf_counter()
+        self._sample_step(params, prompt[:, -1].contiguous(), first)
+        out = [first[:, None].clone()]
+        done = 1
+        while done < n_tokens:
+            if n_tokens - done >= S:
+                g.replay()
+                out.append(hist.t().clone())
+                done += S
+            else:
+                g1.replay()
+                out.append(hist1.t().clone())
+                done += 1
+        torch.cuda.synchronize(self.device)
+        self._next.copy_(out[-1][:, -1])
+        return torch.cat(out, dim=1)[:, :n_tokens], time.perf_counter() - start
+
+    def generate(self, n_tokens=128, prompt=None, return_tokens=False, verbose=True, temperature=None,
+                 top_p=1.0, repetition_penalty=1.0, penalty_mode=0, seed=0):
         """Greedy decode timed like the reference's generate (df_ssm_inference.py:226-243).
 
         The timed region holds n_tokens decode steps: the first consumes the last prompt token
         (token 0 without a prompt, as in the reference), each later one the previous greedy
         token. With return_tokens, returns the (batch, n_tokens) greedy tokens those steps
         produced; earlier prompt tokens are ingested before the timer starts.
+
+        With a temperature, the tokens are drawn instead (dfssm_sample: temperature, top_p,
+        repetition_penalty over the prompt and the tokens drawn so far; penalty_mode 0 is
+        eval/gen_test.py:54-95, 1 the training script's :1066-1078), from a generator seeded by
+        `seed`.
         """
         B = self.batch_size
         self.reset_state()
@@ -315,6 +382,14 @@ class DFSSMModel:
         prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
         if prompt.dim() == 1:
             prompt = prompt.view(-1, 1)
+        if temperature is not None:
+            toks, elapsed = self._generate_sampled(n_tokens, prompt, temperature, top_p, repetition_penalty,
+                                                   penalty_mode, seed)
+            self.last_elapsed = elapsed
+            if verbose:
+                print(f"batch={B}  {n_tokens} sampled steps  {n_tokens * B} total tokens")
+                print(f"  {elapsed*1000:.1f} ms  ({n_tokens * B / elapsed:.0f} tok/s total)")
+            return toks if return_tokens else None
         # graphs are captured before the timer starts; capture executes nothing
         if self._graph is None:
             self._capture_graph()

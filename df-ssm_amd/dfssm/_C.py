@@ -44,6 +44,11 @@ class State(ctypes.Structure):
     _fields_ = [("h", c_void_p), ("conv", c_void_p)]
 
 
+class SampleParams(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("penalty", ctypes.c_float),
+                ("mode", ctypes.c_int32), ("seed", ctypes.c_uint64)]
+
+
 _SIGS = {
     "dfssm_version": (c_int, []),
     "dfssm_error_string": (ctypes.c_char_p, [c_int]),
@@ -65,6 +70,7 @@ _SIGS = {
     "dfssm_layer_phase": (c_int, [ctypes.POINTER(Model), c_int, c_int, P, ctypes.POINTER(State), P, P]),
     "dfssm_lmhead_argmax": (c_int, [ctypes.POINTER(Model), P, P, P, P, P, P]),
     "dfssm_decode_step": (c_int, [ctypes.POINTER(Model), P, P, ctypes.POINTER(State), P, P, P, c_int, P]),
+    "dfssm_sample": (c_int, [ctypes.POINTER(Model), P, P, P, ctypes.POINTER(SampleParams), P, P, P, P]),
     "dfssm_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(Dims), c_int]),
     "dfssm_prefill": (c_int, [ctypes.POINTER(Model), P, c_int, P, ctypes.POINTER(State), P, P, c_int, P, P,
                               c_int, P]),

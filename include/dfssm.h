@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 3
+#define DFSSM_ABI_VERSION 4
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
@@ -162,6 +162,31 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
 int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
                       const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
                       int fuse_next_embed, void* stream);
+
+/* ---- sampling ------------------------------------------------------------------------ */
+typedef struct dfssm_sample_params {
+  float temperature;   /* > 0 */
+  float top_p;         /* >= 0; >= 1 keeps every token, 0 only the most probable */
+  float penalty;       /* repetition penalty r > 0 (1 = none) */
+  int32_t mode;        /* 0: z = logit / T, then / r if the token occurred (eval/gen_test.py:71-74);
+                          1: per occurrence logit > 0 ? / r : * r, then / T
+                          (training/df_ssm_mamba2_distill_dfw.py:1069-1073) */
+  uint64_t seed;
+} dfssm_sample_params;
+
+/* Draw the next token of every sequence from fp16 logits (batch, V) with temperature, repetition
+ * penalty and top-p, as eval/gen_test.py:54-95 and training/df_ssm_mamba2_distill_dfw.py:
+ * 1066-1078 do with torch.sort / cumsum / multinomial. The top-p set is the reference's rule
+ * (a token stays while the probability mass ranked above it is <= top_p) on exact fixed-point
+ * masses; the draw is Gumbel-max with a counter-based generator (splitmix64 of seed, sequence,
+ * step[b], token), deterministic for a given seed (torch's generator is not reproduced).
+ * counts (batch, V) int32 holds each token's occurrences so far (the caller counts the prompt);
+ * the drawn token is added, and step (batch) advances. next (batch) receives the tokens; if
+ * x_next is non-NULL it receives their embedding (as dfssm_embed). workspace: the decode
+ * workspace (scratch for the draw and the error flag). V <= 65536. */
+int dfssm_sample(const dfssm_model* model, const uint16_t* logits, int32_t* counts, uint32_t* step,
+                 const dfssm_sample_params* params, int64_t* next, uint16_t* x_next, void* workspace,
+                 void* stream);
 
 /* ---- prompt prefill ------------------------------------------------------------------- */
 /* Workspace of dfssm_prefill for chunks of up to max_rows = batch x tokens-per-chunk rows

@@ -513,3 +513,92 @@ void or_c_gate_norm(const float* y, const float* z, int ld_z, const float* w, fl
     for (int i = 0; i < DI; ++i) out[(size_t)m * DI + i] = out[(size_t)m * DI + i] * inv * w[i];
   }
 }
+
+/* ---------------------------------------------------------------- sampling ---------------- */
+/* The sampling head's definition (dfssm_sample), restated by its definition rather than by the
+ * kernel's radix select and slab scan: penalty + temperature per eval/gen_test.py:71-74 (mode 0)
+ * or training/df_ssm_mamba2_distill_dfw.py:1069-1073 (mode 1); e = exp(z - max z),
+ * E = floor(e 2^40); tokens ranked by e descending, index ascending (a full sort here); a token is
+ * kept iff the E mass ranked above it is <= floor(top_p * Z) -- the reference's
+ * `(cumsum - p) > top_p` drop rule (gen_test.py:77-80) on exact masses; the draw is the first
+ * kept index (index order) whose cumulative kept mass exceeds R = floor(h S / 2^64), S the kept
+ * mass and h = splitmix64 (Steele, Lea, Flood 2014) of seed ^ (sequence << 40 | step << 17 | 0x1ffff). */
+static uint64_t or_splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+static float or_penalized(float l, int cnt, float T, float r, int mode) {
+  if (mode == 0) {
+    float z = l / T;
+    return cnt > 0 ? z / r : z;
+  }
+  float z = l;
+  for (int k = 0; k < cnt; ++k) z = z > 0.0f ? z / r : z * r;
+  return z / T;
+}
+
+typedef struct { uint32_t key; int idx; } or_rank_t;
+static int or_rank_cmp(const void* pa, const void* pb) {
+  const or_rank_t* a = (const or_rank_t*)pa;
+  const or_rank_t* b = (const or_rank_t*)pb;
+  if (a->key != b->key) return a->key > b->key ? -1 : 1;
+  return a->idx < b->idx ? -1 : (a->idx > b->idx);
+}
+
+/* logits (M, V) fp16, counts (M, V) and step (M) updated as the kernel does; kept (M, V) optional
+ * output of the kept set (1/0). */
+void or_sample(const uint16_t* logits, int32_t* counts, uint32_t* step, int M, int V, float T, float top_p,
+               float r, int mode, uint64_t seed, int64_t* next, uint8_t* kept_out) {
+  float* z = (float*)malloc(sizeof(float) * V);
+  uint64_t* E = (uint64_t*)malloc(sizeof(uint64_t) * V);
+  or_rank_t* rk = (or_rank_t*)malloc(sizeof(or_rank_t) * V);
+  uint8_t* kept = (uint8_t*)malloc(V);
+  for (int b = 0; b < M; ++b) {
+    const uint16_t* lg = logits + (size_t)b * V;
+    int32_t* cn = counts + (size_t)b * V;
+    float m = -INFINITY;
+    for (int i = 0; i < V; ++i) {
+      z[i] = or_penalized(or_h2f(lg[i]), cn[i], T, r, mode);
+      m = fmaxf(m, z[i]);
+    }
+    uint64_t Z = 0;
+    for (int i = 0; i < V; ++i) {
+      float e = or_expf(z[i] - m);
+      memcpy(&rk[i].key, &e, 4);
+      rk[i].idx = i;
+      E[i] = (uint64_t)(e * 1099511627776.0f);
+      Z += E[i];
+    }
+    uint64_t thr = (uint64_t)((double)top_p * (double)Z);
+    if (top_p >= 1.0f || thr >= Z) {
+      memset(kept, 1, V);
+    } else {
+      qsort(rk, V, sizeof(or_rank_t), or_rank_cmp);
+      uint64_t S = 0;
+      for (int k = 0; k < V; ++k) {
+        kept[rk[k].idx] = S <= thr;
+        S += E[rk[k].idx];
+      }
+    }
+    uint64_t S = 0;
+    for (int i = 0; i < V; ++i) if (kept[i]) S += E[i];
+    uint64_t h = or_splitmix64(seed ^ (((uint64_t)b << 40) | ((uint64_t)(step[b] & 0x7fffffu) << 17) | 0x1ffffull));
+    uint64_t R = (uint64_t)(((unsigned __int128)h * S) >> 64);
+    uint64_t acc = 0;
+    int bi = V;
+    for (int i = 0; i < V; ++i) {
+      if (!kept[i]) continue;
+      acc += E[i];
+      if (acc > R) { bi = i; break; }
+    }
+    int tok = bi < V ? bi : 0;
+    next[b] = tok;
+    cn[tok] += 1;
+    step[b] += 1u;
+    if (kept_out) memcpy(kept_out + (size_t)b * V, kept, V);
+  }
+  free(z); free(E); free(rk); free(kept);
+}

@@ -20,6 +20,12 @@ Which check pins which function (each test named in tests/):
   gate_norm, lora, layer   layer_forward (test_oracle_vs_reference.py); closed forms for the SSM
                            (B=0 decay, x=0 readout, D skip)
   LM head + argmax         float64 matmul + numpy argmax first-index rule (test_oracle_pins.py)
+  sampling (or_sample)     top_p = 0 equals the argmax of the penalized logits; the kept set
+                           against a float64 NumPy evaluation of the reference's sort/cumsum
+                           drop rule (gen_test.py:76-80) on logits with separated masses; the
+                           penalty modes against their closed forms; the draw frequencies
+                           against softmax over the kept set (chi-square); the inverse-CDF
+                           draw against a NumPy restatement (test_sampling.py)
 """
 from __future__ import annotations
 
@@ -203,6 +209,23 @@ def lm_head(w, xf: np.ndarray):
     else:
         lib().or_lm_head(_p(xh), None, None, _p(_h(w.emb)), 0, M, V, D, _p(logits), _p(nxt))
     return logits.view(np.float16), nxt
+
+
+def sample(logits16: np.ndarray, counts: np.ndarray, step: np.ndarray, temperature: float, top_p: float,
+           penalty: float, mode: int, seed: int, want_kept: bool = False):
+    """The sampling head's definition (or_sample). counts (M, V) int32 and step (M) uint32 are
+    updated in place as the kernel does. Returns next (M,) int64 [, kept (M, V) bool]."""
+    lg = _h(logits16)
+    M, V = lg.shape
+    assert counts.dtype == np.int32 and counts.flags["C_CONTIGUOUS"] and counts.shape == (M, V)
+    assert step.dtype == np.uint32 and step.flags["C_CONTIGUOUS"] and step.shape == (M,)
+    nxt = np.empty(M, np.int64)
+    kept = np.empty((M, V), np.uint8) if want_kept else None
+    f = lib().or_sample
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                  ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    f(_p(lg), _p(counts), _p(step), M, V, temperature, top_p, penalty, mode, seed, _p(nxt), _p(kept))
+    return (nxt, kept.astype(bool)) if want_kept else nxt
 
 
 # ---------------------------------------------------------------- whole model -------------------
