@@ -77,11 +77,15 @@ struct FusedLds {
 
 // Epilogue inputs of one output row, loaded ahead of the GEMV. Thread t works on row t / 16 of
 // the group with wave partial / LoRA rank s = t % 16; threads s < M also finalize sequence s.
+// Every field is a raw load (each in its own register), made unconditionally from clamped
+// indices and used only in the epilogue: loads complete in issue order, so converting or
+// packing a loaded value here (or a load inside a branch, whose join waits for all loads) would
+// make the workgroup wait for the weight stream before its prologue starts.
 struct EpiRow {
   uint32_t cw01, cw23;
-  float bias, A;             // dt rows: dt_bias and A = -exp(A_log) of the head
-  int8_t la;                 // LoRA A[n][s]
-  uint16_t ws, as, cs0, cs1, cs2, cb, xres;
+  float bias, alog;          // dt rows: dt_bias and A_log of the head (A = -exp(A_log) later)
+  int la;                    // LoRA A[n][s]
+  uint32_t ws, as, cs01, cs2, cb, xres;  // cs01: conv state words 0 | 1 << 16, one (unaligned) load
 };
 
 // Conv-state update of one row, stored after the row group's outputs.
@@ -99,19 +103,14 @@ struct PIn {
 
 template <int M, bool OUT>
 __device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K, const float* norm_w) {
-  const int tid = threadIdx.x;
+  // unconditional loads from a clamped column (threads >= K / 8 re-read column 0; their values
+  // are never used): a load inside a branch makes the compiler wait for all loads at the join
+  const int t = (int)threadIdx.x < K / 8 ? (int)threadIdx.x : 0;
 #pragma unroll
-  for (int m = 0; m < M; ++m) pi.av[m] = u32x4{0u, 0u, 0u, 0u};
-  pi.w0 = f32x4{0.f, 0.f, 0.f, 0.f};
-  pi.w1 = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (tid < K / 8) {
-    if (!OUT) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) pi.av[m] = *(const u32x4*)(act + (size_t)m * K + 8 * tid);
-    }
-    pi.w0 = *(const f32x4*)(norm_w + 8 * tid);
-    pi.w1 = *(const f32x4*)(norm_w + 8 * tid + 4);
-  }
+  for (int m = 0; m < M; ++m)
+    pi.av[m] = OUT ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(act + (size_t)m * K + 8 * t);
+  pi.w0 = *(const f32x4*)(norm_w + 8 * t);
+  pi.w1 = *(const f32x4*)(norm_w + 8 * t + 4);
 }
 
 __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t* bits, int grp, int K) {
@@ -124,32 +123,35 @@ __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t*
   }
 }
 
-// Row n = 64 grp + tid / 16; the sequence-specific inputs for m = tid % 16 < M.
+// Row n = 64 grp + tid / 16; the sequence-specific inputs for m = tid % 16 < M (threads
+// s >= M and rows past N load row / sequence 0's values, never used).
 template <int M, bool IN>
 __device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
-  EpiRow e{};
-  const int tid = threadIdx.x, s = tid & 15, n = grp * 64 + (tid >> 4);
+  EpiRow e;
+  const int tid = threadIdx.x, s = tid & 15, n0 = grp * 64 + (tid >> 4);
   const int N = IN ? a.IPO : a.D;
-  if (n >= N) return e;
+  const int n = n0 < N ? n0 : N - 1;
+  const int m = s < M ? s : 0;
   e.la = (IN ? a.in_lA : a.out_lA)[(size_t)n * DFSSM_LORA_R + s];
   e.as = (IN ? a.in_lAs : a.out_lAs)[n];
-  if (s >= M) return e;
-  const int m = s;
   e.ws = (IN ? a.in_ws : a.out_ws)[n];
   if (IN) {
-    const int ch = n - a.DI, dtr = n - (2 * a.DI + 2 * a.N);
-    if (ch >= 0 && ch < a.C) {
-      const uint16_t* cs = a.conv + ((size_t)m * a.C + ch) * 3;
-      e.cs0 = cs[0]; e.cs1 = cs[1]; e.cs2 = cs[2];
-      const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
-      e.cw01 = wc[0]; e.cw23 = wc[1];
-      e.cb = a.conv_b[ch];
-    } else if (dtr >= 0) {
-      e.bias = a.dt_bias[dtr];
-      e.A = -dev_expf(a.A_log[dtr]);
-    }
+    int ch = n - a.DI, dtr = n - (2 * a.DI + 2 * a.N);
+    ch = ch < 0 ? 0 : (ch >= a.C ? a.C - 1 : ch);
+    dtr = dtr < 0 ? 0 : dtr;
+    const uint16_t* cs = a.conv + ((size_t)m * a.C + ch) * 3;
+    __builtin_memcpy(&e.cs01, cs, 4);
+    e.cs2 = cs[2];
+    const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
+    e.cw01 = wc[0]; e.cw23 = wc[1];
+    e.cb = a.conv_b[ch];
+    e.bias = a.dt_bias[dtr];
+    e.alog = a.A_log[dtr];
+    e.xres = 0u;
   } else {
     e.xres = a.x[(size_t)m * a.D + n];
+    e.cs01 = e.cs2 = e.cw01 = e.cw23 = e.cb = 0u;
+    e.bias = e.alog = 0.0f;
   }
   return e;
 }
@@ -390,7 +392,7 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
   const int tid = threadIdx.x, s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
   const int n = grp * 64 + j;
-  const float aq = r16((float)er.la * h2f(er.as));
+  const float aq = r16((float)(int8_t)er.la * h2f((uint16_t)er.as));
   int accm = 0;
   double lom = 0.0;
 #pragma unroll
@@ -404,7 +406,7 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
   }
   if (s >= M || n >= N) return cp;
   const int m = s;
-  const float y = r16(r16(r16((float)accm) * L.xs[m]) * h2f(er.ws));
+  const float y = r16(r16(r16((float)accm) * L.xs[m]) * h2f((uint16_t)er.ws));
   float out = r16((float)lom + y);
   if (IN) {
     const int ch = n - a.DI, dtr = n - (2 * a.DI + 2 * a.N);
@@ -414,18 +416,18 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
     } else if (ch < a.C) {
       // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later)
       const uint16_t xo = f2h(out);
-      cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, er.cs1, er.cs2, xo};
+      cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, (uint16_t)(er.cs01 >> 16), (uint16_t)er.cs2, xo};
       const float xv = h2f(xo);
-      float o = h2f(er.cs0) * h2f((uint16_t)er.cw01);
-      o = o + h2f(er.cs1) * h2f((uint16_t)(er.cw01 >> 16));
-      o = o + h2f(er.cs2) * h2f((uint16_t)er.cw23);
+      float o = h2f((uint16_t)er.cs01) * h2f((uint16_t)er.cw01);
+      o = o + h2f((uint16_t)(er.cs01 >> 16)) * h2f((uint16_t)(er.cw01 >> 16));
+      o = o + h2f((uint16_t)er.cs2) * h2f((uint16_t)er.cw23);
       o = o + xv * h2f((uint16_t)(er.cw23 >> 16));
-      o = o + h2f(er.cb);
+      o = o + h2f((uint16_t)er.cb);
       const float sig = 1.0f / (1.0f + dev_expf(-o));
       out = o * sig;
     } else {  // dt row of head dtr
       const float dt = dev_log1pf(dev_expf(out + er.bias));
-      const float abar = dev_expf(dt * er.A);
+      const float abar = dev_expf(dt * -dev_expf(er.alog));
       uint64_t* w = a.dtT + ((size_t)m * a.H + dtr) * 2;
       st_dev(w, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, dt));
       st_dev(w + 1, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, abar));
@@ -433,7 +435,7 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
     }
     st_dev(a.projT + (size_t)m * a.IPO + n, tagged(tag, f2h(out)));
   } else {
-    a.x[(size_t)m * a.D + n] = f2h(h2f(er.xres) + out);
+    a.x[(size_t)m * a.D + n] = f2h(h2f((uint16_t)er.xres) + out);
   }
   return cp;
 }
@@ -530,8 +532,15 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   __shared__ FusedLds<M> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, wg = blockIdx.x;
-  const uint32_t epoch = ld_dev(a.launches + wg) + 1u;  // used first at the phase-A stores
-  const uint32_t tag = epoch & 0xffffu;
+  // The launch's epoch is the first load; its tag is derived where it is used (tag_now): the
+  // empty asm keeps the compiler from computing it right after a branch join near the kernel
+  // start, where it can only wait for every load issued so far (the weight stream included).
+  const uint32_t epoch_raw = ld_dev(a.launches + wg);
+  auto tag_now = [&]() {
+    uint32_t v = epoch_raw;
+    asm volatile("" : "+v"(v));
+    return (v + 1u) & 0xffffu;
+  };
   const int gA = (a.IPO + 63) / 64, gC = a.D / 64;
   const int NI = a.H * (a.P / 16), items = M * NI;
   uint32_t* hA = a.hT;
@@ -539,20 +548,20 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
 
   // ---- loads that do not depend on the activations ----
   u32x4 wa[kFMaxCPW];
-  EpiRow ea{};
+  EpiRow ea = {};
   PIn<M> pa;
-  if (wg < gA) {
+  if (wg < gA) {  // x first: the prologue needs it before the weights
+    load_pin<M, false>(pa, a.x, a.D, a.ln_w);
     load_bits(wa, a.in_bits, wg, a.D);
     ea = load_epi<M, true>(a, wg);
-    load_pin<M, false>(pa, a.x, a.D, a.ln_w);
   }
   // state row of this workgroup's first SSM item (the other items' rows load before phase B's polls)
-  f32x2 h0 = {0.f, 0.f};
-  if (wg < items) h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg)));
+  // (unconditional, from a clamped item: see load_pin)
+  const f32x2 h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg < items ? wg : items - 1)));
 
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
   if (wg < gA) {
-    prologue<M, false>(L, pa, nullptr, a.D, tag, a.err);
+    prologue<M, false>(L, pa, nullptr, a.D, 0u, a.err);  // no polls in the IN prologue
     for (int grp = wg; grp < gA; grp += G) {
       if (grp != wg) {
         load_bits(wa, a.in_bits, grp, a.D);
@@ -560,17 +569,18 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       }
       const uint32_t hv = lora_issue(hA, M);
       gemv_partials<M>(L, wa, a.D);
+      const uint32_t tag = tag_now();
       lora_finish<M>(L, hA, hv, tag, a.err);
       __syncthreads();
       store_conv(epilogue<M, true>(L, a, ea, grp, tag));
       __syncthreads();
     }
   } else if (wg < gA + DFSSM_LORA_R) {
-    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag, a.err);
+    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err);
   }
   // ---- phase B: SSM + gate ----
   u32x4 wc[kFMaxCPW];
-  EpiRow ec{};
+  EpiRow ec = {};
   if (wg < gC) {  // phase-C weights, loaded while phase B runs
     load_bits(wc, a.out_bits, wg, a.DI);
     ec = load_epi<M, false>(a, wg);
@@ -588,6 +598,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
         dk[k] = a.Dp[t.head];
       }
     }
+    const uint32_t tag = tag_now();
     for (int k = 0; k < nk; ++k) poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
     __syncthreads();
 #pragma unroll
@@ -599,6 +610,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     __syncthreads();  // LDS reuse after phase A
     PIn<M> pc;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
+    const uint32_t tag = tag_now();
     prologue<M, true>(L, pc, a.gT, a.DI, tag, a.err);
     for (int grp = wg; grp < gC; grp += G) {
       if (grp != wg) {
@@ -614,10 +626,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     }
   } else if (wg < gC + DFSSM_LORA_R) {
     __syncthreads();
-    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag, a.err);
+    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err);
   }
   __syncthreads();  // every wave of this workgroup has read its launch count
-  if (tid == 0) st_dev(a.launches + wg, epoch);
+  if (tid == 0) st_dev(a.launches + wg, epoch_raw + 1u);
 }
 
 static int fused_grid() {
