@@ -41,10 +41,27 @@ constexpr int kFT = 1024;
 constexpr int kFW = kFT / 64;
 constexpr int kFMaxK = 5120;
 constexpr int kFMaxCPW = (kFMaxK / 128 + kFW - 1) / kFW;
+// out_proj in 16-row groups: thread t owns row t % 16 and half-chunks u = t / 16 + 64 j
+constexpr int kC16 = (2 * (kFMaxK / 128) + 63) / 64;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kSpinMax = 1u << 18;
 constexpr int kMaxItems = kFW / 2;  // SSM items per workgroup (two polling waves each)
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Thread and workgroup index, opaque to the optimizer: addresses derived from them are computed
+// where they are used instead of being hoisted to the kernel start and kept live (in registers)
+// across all three phases.
+__device__ __forceinline__ int tix() {
+  int t = __builtin_amdgcn_workitem_id_x();
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int bix() {
+  int t = __builtin_amdgcn_workgroup_id_x();
+  asm volatile("" : "+s"(t));
+  return t;
+}
 
 template <class T>
 __device__ __forceinline__ T ld_dev(const T* p) {
@@ -105,7 +122,7 @@ template <int M, bool OUT>
 __device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K, const float* norm_w) {
   // unconditional loads from a clamped column (threads >= K / 8 re-read column 0; their values
   // are never used): a load inside a branch makes the compiler wait for all loads at the join
-  const int t = (int)threadIdx.x < K / 8 ? (int)threadIdx.x : 0;
+  const int t = tix() < K / 8 ? tix() : 0;
 #pragma unroll
   for (int m = 0; m < M; ++m)
     pi.av[m] = OUT ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(act + (size_t)m * K + 8 * t);
@@ -114,7 +131,7 @@ __device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K,
 }
 
 __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t* bits, int grp, int K) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, CH = K / 128;
+  const int lane = tix() & 63, wave = tix() >> 6, CH = K / 128;
   const u32x4* b = (const u32x4*)bits + (size_t)grp * CH * 64 + lane;
 #pragma unroll
   for (int j = 0; j < kFMaxCPW; ++j) {
@@ -123,12 +140,25 @@ __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t*
   }
 }
 
-// Row n = 64 grp + tid / 16; the sequence-specific inputs for m = tid % 16 < M (threads
+// 16-row group `grp` (rows 16 grp .. 16 grp + 15 of the 64-row tiles): thread (row r = lane % 16,
+// u = 4 wave + lane / 16 + 64 j) loads words 2h, 2h + 1 of chunk c, cu = u = 2c + h.
+__device__ __forceinline__ void load_bits16(u32x2 (&wb)[kC16], const uint32_t* bits, int grp, int K) {
+  const int lane = tix() & 63, wave = tix() >> 6, CH = K / 128;
+  const u32x4* b = (const u32x4*)bits + (size_t)(grp >> 2) * CH * 64 + (grp & 3) * 16 + (lane & 15);
+#pragma unroll
+  for (int j = 0; j < kC16; ++j) {
+    const int cu = 4 * wave + (lane >> 4) + 64 * j;
+    wb[j] = cu < 2 * CH ? __builtin_nontemporal_load((const u32x2*)(b + (size_t)(cu >> 1) * 64) + (cu & 1))
+                        : u32x2{0u, 0u};
+  }
+}
+
+// Row n = RG grp + tid / 16; the sequence-specific inputs for m = tid % 16 < M (threads
 // s >= M and rows past N load row / sequence 0's values, never used).
-template <int M, bool IN>
+template <int M, bool IN, int RG = 64>
 __device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
   EpiRow e;
-  const int tid = threadIdx.x, s = tid & 15, n0 = grp * 64 + (tid >> 4);
+  const int tid = tix(), s = tid & 15, n0 = grp * RG + (tid >> 4);
   const int N = IN ? a.IPO : a.D;
   const int n = n0 < N ? n0 : N - 1;
   const int m = s < M ? s : 0;
@@ -210,7 +240,7 @@ __device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t 
 template <int M, bool OUT, class Body>
 __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K,
                                           uint32_t tag, int* err, Body body) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const bool has_v = tid < K / 8;
   const float wv[8] = {pi.w0[0], pi.w0[1], pi.w0[2], pi.w0[3], pi.w1[0], pi.w1[1], pi.w1[2], pi.w1[3]};
   bool ok = true;
@@ -257,9 +287,10 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
 
 // Projection prologue (GEMV workgroups): per row the amax, the quantization scale, and each
 // wave's bit planes of its own GEMV chunks (no barrier before the GEMV) with their sum q.
-template <int M, bool OUT>
+// CW: the wave's chunks are CW consecutive ones per round of CW * 16 (those its GEMV reads).
+template <int M, bool OUT, int CW = 1>
 __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K, uint32_t tag, int* err) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const int CH = K / 128;
   norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float mx) {
     const float wmax = wave_max_dpp_f32(mx);
@@ -271,7 +302,7 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
     const float xs = quant_scale(amax);
     if (tid == 0) L.xs[m] = xs;
     int qsum = 0;
-    for (int c = wave; c < CH; c += kFW) {
+    for (int c = CW * wave; c < CH; c += (c % CW == CW - 1) ? CW * (kFW - 1) + 1 : 1) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int k0 = 128 * c + 64 * hh;
@@ -293,7 +324,7 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
 template <int M, bool OUT>
 __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT, int K, const float* norm_w,
                           const uint16_t* lBq, int r, uint32_t* hout, uint32_t tag, int* err) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const bool has_v = tid < K / 8;
   PIn<M> pi;
   load_pin<M, OUT>(pi, x, K, norm_w);
@@ -325,7 +356,7 @@ __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT,
 // Packed-bit GEMV of one 64-row group: per-wave partials into L.T (no barrier).
 template <int M>
 __device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[kFMaxCPW], int K) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tix() & 63, wave = tix() >> 6;
   const int CH = K / 128;
   uint32_t cnt[M][8];
 #pragma unroll
@@ -365,15 +396,62 @@ __device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[
   }
 }
 
+// Packed-bit GEMV of one 16-row group: each thread two words of one row, the four threads of a
+// wave that share a row summed by lane exchange; per-wave partials into L.T rows 0..15.
+template <int M>
+__device__ __forceinline__ void gemv_partials16(FusedLds<M>& L, const u32x2 (&wb)[kC16], int K) {
+  const int lane = tix() & 63, wave = tix() >> 6;
+  const int CH = K / 128;
+  uint32_t cnt[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) cnt[m][b] = 0u;
+#pragma unroll
+  for (int j = 0; j < kC16; ++j) {
+    const int cu = 4 * wave + (lane >> 4) + 64 * j;
+    if (cu < 2 * CH) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t w = wb[j][i];
+        const int word = 2 * cu + i;  // = 4 c + 2 h + i
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const u32x4 p0 = *(const u32x4*)&L.planes[m][word][0];
+          const u32x4 p1 = *(const u32x4*)&L.planes[m][word][4];
+          cnt[m][0] += __builtin_popcount(w & p0[0]);
+          cnt[m][1] += __builtin_popcount(w & p0[1]);
+          cnt[m][2] += __builtin_popcount(w & p0[2]);
+          cnt[m][3] += __builtin_popcount(w & p0[3]);
+          cnt[m][4] += __builtin_popcount(w & p1[0]);
+          cnt[m][5] += __builtin_popcount(w & p1[1]);
+          cnt[m][6] += __builtin_popcount(w & p1[2]);
+          cnt[m][7] += __builtin_popcount(w & p1[3]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    int t = 0;
+#pragma unroll
+    for (int b = 0; b < 7; ++b) t += (int)(cnt[m][b] << b);
+    t -= (int)(cnt[m][7] << 7);
+    t += __shfl_xor(t, 16);
+    t += __shfl_xor(t, 32);
+    if (lane < 16) L.T[m][lane][wave] = t;
+  }
+}
+
 // LoRA intermediates of this phase (threads < 16 M): the first load is issued before the GEMV
 // (lora_issue), the poll completes after it (lora_finish) into L.hl; the caller then passes a
 // barrier.
 __device__ __forceinline__ uint32_t lora_issue(const uint32_t* hsrc, int M) {
-  return (int)threadIdx.x < M * DFSSM_LORA_R ? ld_dev(hsrc + threadIdx.x) : 0u;
+  return tix() < M * DFSSM_LORA_R ? ld_dev(hsrc + tix()) : 0u;
 }
 template <int M>
 __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc, uint32_t v, uint32_t tag, int* err) {
-  const int tid = threadIdx.x;
+  const int tid = tix();
   if (tid < M * DFSSM_LORA_R) {
     bool ok = true;
     if ((v >> 16) != tag) v = poll1(hsrc + tid, tag, ok, err);
@@ -386,12 +464,12 @@ __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc
 // sums (exact: integers, and exactly representable products in fp64); thread s = m then
 // finalizes sequence m. IN: z rows store the gate z sigma(z), x/B/C rows conv + SiLU, dt rows
 // softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x.
-template <int M, bool IN>
+template <int M, bool IN, int RG = 64>
 __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag) {
   ConvPend cp{nullptr, 0, 0, 0};
-  const int tid = threadIdx.x, s = tid & 15, j = tid >> 4;
+  const int tid = tix(), s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
-  const int n = grp * 64 + j;
+  const int n = grp * RG + j;
   const float aq = r16((float)(int8_t)er.la * h2f((uint16_t)er.as));
   int accm = 0;
   double lom = 0.0;
@@ -404,7 +482,7 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
       lom = lo;
     }
   }
-  if (s >= M || n >= N) return cp;
+  if (s >= M || j >= RG || n >= N) return cp;
   const int m = s;
   const float y = r16(r16(r16((float)accm) * L.xs[m]) * h2f((uint16_t)er.ws));
   float out = r16((float)lom + y);
@@ -460,7 +538,7 @@ __device__ __forceinline__ Item item_of(const FusedArgs& a, int it) {
 
 // This thread's two state columns of the item's row p = 16 pb + wave.
 __device__ __forceinline__ float* state_row(const FusedArgs& a, const Item& t) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tix() & 63, wave = tix() >> 6;
   return a.h + (((size_t)t.m * a.H + t.head) * a.P + t.pb * 16 + wave) * a.N + 2 * lane;
 }
 
@@ -469,7 +547,7 @@ __device__ __forceinline__ float* state_row(const FusedArgs& a, const Item& t) {
 // lanes 32 and 33 dt and exp(dt A).
 template <int M>
 __device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, uint32_t tag) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tix() & 63, wave = tix() >> 6;
   const uint32_t* pr = a.projT + (size_t)t.m * a.IPO;
   bool ok = true;
   if (wave == 2 * k) {
@@ -508,7 +586,7 @@ __device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item&
 template <int M>
 __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, f32x2 h0,
                                          float Dh, uint32_t tag) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tix() & 63, wave = tix() >> 6;
   const int p = t.pb * 16 + wave;
   const ItemLds& I = L.item[k];
   const uint32_t bp = I.bc[lane], cp = I.bc[DFSSM_WAVE + lane];
@@ -527,11 +605,12 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
   }
 }
 
-template <int M>
+// RC: rows per out_proj group (16, or 64 when D / 16 + 16 groups do not fit the grid).
+template <int M, int RC>
 __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   __shared__ FusedLds<M> L;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = gridDim.x, wg = blockIdx.x;
+  const int tid = tix(), lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, wg = bix();
   // The launch's epoch is the first load; its tag is derived where it is used (tag_now): the
   // empty asm keeps the compiler from computing it right after a branch join near the kernel
   // start, where it can only wait for every load issued so far (the weight stream included).
@@ -541,7 +620,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     asm volatile("" : "+v"(v));
     return (v + 1u) & 0xffffu;
   };
-  const int gA = (a.IPO + 63) / 64, gC = a.D / 64;
+  const int gA = (a.IPO + 63) / 64, gC = a.D / RC;
   const int NI = a.H * (a.P / 16), items = M * NI;
   uint32_t* hA = a.hT;
   uint32_t* hC = a.hT + M * DFSSM_LORA_R;
@@ -579,11 +658,13 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err);
   }
   // ---- phase B: SSM + gate ----
-  u32x4 wc[kFMaxCPW];
+  u32x4 wc[RC == 16 ? 1 : kFMaxCPW];
+  u32x2 wc16[kC16];
   EpiRow ec = {};
   if (wg < gC) {  // phase-C weights, loaded while phase B runs
-    load_bits(wc, a.out_bits, wg, a.DI);
-    ec = load_epi<M, false>(a, wg);
+    if constexpr (RC == 16) load_bits16(wc16, a.out_bits, wg, a.DI);
+    else load_bits(wc, a.out_bits, wg, a.DI);
+    ec = load_epi<M, false, RC>(a, wg);
   }
   const int nk = wg < items ? (items - 1 - wg) / G + 1 : 0;  // <= kMaxItems
   if (nk > 0) {
@@ -611,17 +692,19 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     PIn<M> pc;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
     const uint32_t tag = tag_now();
-    prologue<M, true>(L, pc, a.gT, a.DI, tag, a.err);
+    prologue<M, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);
     for (int grp = wg; grp < gC; grp += G) {
       if (grp != wg) {
-        load_bits(wc, a.out_bits, grp, a.DI);
-        ec = load_epi<M, false>(a, grp);
+        if constexpr (RC == 16) load_bits16(wc16, a.out_bits, grp, a.DI);
+        else load_bits(wc, a.out_bits, grp, a.DI);
+        ec = load_epi<M, false, RC>(a, grp);
       }
       const uint32_t hv = lora_issue(hC, M);
-      gemv_partials<M>(L, wc, a.DI);
+      if constexpr (RC == 16) gemv_partials16<M>(L, wc16, a.DI);
+      else gemv_partials<M>(L, wc, a.DI);
       lora_finish<M>(L, hC, hv, tag, a.err);
       __syncthreads();
-      (void)epilogue<M, false>(L, a, ec, grp, tag);
+      (void)epilogue<M, false, RC>(L, a, ec, grp, tag);
       __syncthreads();
     }
   } else if (wg < gC + DFSSM_LORA_R) {
@@ -639,7 +722,7 @@ static int fused_grid() {
   if (grid[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<4>),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<4, 64>),
                                                      kFT, 0) != hipSuccess || per_cu < 1)
       return 0;
     // one workgroup per CU: all co-resident whatever the per-CU occupancy
@@ -653,6 +736,9 @@ static int fused_grid() {
 // seen every item's output, which then implies that all reads of x are done. A workgroup polls
 // at most kMaxItems items (two waves each). The state width (d_state 128 = two columns per lane)
 // and P % 16 == 0 are checked with the model dims.
+// Rows per out_proj group: 16 when the grid holds D / 16 groups and their 16 LoRA workgroups.
+static int out_rows(int D) { return D / 16 + DFSSM_LORA_R <= fused_grid() ? 16 : 64; }
+
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
   const int G = fused_grid();
   const int gA = (IPO + 63) / 64, gC = D / 64, items = M * H * (P / 16);
@@ -664,7 +750,7 @@ bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
 // out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.
 __global__ void dequant_lora_b_kernel(const int8_t* __restrict__ B, const uint16_t* __restrict__ Bs, int K,
                                       uint16_t* __restrict__ out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = bix() * blockDim.x + tix();
   if (i < DFSSM_LORA_R * K) out[i] = f2h((float)B[i] * h2f(Bs[i / K]));
 }
 
@@ -677,13 +763,20 @@ hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uin
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
   if (!fused_layer_supported(M, a.IPO, a.D, a.DI, a.H, a.P)) return hipErrorNotSupported;
   const int G = fused_grid();
+  const bool r16 = out_rows(a.D) == 16;
+#define DFSSM_FUSED(MM)                                                                       \
+  case MM:                                                                                    \
+    if (r16) hipLaunchKernelGGL((layer_fused_kernel<MM, 16>), dim3(G), dim3(kFT), 0, s, a);   \
+    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64>), dim3(G), dim3(kFT), 0, s, a);       \
+    break;
   switch (M) {
-    case 1: hipLaunchKernelGGL(layer_fused_kernel<1>, dim3(G), dim3(kFT), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(layer_fused_kernel<2>, dim3(G), dim3(kFT), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(layer_fused_kernel<3>, dim3(G), dim3(kFT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(layer_fused_kernel<4>, dim3(G), dim3(kFT), 0, s, a); break;
+    DFSSM_FUSED(1)
+    DFSSM_FUSED(2)
+    DFSSM_FUSED(3)
+    DFSSM_FUSED(4)
     default: return hipErrorInvalidValue;
   }
+#undef DFSSM_FUSED
   return hipGetLastError();
 }
 
