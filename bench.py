@@ -107,6 +107,26 @@ def time_prefill(m, prompts):
     return e0.elapsed_time(e1)
 
 
+def time_state_df(m, reps=20):
+    """One density-field quantization of the whole state (dfssm_state_density_field with
+    sigma-delta, K = 8 bank), averaged over `reps` calls timed with HIP events on the library's
+    stream. Returns (us per call, bytes per call): the state and the error are read and written."""
+    import torch
+    from df_ssm_inference import StateDensityField
+    df = StateDensityField.random(K=8, num_banks=64)
+    m.apply_state_density_field(df, 0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for c in range(reps):
+        m.apply_state_density_field(df, c)
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    m.reset_state()
+    return us, 4 * m.h_state.numel() * 4
+
+
 def time_decode(m, prompts, steps, warmup):
     import torch
     m.reset_state()
@@ -266,6 +286,11 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
                "sample_kernel_us_per_launch": round(samp_us, 2)}
     log(f"sampled decode batch {B}: {samp_ms * 1e3:.1f} us/step, {sampled['tok_s']:.0f} tok/s "
         f"(sampler {samp_us:.1f} us/launch)")
+    df_us, df_bytes = time_state_df(m)
+    state_df = {"us_per_call": round(df_us, 2), "bytes_per_call": df_bytes,
+                "gbs": round(df_bytes / (df_us * 1e-6) / 1e9, 1),
+                "note": "quantization of every layer's state at a chunk boundary (once per block_len tokens)"}
+    log(f"density-field state batch {B}: {df_us:.1f} us per boundary, {state_df['gbs']:.0f} GB/s")
     kt = time_kernels(m)
     phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
                 "head+argmax": 3, "layer (one launch)": 4}
@@ -284,7 +309,7 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
                              "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / PEAK_GBS, 4),
                              "roofline_tok_s": round(B / (step_bytes / (PEAK_GBS * 1e9)), 1)},
            "kernels": kernels, "dispatch_us_per_launch": round(kt["empty"][0], 2), "prefill": prefill,
-           "sampled": sampled}
+           "sampled": sampled, "state_df": state_df}
     del m
     torch.cuda.empty_cache()
     return res, w, prompts
@@ -416,6 +441,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": main_res["prefill"],
         "sampled": main_res["sampled"],
+        "state_df": main_res["state_df"],
     }
     if second:
         out["batch2"] = {"batch": second["batch"], "tok_s": second["tok_s"], "ms_per_step": second["ms_per_step"],

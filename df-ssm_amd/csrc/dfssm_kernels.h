@@ -226,6 +226,17 @@ hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s);
 size_t head_digit_bytes(int M, int D);  // HeadArgs::hdig size for the batched int8 head
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s);
 hipError_t launch_sample(const SampleArgs& a, int batch, hipStream_t s);
+
+// Density-field state quantization at a chunk boundary: rows of 128 fp32 values.
+constexpr int kStateDfMaxKK = 1024;
+struct StateDfArgs {
+  float* h;                 // (rows, 128) state, quantized in place
+  float* sd_error;          // (rows, 128) sigma-delta error, updated in place; null = none
+  const float* thresholds;  // (kk) sorted thresholds of the bank
+  long long rows;
+  int kk, sd_bits;          // sd_bits >= 32: the error is kept unquantized
+};
+hipError_t launch_state_df(const StateDfArgs& a, hipStream_t s);
 hipError_t launch_conv_seq(const ConvSeqArgs& a, int batch, hipStream_t s);
 hipError_t launch_ssm_scan(const ScanArgs& a, int batch, hipStream_t s);
 hipError_t launch_last_rows(const uint16_t* src, uint16_t* dst, int batch, int T, int D, hipStream_t s);

@@ -66,6 +66,35 @@ def _dev(a: np.ndarray, dev) -> torch.Tensor:
     return torch.from_numpy(a).to(dev)
 
 
+class StateDensityField:
+    """Density-field state at inference (df_ssd_scan, training/df_ssm_mamba2_distill_dfw.py:114-173):
+    thresholds (num_banks, K*K) per-bank sorted thresholds (SprayBank.thresholds, :79-91; rows are
+    sorted here), block_len the chunk length, sigma_delta and sd_bits as DensityFieldConfig
+    (:96-103)."""
+
+    def __init__(self, thresholds, block_len: int = 64, sigma_delta: bool = True, sd_bits: int = 8):
+        t = np.sort(np.asarray(thresholds, np.float32), axis=-1)
+        if t.ndim != 2 or not 1 <= t.shape[1] <= 1024:
+            raise ValueError("thresholds must be (num_banks, K*K) with K*K <= 1024")
+        if block_len < 1 or sd_bits < 1:
+            raise ValueError("block_len and sd_bits must be >= 1")
+        self.thresholds = np.ascontiguousarray(t)
+        self.block_len, self.sigma_delta, self.sd_bits = int(block_len), bool(sigma_delta), int(sd_bits)
+        self._dev = {}
+
+    @classmethod
+    def random(cls, K: int = 8, num_banks: int = 256, seed: int = 0, **kw):
+        """Bank of uniform sorted thresholds, as SprayBank.__init__ draws them (torch.rand)."""
+        g = torch.Generator().manual_seed(seed)
+        return cls(torch.rand(num_banks, K * K, generator=g).numpy(), **kw)
+
+    def device_thresholds(self, device) -> torch.Tensor:
+        key = str(device)
+        if key not in self._dev:
+            self._dev[key] = torch.from_numpy(self.thresholds).to(device)
+        return self._dev[key]
+
+
 class DFSSMModel:
     def __init__(self, path, device="cuda", batch_size=1, weights: Optional[DFSSMWeights] = None):
         self.device = _require_gpu(device)
@@ -192,6 +221,63 @@ class DFSSMModel:
     def reset_state(self):
         self.h_state.zero_()
         self.conv_state.zero_()
+        if getattr(self, "_df_err", None) is not None:
+            self._df_err.zero_()
+
+    # ------------------------------------------------------------------ density-field state
+    def apply_state_density_field(self, df: "StateDensityField", chunk: int) -> None:
+        """Quantize every layer's SSM state as df_ssd_scan does at the end of chunk `chunk`
+        (training/df_ssm_mamba2_distill_dfw.py:139-165), with bank chunk % num_banks and, if
+        df.sigma_delta, the sigma-delta error carried between chunks (zeroed by reset_state)."""
+        R = df.device_thresholds(self.device)
+        err = None
+        if df.sigma_delta:
+            if getattr(self, "_df_err", None) is None:
+                self._df_err = torch.zeros_like(self.h_state)
+            err = self._df_err
+        bank = R[chunk % R.shape[0]]
+        _C.check(_C.lib().dfssm_state_density_field(
+            self.h_state.data_ptr(), None if err is None else err.data_ptr(), self.h_state.numel() // 128,
+            self.cfg.d_state, bank.data_ptr(), R.shape[1], df.sd_bits, _C.stream()), "state_density_field")
+
+    def _generate_state_df(self, n_tokens: int, prompt: torch.Tensor, df: "StateDensityField"):
+        """Greedy decode with the density-field state: the prompt is prefilled in segments that
+        end at chunk boundaries and the steps run in graphs that do not cross one; after the
+        token at position t (from 0, prompt included) with (t + 1) % block_len == 0 the state
+        is quantized with chunk index (t + 1) / block_len - 1."""
+        L = df.block_len
+        pos = 0
+
+        def boundary():
+            if pos % L == 0:
+                self.apply_state_density_field(df, pos // L - 1)
+
+        if self._graph is None:
+            self._capture_graph()
+        body = prompt[:, :-1]
+        while pos < body.shape[1]:
+            n = min(L - pos % L, body.shape[1] - pos)
+            self.prefill(body[:, pos:pos + n])
+            pos += n
+            boundary()
+        torch.cuda.synchronize(self.device)
+        start = time.perf_counter()
+        self._tok.copy_(prompt[:, -1])
+        self._graph.replay()
+        out = [self._next.clone()[:, None]]
+        pos += 1
+        boundary()
+        done = 1
+        while done < n_tokens:
+            s = min(8, n_tokens - done, L - pos % L)
+            g, hist = self._gen_graph(s)
+            g.replay()
+            out.append(hist.t().clone())
+            done += s
+            pos += s
+            boundary()
+        torch.cuda.synchronize(self.device)
+        return torch.cat(out, dim=1)[:, :n_tokens], time.perf_counter() - start
 
     # ------------------------------------------------------------------ steps
     def _decode(self, tokens: Optional[torch.Tensor], logits: Optional[torch.Tensor], nxt: torch.Tensor, fuse: bool):
@@ -362,7 +448,7 @@ class DFSSMModel:
         return torch.cat(out, dim=1)[:, :n_tokens], time.perf_counter() - start
 
     def generate(self, n_tokens=128, prompt=None, return_tokens=False, verbose=True, temperature=None,
-                 top_p=1.0, repetition_penalty=1.0, penalty_mode=0, seed=0):
+                 top_p=1.0, repetition_penalty=1.0, penalty_mode=0, seed=0, state_df=None):
         """Greedy decode timed like the reference's generate (df_ssm_inference.py:226-243).
 
         The timed region holds n_tokens decode steps: the first consumes the last prompt token
@@ -374,6 +460,9 @@ class DFSSMModel:
         repetition_penalty over the prompt and the tokens drawn so far; penalty_mode 0 is
         eval/gen_test.py:54-95, 1 the training script's :1066-1078), from a generator seeded by
         `seed`.
+
+        With state_df (a StateDensityField; greedy only), the SSM state is quantized at every
+        block_len-token chunk boundary as in training (apply_state_density_field).
         """
         B = self.batch_size
         self.reset_state()
@@ -382,6 +471,15 @@ class DFSSMModel:
         prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
         if prompt.dim() == 1:
             prompt = prompt.view(-1, 1)
+        if state_df is not None:
+            if temperature is not None:
+                raise ValueError("state_df is supported with greedy decoding only")
+            toks, elapsed = self._generate_state_df(n_tokens, prompt, state_df)
+            self.last_elapsed = elapsed
+            if verbose:
+                print(f"batch={B}  {n_tokens} steps (density-field state)  {n_tokens * B} total tokens")
+                print(f"  {elapsed*1000:.1f} ms  ({n_tokens * B / elapsed:.0f} tok/s total)")
+            return toks if return_tokens else None
         if temperature is not None:
             toks, elapsed = self._generate_sampled(n_tokens, prompt, temperature, top_p, repetition_penalty,
                                                    penalty_mode, seed)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 4
+#define DFSSM_ABI_VERSION 5
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
@@ -178,8 +178,9 @@ typedef struct dfssm_sample_params {
  * penalty and top-p, as eval/gen_test.py:54-95 and training/df_ssm_mamba2_distill_dfw.py:
  * 1066-1078 do with torch.sort / cumsum / multinomial. The top-p set is the reference's rule
  * (a token stays while the probability mass ranked above it is <= top_p) on exact fixed-point
- * masses; the draw is Gumbel-max with a counter-based generator (splitmix64 of seed, sequence,
- * step[b], token), deterministic for a given seed (torch's generator is not reproduced).
+ * masses E = floor(exp(z - max) 2^40); the draw is by inverse CDF over the kept tokens in index
+ * order, at R = floor(h S / 2^64) (S the kept mass, h = splitmix64 of seed, sequence and step[b]),
+ * deterministic for a given seed (torch's generator is not reproduced).
  * counts (batch, V) int32 holds each token's occurrences so far (the caller counts the prompt);
  * the drawn token is added, and step (batch) advances. next (batch) receives the tokens; if
  * x_next is non-NULL it receives their embedding (as dfssm_embed). workspace: the decode
@@ -207,6 +208,23 @@ size_t dfssm_prefill_workspace_bytes(const dfssm_dims* dims, int max_rows);
 int dfssm_prefill(const dfssm_model* model, const int64_t* tokens, int n_tokens, uint16_t* x,
                   const dfssm_state* state, void* workspace, void* prefill_workspace, int max_rows,
                   uint16_t* logits, int64_t* next, int fuse_next_embed, void* stream);
+
+/* ---- density-field state (row f4) ------------------------------------------------------- */
+/* Quantize SSM state rows at a chunk boundary as training/df_ssm_mamba2_distill_dfw.py:139-165
+ * (df_ssd_scan) does after every block_len tokens. The reference applies it in training only.
+ * Per row of d_state = 128 fp32 values:
+ *   mean and unbiased std (clamped to 1e-8), lo = mean - 3 std, range = max(6 std, 1e-8),
+ *   hs = clamp((h - lo) / range, 0, 1), hc = clamp(hs + e, 0, 1) (e = sd_error, if given),
+ *   q = (number of thresholds[0..kk) below hc) / kk  (SprayBank.quantize, :88-91),
+ *   e = round(clamp(hc - q, -1, 1) 2^(sd_bits-1)) / 2^(sd_bits-1)  (_quantize_error, :105-110;
+ *       unquantized for sd_bits >= 32),
+ *   h = q range + lo.
+ * h and sd_error are (rows, 128), updated in place; sd_error NULL = no sigma-delta.
+ * thresholds: the kk sorted thresholds of the bank for this chunk (bank = chunk % num_banks),
+ * 1 <= kk <= 1024. Both row sums are fp64 over a fixed adjacent-pair tree, so results are
+ * deterministic. */
+int dfssm_state_density_field(float* h, float* sd_error, int64_t rows, int d_state,
+                              const float* thresholds, int kk, int sd_bits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -602,3 +602,52 @@ void or_sample(const uint16_t* logits, int32_t* counts, uint32_t* step, int M, i
   }
   free(z); free(E); free(rk); free(kept);
 }
+
+/* Density-field state quantization at a chunk boundary, training/df_ssm_mamba2_distill_dfw.py:
+ * 139-165 (df_ssd_scan: mean/std scaling, sigma-delta), :88-91 (SprayBank.quantize: searchsorted
+ * count / KK), :105-110 (_quantize_error). Rows of 128 values. The two row sums are fp64 sums of
+ * the value pairs (2l, 2l+1) over the adjacent-pair tree; std is unbiased (torch.std). */
+static double or_tree_sum64(double* v) {
+  for (int w = 1; w < 64; w *= 2)
+    for (int l = 0; l < 64; l += 2 * w) v[l] = v[l] + v[l + w];
+  return v[0];
+}
+void or_state_df(float* h, float* sd_error, long rows, const float* R, int kk, int sd_bits) {
+  for (long r = 0; r < rows; ++r) {
+    float* x = h + r * 128;
+    float* e = sd_error ? sd_error + r * 128 : NULL;
+    double v[64];
+    for (int l = 0; l < 64; ++l) v[l] = (double)x[2 * l] + (double)x[2 * l + 1];
+    const float mean = (float)(or_tree_sum64(v) / 128.0);
+    for (int l = 0; l < 64; ++l) {
+      const float d0 = x[2 * l] - mean, d1 = x[2 * l + 1] - mean;
+      v[l] = (double)d0 * (double)d0 + (double)d1 * (double)d1;
+    }
+    float sd = sqrtf((float)(or_tree_sum64(v) / 127.0));
+    if (!(sd > 1e-8f)) sd = 1e-8f;
+    const float t3 = 3.0f * sd, t6 = 6.0f * sd;
+    const float lo = mean - t3;
+    const float range = t6 > 1e-8f ? t6 : 1e-8f;
+    const float scale = sd_bits < 32 ? (float)(1 << (sd_bits - 1)) : 1.0f;
+    for (int k = 0; k < 128; ++k) {
+      float hs = (x[k] - lo) / range;
+      hs = hs < 0.0f ? 0.0f : (hs > 1.0f ? 1.0f : hs);
+      float hc = hs;
+      if (e) {
+        hc = hs + e[k];
+        hc = hc < 0.0f ? 0.0f : (hc > 1.0f ? 1.0f : hc);
+      }
+      int cnt = 0;
+      while (cnt < kk && R[cnt] < hc) ++cnt;  /* sorted: the number of thresholds below hc */
+      const float q = (float)cnt / (float)kk;
+      if (e) {
+        float d = hc - q;
+        d = d < -1.0f ? -1.0f : (d > 1.0f ? 1.0f : d);
+        if (sd_bits < 32) d = rintf(d * scale) / scale;
+        e[k] = d;
+      }
+      const float qr = q * range;
+      x[k] = qr + lo;
+    }
+  }
+}

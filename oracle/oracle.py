@@ -391,3 +391,18 @@ class OracleCPUModel:
         lib().or_c_rms_norm(_p(x), _p(_f32(self.w.norm_f)), _p(xf), 1, c.d_model)
         logits = xf @ self.emb32.T
         return logits, int(np.argmax(logits))
+
+
+def state_density_field(h: np.ndarray, thresholds: np.ndarray, sd_error: Optional[np.ndarray] = None,
+                        sd_bits: int = 8):
+    """or_state_df on a copy: (rows, 128) fp32 state (and sigma-delta error) after the chunk-
+    boundary quantization of df_ssd_scan (training/df_ssm_mamba2_distill_dfw.py:139-165) with the
+    bank's sorted thresholds. Returns (h, sd_error or None)."""
+    h = np.ascontiguousarray(h, np.float32).reshape(-1, 128).copy()
+    e = None if sd_error is None else np.ascontiguousarray(sd_error, np.float32).reshape(-1, 128).copy()
+    R = np.ascontiguousarray(thresholds, np.float32).reshape(-1)
+    f = lib().or_state_df
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    f.restype = None
+    f(h.ctypes.data, None if e is None else e.ctypes.data, h.shape[0], R.ctypes.data, R.size, sd_bits)
+    return h, e
