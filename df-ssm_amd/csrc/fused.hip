@@ -285,6 +285,20 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
   }
 }
 
+// Bit planes of 64 int8 values (q of value k0 + lane) into the 16 words at dst (LDS, 16-byte
+// aligned), from lane 0: word 2b + h = bit b of values k0 + 32h .. k0 + 32h + 31, i.e. each
+// plane's 64-bit ballot stored whole (one 64-bit register move per plane).
+__device__ __forceinline__ void planes_store64(uint32_t* dst, int q, int lane) {
+  uint64_t b64[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) b64[b] = __ballot((q >> b) & 1);
+  if (lane == 0) {
+    uint64_t* d = (uint64_t*)dst;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) d[b] = b64[b];
+  }
+}
+
 // Projection prologue (GEMV workgroups): per row the amax, the quantization scale, and each
 // wave's bit planes of its own GEMV chunks (no barrier before the GEMV) with their sum q.
 // CW: the wave's chunks are CW consecutive ones per round of CW * 16 (those its GEMV reads).
@@ -308,9 +322,7 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
         const int k0 = 128 * c + 64 * hh;
         const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
         qsum += q;
-        uint32_t pw[16];
-        planes64(q, pw);
-        planes_store(&L.planes[m][k0 / 32][0], pw);
+        planes_store64(&L.planes[m][k0 / 32][0], q, lane);
       }
     }
     const int wq = wave_sum_dpp_i32(qsum);
@@ -368,20 +380,19 @@ __device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[
     const int c = wave + kFW * j;
     if (c < CH) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w = wb[j][i];
+      for (int sh = 0; sh < 2; ++sh) {  // the two 64-value sets of the chunk
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const u32x4 p0 = *(const u32x4*)&L.planes[m][c * 4 + i][0];
-          const u32x4 p1 = *(const u32x4*)&L.planes[m][c * 4 + i][4];
-          cnt[m][0] += __builtin_popcount(w & p0[0]);
-          cnt[m][1] += __builtin_popcount(w & p0[1]);
-          cnt[m][2] += __builtin_popcount(w & p0[2]);
-          cnt[m][3] += __builtin_popcount(w & p0[3]);
-          cnt[m][4] += __builtin_popcount(w & p1[0]);
-          cnt[m][5] += __builtin_popcount(w & p1[1]);
-          cnt[m][6] += __builtin_popcount(w & p1[2]);
-          cnt[m][7] += __builtin_popcount(w & p1[3]);
+          const u32x4* ps = (const u32x4*)&L.planes[m][c * 4 + 2 * sh][0];
+          const u32x4 d0 = ps[0], d1 = ps[1], d2 = ps[2], d3 = ps[3];
+          const uint32_t pl[16] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3],
+                                   d2[0], d2[1], d2[2], d2[3], d3[0], d3[1], d3[2], d3[3]};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t w = wb[j][2 * sh + h];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) cnt[m][b] += __builtin_popcount(w & pl[2 * b + h]);
+          }
         }
       }
     }
@@ -412,21 +423,17 @@ __device__ __forceinline__ void gemv_partials16(FusedLds<M>& L, const u32x2 (&wb
     const int cu = 4 * wave + (lane >> 4) + 64 * j;
     if (cu < 2 * CH) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint32_t w = wb[j][i];
-        const int word = 2 * cu + i;  // = 4 c + 2 h + i
+      for (int m = 0; m < M; ++m) {
+        // the words 2 cu, 2 cu + 1 are the halves of 64-value set cu
+        const u32x4* ps = (const u32x4*)&L.planes[m][2 * cu][0];
+        const u32x4 d0 = ps[0], d1 = ps[1], d2 = ps[2], d3 = ps[3];
+        const uint32_t pl[16] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3],
+                                 d2[0], d2[1], d2[2], d2[3], d3[0], d3[1], d3[2], d3[3]};
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const u32x4 p0 = *(const u32x4*)&L.planes[m][word][0];
-          const u32x4 p1 = *(const u32x4*)&L.planes[m][word][4];
-          cnt[m][0] += __builtin_popcount(w & p0[0]);
-          cnt[m][1] += __builtin_popcount(w & p0[1]);
-          cnt[m][2] += __builtin_popcount(w & p0[2]);
-          cnt[m][3] += __builtin_popcount(w & p0[3]);
-          cnt[m][4] += __builtin_popcount(w & p1[0]);
-          cnt[m][5] += __builtin_popcount(w & p1[1]);
-          cnt[m][6] += __builtin_popcount(w & p1[2]);
-          cnt[m][7] += __builtin_popcount(w & p1[3]);
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t w = wb[j][i];
+#pragma unroll
+          for (int b = 0; b < 8; ++b) cnt[m][b] += __builtin_popcount(w & pl[2 * b + i]);
         }
       }
     }
