@@ -12,9 +12,12 @@
 //   B  SSM + gate: item (sequence, head, 16-row block); two waves per item poll the words the
 //      item needs (gate, x, B, C, dt) into LDS, then every wave updates one fp32 state row and
 //      writes its g.
-//   C  out_proj: workgroup w < gC = D/64 reads all of g, runs the gated RMSNorm prologue and the
-//      GEMV and adds the residual into x; workgroups gC..gC+15 compute the out_proj LoRA
+//   C  out_proj: workgroup w < gC = D/RC (RC = 16 rows per group, 64 when D/16 + 16 groups do
+//      not fit the grid) reads all of g, runs the gated RMSNorm prologue and the GEMV of its rows
+//      and adds the residual into x; workgroups gC..gC+15 compute the out_proj LoRA
 //      intermediates as in phase A.
+// The prologues and GEMVs are bound by VALU issue (16 waves share the CU's four 16-lane SIMDs):
+// the quantizer's bit planes are built once per 64 values with 8 ballots, stored whole.
 // The weights and the state do not depend on the activations, so each workgroup issues those
 // loads first.
 //
