@@ -12,7 +12,7 @@
 //   B  SSM + gate: item (sequence, head, 16-row block); two waves per item poll the words the
 //      item needs (gate, x, B, C, dt) into LDS, then every wave updates one fp32 state row and
 //      writes its g.
-//   C  out_proj: workgroup w < gC = D/RC (RC = 16 rows per group, 64 when D/16 + 16 groups do
+//   C  out_proj: workgroup w < gC = D/RC (RC = 32 rows per group, 64 when D/32 + 16 groups do
 //      not fit the grid) reads all of g, runs the gated RMSNorm prologue and the GEMV of its rows
 //      and adds the residual into x; workgroups gC..gC+15 compute the out_proj LoRA
 //      intermediates as in phase A.
@@ -44,8 +44,10 @@ constexpr int kFT = 1024;
 constexpr int kFW = kFT / 64;
 constexpr int kFMaxK = 5120;
 constexpr int kFMaxCPW = (kFMaxK / 128 + kFW - 1) / kFW;
-// out_proj in 16-row groups: thread t owns row t % 16 and half-chunks u = t / 16 + 64 j
-constexpr int kC16 = (2 * (kFMaxK / 128) + 63) / 64;
+// out_proj in RG-row groups (RG = 16 or 32): thread t owns row t % RG and half-chunks
+// u = t / RG + (1024 / RG) j
+template <int RG>
+constexpr int kCR = (2 * (kFMaxK / 128) + kFT / RG - 1) / (kFT / RG);
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kSpinMax = 1u << 18;
 constexpr int kMaxItems = kFW / 2;  // SSM items per workgroup (two polling waves each)
@@ -143,14 +145,16 @@ __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t*
   }
 }
 
-// 16-row group `grp` (rows 16 grp .. 16 grp + 15 of the 64-row tiles): thread (row r = lane % 16,
-// u = 4 wave + lane / 16 + 64 j) loads words 2h, 2h + 1 of chunk c, cu = u = 2c + h.
-__device__ __forceinline__ void load_bits16(u32x2 (&wb)[kC16], const uint32_t* bits, int grp, int K) {
+// RG-row group `grp` (rows RG grp .. RG grp + RG - 1 of the 64-row tiles): thread (row
+// r = lane % RG, u = (64 / RG) wave + lane / RG + (1024 / RG) j) loads words 2h, 2h + 1 of chunk c,
+// cu = u = 2c + h.
+template <int RG>
+__device__ __forceinline__ void load_bits_rg(u32x2 (&wb)[kCR<RG>], const uint32_t* bits, int grp, int K) {
   const int lane = tix() & 63, wave = tix() >> 6, CH = K / 128;
-  const u32x4* b = (const u32x4*)bits + (size_t)(grp >> 2) * CH * 64 + (grp & 3) * 16 + (lane & 15);
+  const u32x4* b = (const u32x4*)bits + (size_t)(grp / (64 / RG)) * CH * 64 + (grp % (64 / RG)) * RG + lane % RG;
 #pragma unroll
-  for (int j = 0; j < kC16; ++j) {
-    const int cu = 4 * wave + (lane >> 4) + 64 * j;
+  for (int j = 0; j < kCR<RG>; ++j) {
+    const int cu = (64 / RG) * wave + lane / RG + (kFT / RG) * j;
     wb[j] = cu < 2 * CH ? __builtin_nontemporal_load((const u32x2*)(b + (size_t)(cu >> 1) * 64) + (cu & 1))
                         : u32x2{0u, 0u};
   }
@@ -410,10 +414,11 @@ __device__ __forceinline__ void gemv_partials(FusedLds<M>& L, const u32x4 (&wb)[
   }
 }
 
-// Packed-bit GEMV of one 16-row group: each thread two words of one row, the four threads of a
-// wave that share a row summed by lane exchange; per-wave partials into L.T rows 0..15.
-template <int M>
-__device__ __forceinline__ void gemv_partials16(FusedLds<M>& L, const u32x2 (&wb)[kC16], int K) {
+// Packed-bit GEMV of one RG-row group: each thread two words of one row per half-chunk, the
+// threads of a wave that share a row summed by lane exchange; per-wave partials into L.T rows
+// 0..RG-1.
+template <int M, int RG>
+__device__ __forceinline__ void gemv_partials_rg(FusedLds<M>& L, const u32x2 (&wb)[kCR<RG>], int K) {
   const int lane = tix() & 63, wave = tix() >> 6;
   const int CH = K / 128;
   uint32_t cnt[M][8];
@@ -422,8 +427,8 @@ __device__ __forceinline__ void gemv_partials16(FusedLds<M>& L, const u32x2 (&wb
 #pragma unroll
     for (int b = 0; b < 8; ++b) cnt[m][b] = 0u;
 #pragma unroll
-  for (int j = 0; j < kC16; ++j) {
-    const int cu = 4 * wave + (lane >> 4) + 64 * j;
+  for (int j = 0; j < kCR<RG>; ++j) {
+    const int cu = (64 / RG) * wave + lane / RG + (kFT / RG) * j;
     if (cu < 2 * CH) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
@@ -447,9 +452,9 @@ __device__ __forceinline__ void gemv_partials16(FusedLds<M>& L, const u32x2 (&wb
 #pragma unroll
     for (int b = 0; b < 7; ++b) t += (int)(cnt[m][b] << b);
     t -= (int)(cnt[m][7] << 7);
-    t += __shfl_xor(t, 16);
+    if (RG == 16) t += __shfl_xor(t, 16);
     t += __shfl_xor(t, 32);
-    if (lane < 16) L.T[m][lane][wave] = t;
+    if (lane < RG) L.T[m][lane][wave] = t;
   }
 }
 
@@ -615,7 +620,7 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
   }
 }
 
-// RC: rows per out_proj group (16, or 64 when D / 16 + 16 groups do not fit the grid).
+// RC: rows per out_proj group (32, or 64 when D / 32 + 16 groups do not fit the grid).
 template <int M, int RC>
 __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   __shared__ FusedLds<M> L;
@@ -668,11 +673,11 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err);
   }
   // ---- phase B: SSM + gate ----
-  u32x4 wc[RC == 16 ? 1 : kFMaxCPW];
-  u32x2 wc16[kC16];
+  u32x4 wc[RC < 64 ? 1 : kFMaxCPW];
+  u32x2 wcr[kCR<RC < 64 ? RC : 16>];
   EpiRow ec = {};
   if (wg < gC) {  // phase-C weights, loaded while phase B runs
-    if constexpr (RC == 16) load_bits16(wc16, a.out_bits, wg, a.DI);
+    if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, wg, a.DI);
     else load_bits(wc, a.out_bits, wg, a.DI);
     ec = load_epi<M, false, RC>(a, wg);
   }
@@ -702,15 +707,15 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     PIn<M> pc;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
     const uint32_t tag = tag_now();
-    prologue<M, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);
+    prologue<M, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);  // the chunks of the wave's GEMV
     for (int grp = wg; grp < gC; grp += G) {
       if (grp != wg) {
-        if constexpr (RC == 16) load_bits16(wc16, a.out_bits, grp, a.DI);
+        if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, grp, a.DI);
         else load_bits(wc, a.out_bits, grp, a.DI);
         ec = load_epi<M, false, RC>(a, grp);
       }
       const uint32_t hv = lora_issue(hC, M);
-      if constexpr (RC == 16) gemv_partials16<M>(L, wc16, a.DI);
+      if constexpr (RC < 64) gemv_partials_rg<M, RC>(L, wcr, a.DI);
       else gemv_partials<M>(L, wc, a.DI);
       lora_finish<M>(L, hC, hv, tag, a.err);
       __syncthreads();
@@ -746,8 +751,9 @@ static int fused_grid() {
 // seen every item's output, which then implies that all reads of x are done. A workgroup polls
 // at most kMaxItems items (two waves each). The state width (d_state 128 = two columns per lane)
 // and P % 16 == 0 are checked with the model dims.
-// Rows per out_proj group: 16 when the grid holds D / 16 groups and their 16 LoRA workgroups.
-static int out_rows(int D) { return D / 16 + DFSSM_LORA_R <= fused_grid() ? 16 : 64; }
+// Rows per out_proj group: 32 when D / 32 groups and the 16 LoRA workgroups fit the grid, else 64.
+// (16-row groups measured 1% slower per step at batch 1: 128 pollers of the gated words.)
+static int out_rows(int D) { return D / 32 + DFSSM_LORA_R <= fused_grid() ? 32 : 64; }
 
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
   const int G = fused_grid();
@@ -773,11 +779,11 @@ hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uin
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
   if (!fused_layer_supported(M, a.IPO, a.D, a.DI, a.H, a.P)) return hipErrorNotSupported;
   const int G = fused_grid();
-  const bool r16 = out_rows(a.D) == 16;
-#define DFSSM_FUSED(MM)                                                                       \
-  case MM:                                                                                    \
-    if (r16) hipLaunchKernelGGL((layer_fused_kernel<MM, 16>), dim3(G), dim3(kFT), 0, s, a);   \
-    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64>), dim3(G), dim3(kFT), 0, s, a);       \
+  const int rc = out_rows(a.D);
+#define DFSSM_FUSED(MM)                                                                          \
+  case MM:                                                                                       \
+    if (rc == 32) hipLaunchKernelGGL((layer_fused_kernel<MM, 32>), dim3(G), dim3(kFT), 0, s, a);   \
+    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64>), dim3(G), dim3(kFT), 0, s, a);          \
     break;
   switch (M) {
     DFSSM_FUSED(1)

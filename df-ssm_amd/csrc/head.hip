@@ -393,22 +393,40 @@ static hipError_t launch_head_mf(const HeadArgs& a, int groups, size_t shm, hipS
   hipLaunchKernelGGL((head_kernel<M, F16>), dim3(groups), dim3(256), shm, s, a);
   return hipGetLastError();
 }
-template <int M>
-static hipError_t launch_head_m(const HeadArgs& a, int groups, size_t shm, hipStream_t s) {
-  return a.f16 ? launch_head_mf<M, true>(a, groups, shm, s) : launch_head_i8<M>(a, groups, s);
-}
 
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
   const int groups = (a.V + 63) / 64;
-  const size_t shm = (size_t)M * a.D * sizeof(double);
-  if (shm > 120 * 1024) return hipErrorInvalidValue;
-  switch (M) {
-    case 1: return launch_head_m<1>(a, groups, shm, s);
-    case 2: return launch_head_m<2>(a, groups, shm, s);
-    case 3: return launch_head_m<3>(a, groups, shm, s);
-    case 4: return launch_head_m<4>(a, groups, shm, s);
-    default: return hipErrorInvalidValue;
+  if (M < 1 || M > 4) return hipErrorInvalidValue;
+  if (!a.f16) {
+    switch (M) {
+      case 1: return launch_head_i8<1>(a, groups, s);
+      case 2: return launch_head_i8<2>(a, groups, s);
+      case 3: return launch_head_i8<3>(a, groups, s);
+      default: return launch_head_i8<4>(a, groups, s);
+    }
   }
+  // fp16 table: the rows' final-normed values sit in LDS as fp64 (8 D bytes per row, at most
+  // 120 KiB), so wide models run the rows in launches of fewer rows, one after the other
+  const size_t per_row = (size_t)a.D * sizeof(double);
+  const int fit = (int)((120 * 1024) / per_row);
+  if (fit < 1) return hipErrorInvalidValue;
+  for (int r0 = 0; r0 < M; r0 += fit) {
+    const int mr = M - r0 < fit ? M - r0 : fit;
+    HeadArgs b = a;
+    b.x = a.x + (size_t)r0 * a.D;
+    b.logits = a.logits ? a.logits + (size_t)r0 * a.V : nullptr;
+    b.next = a.next + r0;
+    b.x_next = a.x_next ? a.x_next + (size_t)r0 * a.D : nullptr;
+    hipError_t e;
+    switch (mr) {
+      case 1: e = launch_head_mf<1, true>(b, groups, per_row, s); break;
+      case 2: e = launch_head_mf<2, true>(b, groups, 2 * per_row, s); break;
+      case 3: e = launch_head_mf<3, true>(b, groups, 3 * per_row, s); break;
+      default: e = launch_head_mf<4, true>(b, groups, 4 * per_row, s); break;
+    }
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_embed(const EmbedArgs& a, int M, hipStream_t s) {

@@ -136,6 +136,55 @@ def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
     assert gpu.error_flag() == 0
 
 
+@pytest.mark.parametrize("B", [1, 4])
+def test_one_launch_layer_wide_model(B):
+    """d_model 4096 (128 out_proj groups of 32 rows, the widest grid use): the one-launch layer
+    against the five-kernel form, bit for bit."""
+    from dfssm import _C
+    from dfssm.format import DFSSMConfig
+    c = DFSSMConfig(n_layer=1, d_model=4096, d_inner=4096, d_state=128, nheads=64, headdim=64, ngroups=1,
+                    vocab_size=1000, kw=4)
+    w = make_weights(c, seed=5)
+    print(f"wide one-launch B={B}", flush=True)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    gpu.ingest(torch.from_numpy(make_prompts(B, c.vocab_size, 3)))
+    lib = _C.lib()
+    x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    _C.check(lib.dfssm_layer_step(gpu._model, 0, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(), _C.stream()))
+    x1, h1, c1 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    gpu.x.copy_(x0); gpu.h_state.copy_(h0); gpu.conv_state.copy_(c0)
+    for ph in range(5):
+        _C.check(lib.dfssm_layer_phase(gpu._model, 0, ph, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
+                                       _C.stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(gpu.x.view(torch.int16), x1.view(torch.int16))
+    assert torch.equal(gpu.h_state, h1)
+    assert torch.equal(gpu.conv_state.view(torch.int16), c1.view(torch.int16))
+    assert gpu.error_flag() == 0
+
+
+@pytest.mark.parametrize("emb_code", [0, 1])
+def test_wide_model_head_batch4(emb_code):
+    """d_model 4096 at batch 4: the exact head for both table types (the fp16 table's fp64 head
+    holds 3 rows in LDS, so it runs the rows in two launches) against the oracle's logits."""
+    from dfssm.format import DFSSMConfig
+    c = DFSSMConfig(n_layer=1, d_model=4096, d_inner=4096, d_state=128, nheads=64, headdim=64, ngroups=1,
+                    vocab_size=1000, kw=4, emb_code=emb_code)
+    w = make_weights(c, seed=6)
+    B = 4
+    print(f"wide head emb_code={emb_code}", flush=True)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    orc = O.OracleModel(w, B)
+    tok = make_prompts(B, c.vocab_size, 1)[:, 0]
+    for t in range(3):
+        lg = _np16(gpu.forward(torch.from_numpy(tok).to(DEV))).astype(np.float32)
+        lo, nxt = orc.step(tok)
+        assert np.abs(lg - lo.astype(np.float32)).max() == 0.0, f"step {t}"
+        np.testing.assert_array_equal(lg.argmax(axis=1), nxt)
+        tok = nxt
+    assert gpu.error_flag() == 0
+
+
 @pytest.fixture(scope="module")
 def tiny_weights_f16():
     # the exporter's fp16 embedding table (format embedding code 0)
