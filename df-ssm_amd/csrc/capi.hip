@@ -601,7 +601,7 @@ int dfssm_state_density_field(float* h, float* sd_error, int64_t rows, int d_sta
   if (!h || !thresholds) return DFSSM_E_NULL;
   if (d_state != 128) return DFSSM_E_DIMS;
   if (rows < 0 || kk < 1 || kk > kStateDfMaxKK || sd_bits < 1) return DFSSM_E_RANGE;
-  if (((uintptr_t)h & 7u) || ((uintptr_t)sd_error & 7u) || ((uintptr_t)thresholds & 3u)) return DFSSM_E_ALIGN;
+  if (((uintptr_t)h & 15u) || ((uintptr_t)sd_error & 15u) || ((uintptr_t)thresholds & 3u)) return DFSSM_E_ALIGN;
   StateDfArgs a{};
   a.h = h; a.sd_error = sd_error; a.thresholds = thresholds; a.rows = rows; a.kk = kk; a.sd_bits = sd_bits;
   return hip_status(launch_state_df(a, as_stream(stream)));

@@ -219,7 +219,7 @@ int dfssm_prefill(const dfssm_model* model, const int64_t* tokens, int n_tokens,
  *   e = round(clamp(hc - q, -1, 1) 2^(sd_bits-1)) / 2^(sd_bits-1)  (_quantize_error, :105-110;
  *       unquantized for sd_bits >= 32),
  *   h = q range + lo.
- * h and sd_error are (rows, 128), updated in place; sd_error NULL = no sigma-delta.
+ * h and sd_error are (rows, 128), 16-byte aligned, updated in place; sd_error NULL = no sigma-delta.
  * thresholds: the kk sorted thresholds of the bank for this chunk (bank = chunk % num_banks),
  * 1 <= kk <= 1024. Both row sums are fp64 over a fixed adjacent-pair tree, so results are
  * deterministic. */
