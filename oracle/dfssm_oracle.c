@@ -194,6 +194,7 @@ void or_scaffold_acc(const uint32_t* bits, const int8_t* q, int M, int N, int K,
  * _rms_norm, df_ssm_inference.py:141-145, followed by copy_ into an fp16 buffer (:165,196,210).
  * The mean is sum * (1/K) as ATen's mean reduction computes it. */
 void or_rmsnorm(const uint16_t* x, const float* w, int M, int K, uint16_t* out) {
+#pragma omp parallel for schedule(static)
   for (int m = 0; m < M; ++m) {
     const uint16_t* xm = x + (size_t)m * K;
     double ss = 0.0;
@@ -211,6 +212,7 @@ void or_rmsnorm(const uint16_t* x, const float* w, int M, int K, uint16_t* out) 
  *                                                     by multiplying with its fp32 reciprocal)
  *   q = clamp(rne(fp16(x / s)), -128, 127)          (tensor/tensor division is IEEE fp32) */
 void or_quantize(const uint16_t* xn, int M, int K, int8_t* q, uint16_t* s) {
+#pragma omp parallel for schedule(static)
   for (int m = 0; m < M; ++m) {
     const uint16_t* xm = xn + (size_t)m * K;
     float amax = 0.0f;
@@ -233,6 +235,7 @@ void or_quantize(const uint16_t* xn, int M, int K, int8_t* q, uint16_t* s) {
 /* h16[m][r] = fp16(sum_k xn[m][k] * B16[r][k]) with B16 = fp16(B_i8 * B_s[r]) (the load-time
  * dequant of df_ssm_inference.py:83, then the fp16 GEMM x_norm @ lora_B.T of :173). */
 void or_lora_h(const uint16_t* xn, const int8_t* lB, const uint16_t* lBs, int M, int K, uint16_t* h16) {
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m)
     for (int r = 0; r < LORA_R; ++r) {
       float bs = hf(lBs[r]);
@@ -251,6 +254,7 @@ void or_lora_h(const uint16_t* xn, const int8_t* lB, const uint16_t* lBs, int M,
  * and the sum is the fp32 addmm_ of :173 / :204. */
 void or_dequant_lora(const int32_t* acc, const uint16_t* xs, const uint16_t* ws, const uint16_t* h16,
                      const int8_t* lA, const uint16_t* lAs, int M, int N, uint16_t* out) {
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m)
     for (int n = 0; n < N; ++n) {
       float a16 = hf(or_f2h((float)acc[(size_t)m * N + n]));
@@ -271,6 +275,7 @@ void or_dequant_lora(const int32_t* acc, const uint16_t* xs, const uint16_t* ws,
  * left to right), state <- (s1, s2, x), x <- fp16(out * 1/(1+exp(-out))). Products of two fp16
  * values are exact in fp32, so the order of additions is the only rounding choice. */
 void or_conv_step(uint16_t* state, uint16_t* xbc, int ld, const uint16_t* w, const uint16_t* b, int M, int C) {
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m)
     for (int ch = 0; ch < C; ++ch) {
       uint16_t* cs = state + ((size_t)m * C + ch) * 3;
@@ -308,15 +313,20 @@ void or_ssm_step(float* h, const uint16_t* xbc, int ld_xbc, const uint16_t* dt_r
       const uint16_t* xr = xbc + (size_t)m * ld_xbc;
       float dt = or_log1pf(or_expf(hf(dt_raw[(size_t)m * ld_dt + hd]) + dt_bias[hd]));
       float abar = or_expf(dt * -or_expf(A_log[hd]));
+      float Bf[512], Cf[512]; /* N <= 512: B and C of this sequence, converted once */
+      for (int n = 0; n < N; ++n) {
+        Bf[n] = hf(xr[DI + n]);
+        Cf[n] = hf(xr[DI + N + n]);
+      }
       for (int p = 0; p < P; ++p) {
         float xv = hf(xr[hd * P + p]);
         float X = xv * dt;
         float* hp = h + (((size_t)m * H + hd) * P + p) * N;
         double acc = 0.0;
         for (int n = 0; n < N; ++n) {
-          float hn = fmaf(abar, hp[n], X * hf(xr[DI + n]));
+          float hn = fmaf(abar, hp[n], X * Bf[n]);
           hp[n] = hn;
-          acc += (double)hf(xr[DI + N + n]) * (double)hn;
+          acc += (double)Cf[n] * (double)hn;
         }
         y[(size_t)m * DI + hd * P + p] = or_f2h((float)acc + xv * Dp[hd]);
       }
@@ -328,6 +338,7 @@ void or_ssm_step(float* h, const uint16_t* xbc, int ld_xbc, const uint16_t* dt_r
 /* g = fp16(y * fp16(z * fp16(sigmoid(z)))) -- the three fp16 tensor ops of
  * df_ssm_inference.py:194-195; the gated RMSNorm is or_rmsnorm on g. */
 void or_gate(const uint16_t* y, const uint16_t* z, int ld_z, int M, int DI, uint16_t* g) {
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m)
     for (int k = 0; k < DI; ++k) {
       float zv = hf(z[(size_t)m * ld_z + k]);
