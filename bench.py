@@ -127,23 +127,35 @@ def time_state_df(m, reps=20):
     return us, 4 * m.h_state.numel() * 4
 
 
+def replay_steps(graph_of, n):
+    """Replay decode graphs covering exactly n steps: graphs of STEPS_PER_GRAPH steps, then one
+    graph of the remainder. graph_of(S) returns (graph, history) for S fused steps."""
+    full, rest = divmod(n, STEPS_PER_GRAPH)
+    if full:
+        g, _ = graph_of(STEPS_PER_GRAPH)
+        for _ in range(full):
+            g.replay()
+    if rest:
+        graph_of(rest)[0].replay()
+
+
 def time_decode(m, prompts, steps, warmup):
+    """Exactly `warmup` untimed then `steps` timed greedy steps (HIP events on the launch stream);
+    returns (ms, steps)."""
     import torch
     m.reset_state()
     m.ingest(torch.from_numpy(prompts))
-    g, _ = m._gen_graph(STEPS_PER_GRAPH)
-    for _ in range(max(1, warmup // STEPS_PER_GRAPH)):
-        g.replay()
+    for S in {STEPS_PER_GRAPH, steps % STEPS_PER_GRAPH, warmup % STEPS_PER_GRAPH} - {0}:
+        m._gen_graph(S)  # capture before timing
+    replay_steps(m._gen_graph, warmup)
     torch.cuda.synchronize()
-    reps = max(1, steps // STEPS_PER_GRAPH)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        g.replay()
+    replay_steps(m._gen_graph, steps)
     e1.record()
     e1.synchronize()
     ms = e0.elapsed_time(e1)
-    return ms, reps * STEPS_PER_GRAPH
+    return ms, steps
 
 
 def time_sampled(m, prompts, steps, warmup, T=0.7, top_p=0.9, penalty=1.2):
@@ -157,18 +169,17 @@ def time_sampled(m, prompts, steps, warmup, T=0.7, top_p=0.9, penalty=1.2):
     m._counts.zero_()
     m._sstep.zero_()
     m.ingest(torch.from_numpy(prompts))
-    g, _ = m._sample_graph(STEPS_PER_GRAPH, params)
-    for _ in range(max(1, warmup // STEPS_PER_GRAPH)):
-        g.replay()
+    graph_of = lambda S: m._sample_graph(S, params)  # noqa: E731
+    for S in {STEPS_PER_GRAPH, steps % STEPS_PER_GRAPH, warmup % STEPS_PER_GRAPH} - {0}:
+        graph_of(S)
+    replay_steps(graph_of, warmup)
     torch.cuda.synchronize()
-    reps = max(1, steps // STEPS_PER_GRAPH)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        g.replay()
+    replay_steps(graph_of, steps)
     e1.record()
     e1.synchronize()
-    ms = e0.elapsed_time(e1) / (reps * STEPS_PER_GRAPH)
+    ms = e0.elapsed_time(e1) / steps
     lib = _C.lib()
     out = torch.zeros(m.batch_size, dtype=torch.int64, device="cuda:0")
     ks = torch.cuda.CUDAGraph()
@@ -242,18 +253,133 @@ def time_kernels(m, reps=10):
     return out
 
 
-def cpu_baseline(weights, prompt, n_tokens):
+def cpu_baseline(model_path, prompt, n_tokens):
+    """The reference's cpu_inference.c (oracle/_ref, HEADDIM 64) on the same .dfssm file and prompt,
+    timed on this host: warm-up step, reset, the prompt untimed, n_tokens timed greedy steps
+    (cpu_inference_driver.py:186-204). Run twice in child processes, so that OpenMP reads its
+    settings at load: 4 threads (the reference's published setting, README.md:67) and the physical
+    cores of one socket (at most the 16 CPUs a one-GPU box shares), both with
+    OMP_PROC_BIND=close OMP_PLACES=cores and the NumPy BLAS threads set to match."""
+    import subprocess
     from oracle import ref_driver
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
     if not ref_driver.available():
         log("reference CPU kernels unavailable (not built or no AVX-512 VNNI on this host)")
         return None
-    m = ref_driver.RefCPUModel(weights)
-    toks, secs = m.generate(prompt, n_tokens)
-    return {"value": round(n_tokens / secs, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"batch 1, 1.3B shape: warm-up step, reset, {len(prompt)}-token prompt untimed, "
-                      f"{n_tokens} timed greedy steps of the reference cpu_inference.c (HEADDIM 64, "
-                      f"AVX-512 VNNI, OpenMP {threads} threads) + NumPy fp32 head; {secs:.1f} s"}
+    info = ref_driver.cpu_description()
+    socket_threads = max(1, min(info["cores_per_socket"], info["allowed_cpus"], 16))
+    runs = []
+    for threads in sorted({4, socket_threads}):
+        env = dict(os.environ)
+        env.update(OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close", OMP_PLACES="cores",
+                   OPENBLAS_NUM_THREADS=str(threads), MKL_NUM_THREADS=str(threads))
+        cmd = [sys.executable, "-u", "-m", "oracle.ref_driver", "--model", model_path,
+               "--prompt", ",".join(str(int(t)) for t in prompt), "--tokens", str(n_tokens)]
+        log(f"reference CPU decode, {threads} threads, {n_tokens} steps")
+        r = subprocess.run(cmd, cwd=REPO, env=env, capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            log(f"reference CPU run failed: {r.stderr[-400:]}")
+            continue
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        runs.append({"threads": threads, "tok_s": round(d["tok_s"], 3), "seconds": round(d["seconds"], 2),
+                     "us_per_token": round(1e6 * d["seconds"] / n_tokens, 1)})
+        log(f"  {d['tok_s']:.2f} tok/s")
+    if not runs:
+        return None
+    best = max(runs, key=lambda r: r["tok_s"])
+    return {"value": best["tok_s"], "unit": "tok/s", "cores": best["threads"], "kind": "reference",
+            "sample": f"batch 1, 1.3B shape (the bench's .dfssm file): warm-up step, reset, {len(prompt)}-token "
+                      f"prompt untimed, {n_tokens} timed greedy steps of the reference cpu_inference.c "
+                      "(HEADDIM 64, AVX-512 VNNI, OpenMP, OMP_PROC_BIND=close OMP_PLACES=cores) + NumPy fp32 "
+                      "head; value = the faster of the runs below",
+            "runs": runs, "cpu": info}
+
+
+def scaffold_op_bytes(M, N, K):
+    """Algorithmic bytes of one dfssm_scaffold_lora_gemm call (acc not written): sign bits, row
+    scales, LoRA A + scales, the fp16 LoRA-B table, q + scales, xn, the intermediates h, y."""
+    return N * K // 8 + 2 * N + 16 * N + 2 * N + 32 * K + M * K + 2 * M + 2 * M * K + 2 * 16 * M + 2 * M * N
+
+
+def scaffold_microbench(Ms=(1, 4, 16, 32), min_bytes=1 << 30, reps=3):
+    """BASELINE config 1 in isolation: in_proj (K 2048 -> N 8512) and out_proj (K 4096 -> N 2048),
+    each call = dfssm_scaffold_lora_gemm (LoRA intermediates + scaffold GEMV/GEMM + LoRA epilogue).
+    The calls rotate over distinct weight copies (bits, scales, LoRA A, LoRA-B table) totalling more
+    than `min_bytes`, so the weights stream from HBM, not from the 256 MB last-level cache; one graph
+    holds one call per copy, timed with HIP events. Returns {proj: {M: result}}."""
+    import numpy as np
+    import torch
+    from dfssm import _C
+    lib = _C.lib()
+    dev = "cuda:0"
+    out = {}
+    for name, N, K in (("in_proj", 8512, 2048), ("out_proj", 2048, 4096)):
+        tiled = lib.dfssm_tiled_bits_bytes(N, K)
+        per_copy = tiled + 2 * N + 16 * N + 2 * N + 32 * K
+        n = -(-min_bytes // per_copy)
+        g = torch.Generator(device=dev).manual_seed(1)
+        bits = torch.randint(-2**31, 2**31 - 1, (n, tiled // 4), dtype=torch.int32, device=dev, generator=g)
+        ws = (torch.rand(n, N, device=dev, generator=g) * 0.04 + 0.01).half()
+        lA = torch.randint(-127, 128, (n, N, 16), dtype=torch.int8, device=dev, generator=g)
+        lAs = (torch.rand(n, N, device=dev, generator=g) * 1.7e-3 + 0.85e-3).half()
+        lBq = (torch.randn(n, 16, K, device=dev, generator=g) / (np.sqrt(K))).half()
+        res = {}
+        for M in Ms:
+            xn = torch.randn(M, K, device=dev, generator=g).half()
+            q = torch.clamp(torch.round(torch.randn(M, K, device=dev, generator=g) * 40), -127, 127).to(torch.int8)
+            xs = (torch.rand(M, device=dev, generator=g) * 0.04 + 0.01).half()
+            h = torch.empty(M, 16, dtype=torch.float16, device=dev)
+            y = torch.empty(M, N, dtype=torch.float16, device=dev)
+
+            def call(i):
+                _C.check(lib.dfssm_scaffold_lora_gemm(
+                    bits[i].data_ptr(), ws[i].data_ptr(), q.data_ptr(), xs.data_ptr(), xn.data_ptr(),
+                    lA[i].data_ptr(), lAs[i].data_ptr(), lBq[i].data_ptr(), M, N, K, h.data_ptr(), None,
+                    y.data_ptr(), _C.stream()), "scaffold_lora_gemm")
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for i in range(n):
+                    call(i)
+            gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                gr.replay()
+            e1.record()
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+            b = scaffold_op_bytes(M, N, K)
+            gbs = b / (us * 1e-6) / 1e9
+            res[M] = {"us_per_call": round(us, 3), "bytes_per_call": b, "gbs": round(gbs, 1),
+                      "frac": round(gbs / PEAK_GBS, 4), "ops_per_call": 2 * M * N * K,
+                      "tops": round(2 * M * N * K / (us * 1e-6) / 1e12, 3), "weight_copies": n,
+                      "rotated_bytes": n * per_copy}
+            log(f"scaffold {name} M={M}: {us:.2f} us/call, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of HBM), "
+                f"{n} copies x {per_copy / 1e6:.2f} MB")
+        out[name] = res
+        del bits, ws, lA, lAs, lBq
+        torch.cuda.empty_cache()
+    return out
+
+
+def phase_sweep(B, path, layers=12):
+    """Counter-run driver (for rocprofv3 --pmc): the 1.3B model at batch B, 4 prompt tokens
+    ingested, then each of the five layer kernels (dfssm_layer_phase) on `layers` layers and the
+    head once; no timing, prints a line per stage."""
+    import torch
+    from dfssm import _C
+    from dfssm.synth import make_prompts
+    m, _ = build_model(B, path)
+    m.ingest(torch.from_numpy(make_prompts(B, m.cfg.vocab_size, 4)), step_by_step=True)
+    lib = _C.lib()
+    for li in range(layers):
+        for ph in range(5):
+            _C.check(lib.dfssm_layer_phase(m._model, li, ph, m.x.data_ptr(), m._state, m.workspace.data_ptr(),
+                                           _C.stream()))
+    _C.check(lib.dfssm_lmhead_argmax(m._model, m.x.data_ptr(), m.workspace.data_ptr(), None, m._next.data_ptr(),
+                                     None, _C.stream()))
+    torch.cuda.synchronize()
+    log(f"phase sweep batch {B}: {layers} layers x 5 kernels + head done")
 
 
 def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
@@ -379,6 +505,15 @@ def roofline_of(res, name=None):
             "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]}
 
 
+def scaffold_roofline(sc):
+    """The metric's "scaffold matmul % HBM roofline": the rotated microbench's in_proj call at M = 1."""
+    r = sc["in_proj"][1]
+    return {"bound": "hbm", "kernel": "dfssm_scaffold_lora_gemm in_proj (K 2048 -> N 8512), M = 1, "
+                                      f"{r['weight_copies']} rotated weight copies",
+            "achieved": r["gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
+            "bytes_per_launch": r["bytes_per_call"], "us_per_launch": r["us_per_call"], "traffic": None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,16 +522,22 @@ def main():
     ap.add_argument("--batch", type=int, default=1, help="batch of the headline value")
     ap.add_argument("--batch2", type=int, default=32, help="second batch reported beside it (0: skip)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=48)
+    ap.add_argument("--cpu-steps", type=int, default=128)
     ap.add_argument("--model-path", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_1p3b_seed0.dfssm"))
     ap.add_argument("--config4", type=int, default=1,
                     help="also measure config 4: 2.7B shape, batch 64, 512-token prompt, 256 timed steps (0: skip)")
     ap.add_argument("--model-path-2p7b", default=os.path.join(os.environ.get("TMPDIR", "/tmp"), "dfssm_2p7b_seed0.dfssm"))
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 10 device-to-device copies of this many MiB (counter calibration) and exit")
+    ap.add_argument("--phase-sweep", type=int, default=0,
+                    help="only run the five layer kernels on 12 layers and the head at this batch (counter runs)")
+    ap.add_argument("--scaffold", type=int, default=1, help="run the rotated scaffold microbench (0: skip)")
     a = ap.parse_args()
     if a.copy_mib:
         copy_calibration(a.copy_mib)
+        return
+    if a.phase_sweep:
+        phase_sweep(a.phase_sweep, a.model_path)
         return
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
@@ -404,6 +545,7 @@ def main():
         sys.exit(2)
 
     main_res, w, prompts = measure(a.batch, a.model_path, a.steps, a.warmup)
+    scaffold = scaffold_microbench() if a.scaffold else None
     second = None
     if a.batch2 and a.batch2 != a.batch:
         second, _, _ = measure(a.batch2, a.model_path, a.steps, a.warmup)
@@ -414,9 +556,7 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        from dfssm.format import read_dfssm
-        wts = w if w is not None else read_dfssm(a.model_path)
-        cpu = cpu_baseline(wts, prompts[0], a.cpu_steps)
+        cpu = cpu_baseline(a.model_path, prompts[0], a.cpu_steps)
         if cpu:
             log(f"reference CPU: {cpu['value']} tok/s on {cpu['cores']} threads")
 
@@ -435,7 +575,8 @@ def main():
                    "d_state": cfg.d_state, "vocab": cfg.vocab_size, "embedding": "int8+row scale",
                    "arith": "1-bit x int8 scaffold (int32 acc), fp16 activations, fp32 SSM state"},
         "roofline": roofline_of(main_res),
-        "scaffold_roofline": roofline_of(main_res, "in_proj+conv"),
+        "scaffold_roofline": scaffold_roofline(scaffold) if scaffold else roofline_of(main_res, "in_proj+conv"),
+        "scaffold_microbench": scaffold,
         "step_roofline": main_res["step_roofline"],
         "kernels": main_res["kernels"],
         "cpu_baseline": cpu,

@@ -129,6 +129,12 @@ int dfssm_check_dims(const dfssm_dims* d) {
   return DFSSM_OK;
 }
 
+int dfssm_one_launch_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
+  if (!d || dfssm_check_dims(d) != DFSSM_OK) return 0;
+  const Derived r = derive(d);
+  return fused_plan(cus, blocks_per_cu, blocks_per_cu, r.B, r.IPO, r.D, r.DI, r.H, r.P, nullptr);
+}
+
 size_t dfssm_tiled_bits_bytes(int rows, int k) {
   if (rows <= 0 || k <= 0) return 0;
   return (size_t)((rows + 63) / 64 * 64) * (size_t)(k / 32) * 4;
@@ -167,7 +173,7 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
   if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
   if (!aligned16(tiled_bits) || !aligned16(q)) return DFSSM_E_ALIGN;
   if (M <= 4) {
-    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, N, K};
+    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, nullptr, nullptr, nullptr, N, K};
     return hip_status(launch_scaffold(a, M, as_stream(stream)));
   }
   GemmArgs a{};
@@ -177,6 +183,34 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
   a.out = y_out; a.ld_out = N; a.acc_out = acc_out;
   a.N = N; a.K = K;
   return hip_status(launch_gemm(a, DFSSM_MODE_SCAFFOLD, as_stream(stream)));
+}
+
+int dfssm_scaffold_lora_gemm(const uint32_t* tiled_bits, const uint16_t* wscale, const int8_t* q,
+                             const uint16_t* xscale, const uint16_t* xn, const int8_t* lA, const uint16_t* lA_s,
+                             const uint16_t* lBq, int M, int N, int K, uint16_t* lora_h, int32_t* acc_out,
+                             uint16_t* y_out, void* stream) {
+  if (!tiled_bits || !wscale || !q || !xscale || !xn || !lA || !lA_s || !lBq || !lora_h || !y_out)
+    return DFSSM_E_NULL;
+  if (M < 1 || M > 64) return DFSSM_E_BATCH;
+  if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
+  if (!aligned16(tiled_bits) || !aligned16(q) || !aligned16(xn) || !aligned16(lBq) || !aligned16(lA))
+    return DFSSM_E_ALIGN;
+  hipStream_t s = as_stream(stream);
+  LoraHArgs la{xn, lBq, lora_h, K};
+  hipError_t e = launch_lora_h(la, M, s);
+  if (e != hipSuccess) return hip_status(e);
+  if (M <= 4) {
+    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, lA, lA_s, lora_h, N, K};
+    return hip_status(launch_scaffold(a, M, s));
+  }
+  GemmArgs a{};
+  a.bits = tiled_bits; a.wscale = wscale;
+  a.q = q; a.ld_q = K; a.M = M;
+  a.xs16 = xscale;
+  a.lA = lA; a.lAs = lA_s; a.h16 = lora_h;
+  a.out = y_out; a.ld_out = N; a.acc_out = acc_out;
+  a.N = N; a.K = K;
+  return hip_status(launch_gemm(a, DFSSM_MODE_SCAFFOLD, s));
 }
 
 int dfssm_rmsnorm_quantize(const uint16_t* x, const float* w, int M, int K, uint16_t* xn_out,

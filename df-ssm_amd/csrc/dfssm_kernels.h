@@ -61,6 +61,7 @@ struct GemmArgs {
   const float* xs;           // (M) activation scales (fp16 values) or null
   const uint16_t* xs16;      // (M) fp16 activation scales (SCAFFOLD), used when xs is null
   const float* h;            // (M, 16) LoRA intermediate (IN / OUT)
+  const uint16_t* h16;       // SCAFFOLD with LoRA (lA non-null): (M, 16) fp16 intermediates
   uint16_t* out;             // IN: proj; OUT: residual x (in place); SCAFFOLD: y (may be null)
   int ld_out;
   int32_t* acc_out;          // optional (M, N) accumulators
@@ -78,9 +79,21 @@ struct ScaffoldArgs {
   const uint16_t* xscale;    // (M) fp16 (needed only with y_out)
   const uint16_t* wscale;    // (N) fp16 (needed only with y_out)
   int32_t* acc_out;          // (M, N) or null
-  uint16_t* y_out;           // (M, N) fp16(fp16(fp16(acc) * xs) * ws) or null
+  uint16_t* y_out;           // (M, N) fp16(fp16(fp16(acc) * xs) * ws) [+ LoRA term] or null
+  const int8_t* lA;          // optional LoRA: (N, 16) int8 A, (N) fp16 scales, (M, 16) fp16 h
+  const uint16_t* lAs;
+  const uint16_t* h16;
   int N, K;
 };
+
+// LoRA intermediates of the stand-alone scaffold op: h[m][r] = fp16(sum_k xn[m][k] * lBq[r][k]).
+struct LoraHArgs {
+  const uint16_t* xn;        // (M, K) fp16
+  const uint16_t* lBq;       // (16, K) fp16(B_i8 * B_s)
+  uint16_t* h;               // (M, 16) fp16
+  int K;
+};
+hipError_t launch_lora_h(const LoraHArgs& a, int M, hipStream_t s);
 
 struct SsmArgs {
   float* h;                  // (M, H, P, N) fp32 state, updated in place
@@ -211,6 +224,9 @@ constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
 constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
 
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);
+// Grid of the one-launch layer on a device with `cus` CUs where per_cu32 / per_cu64 workgroups of
+// the 32- / 64-row-group instantiations fit per CU; 0 = use the five-kernel form. *rc_out = RC.
+int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int DI, int H, int P, int* rc_out);
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s);
 hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, hipStream_t s);
 

@@ -730,37 +730,72 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   if (tid == 0) st_dev(a.launches + wg, epoch_raw + 1u);
 }
 
-static int fused_grid() {
-  static int grid[16] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
-  if (grid[dev] == 0) {
-    int cus = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<4, 64>),
-                                                     kFT, 0) != hipSuccess || per_cu < 1)
-      return 0;
-    // one workgroup per CU: all co-resident whatever the per-CU occupancy
-    grid[dev] = cus < kFusedMaxGrid ? cus : kFusedMaxGrid;
-  }
-  return grid[dev];
+// The one-launch layer waits between its workgroups, so all G of them must be resident at once:
+// G = one workgroup per CU (at most kFusedMaxGrid), which holds only if the launched
+// instantiation fits at least once per CU (per_cu >= 1, from the occupancy query of that exact
+// kernel). The grid must also hold the phase-A and phase-C workgroups plus their 16 LoRA
+// workgroups, and every workgroup that reads x in phase A must also own an SSM item: phase C
+// overwrites x once it has seen every item's output, which then implies that all reads of x are
+// done. A workgroup polls at most kMaxItems items (two waves each). The state width (d_state 128 =
+// two columns per lane) and P % 16 == 0 are checked with the model dims.
+// Rows per out_proj group (RC): 32 when D / 32 groups and the 16 LoRA workgroups fit the grid, else
+// 64 (16-row groups measured 1% slower per step at batch 1: 128 pollers of the gated words).
+// Returns G, or 0 when the layer must run as five kernels.
+int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int DI, int H, int P, int* rc_out) {
+  const int G = cus < kFusedMaxGrid ? cus : kFusedMaxGrid;
+  if (G < 1 || M < 1 || M > 4) return 0;
+  const int rc = D / 32 + DFSSM_LORA_R <= G ? 32 : 64;
+  const int per_cu = rc == 32 ? per_cu32 : per_cu64;
+  if (per_cu < 1 || (long long)per_cu * cus < G) return 0;  // not all workgroups co-resident
+  const int gA = (IPO + 63) / 64, gC = D / rc, items = M * H * (P / 16);
+  if (gA > kFusedMaxGroups || D > kFMaxK || DI > kFMaxK || G < gA + DFSSM_LORA_R || G < gC + DFSSM_LORA_R ||
+      items < gA + DFSSM_LORA_R || items > kMaxItems * G)
+    return 0;
+  if (rc_out) *rc_out = rc;
+  return G;
 }
 
-// The grid must hold the phase-A and phase-C workgroups plus their 16 LoRA workgroups, and every
-// workgroup that reads x in phase A must also own an SSM item: phase C overwrites x once it has
-// seen every item's output, which then implies that all reads of x are done. A workgroup polls
-// at most kMaxItems items (two waves each). The state width (d_state 128 = two columns per lane)
-// and P % 16 == 0 are checked with the model dims.
-// Rows per out_proj group: 32 when D / 32 groups and the 16 LoRA workgroups fit the grid, else 64.
-// (16-row groups measured 1% slower per step at batch 1: 128 pollers of the gated words.)
-static int out_rows(int D) { return D / 32 + DFSSM_LORA_R <= fused_grid() ? 32 : 64; }
+template <int M, int RC>
+static int occupancy_of() {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<M, RC>),
+                                                   kFT, 0) != hipSuccess)
+    return 0;
+  return per_cu;
+}
+
+// Device facts for the plan, queried once per device: CU count and, per batch M = 1..4, the
+// occupancy of both row-group instantiations.
+struct FusedDev {
+  int cus = -1;
+  int per_cu[5][2] = {};
+};
+
+static const FusedDev* fused_dev() {
+  static FusedDev devs[16];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+  FusedDev& d = devs[dev];
+  if (d.cus < 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+    d.per_cu[1][0] = occupancy_of<1, 32>(); d.per_cu[1][1] = occupancy_of<1, 64>();
+    d.per_cu[2][0] = occupancy_of<2, 32>(); d.per_cu[2][1] = occupancy_of<2, 64>();
+    d.per_cu[3][0] = occupancy_of<3, 32>(); d.per_cu[3][1] = occupancy_of<3, 64>();
+    d.per_cu[4][0] = occupancy_of<4, 32>(); d.per_cu[4][1] = occupancy_of<4, 64>();
+    d.cus = cus;
+  }
+  return &d;
+}
+
+static int fused_grid(int M, int IPO, int D, int DI, int H, int P, int* rc) {
+  const FusedDev* d = fused_dev();
+  if (!d || M < 1 || M > 4) return 0;
+  return fused_plan(d->cus, d->per_cu[M][0], d->per_cu[M][1], M, IPO, D, DI, H, P, rc);
+}
 
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
-  const int G = fused_grid();
-  const int gA = (IPO + 63) / 64, gC = D / 64, items = M * H * (P / 16);
-  return G >= 1 && M >= 1 && M <= 4 && gA <= kFusedMaxGroups && D <= kFMaxK && DI <= kFMaxK &&
-         G >= gA + DFSSM_LORA_R && G >= gC + DFSSM_LORA_R && items >= gA + DFSSM_LORA_R &&
-         items <= kMaxItems * G;
+  return fused_grid(M, IPO, D, DI, H, P, nullptr) > 0;
 }
 
 // out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.
@@ -777,9 +812,9 @@ hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uin
 }
 
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
-  if (!fused_layer_supported(M, a.IPO, a.D, a.DI, a.H, a.P)) return hipErrorNotSupported;
-  const int G = fused_grid();
-  const int rc = out_rows(a.D);
+  int rc = 0;
+  const int G = fused_grid(M, a.IPO, a.D, a.DI, a.H, a.P, &rc);
+  if (G < 1) return hipErrorNotSupported;
 #define DFSSM_FUSED(MM)                                                                          \
   case MM:                                                                                       \
     if (rc == 32) hipLaunchKernelGGL((layer_fused_kernel<MM, 32>), dim3(G), dim3(kFT), 0, s, a);   \

@@ -81,8 +81,9 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   if (MODE != DFSSM_MODE_SCAFFOLD) {
     hv0 = a.h[(size_t)m_begin * DFSSM_LORA_R + hi0];
     xsv0 = a.xs[m_begin + xi0];
-  } else if (a.xs16) {  // absent when only the accumulators are written
-    xsh0 = a.xs16[m_begin + xi0];
+  } else {
+    if (a.xs16) xsh0 = a.xs16[m_begin + xi0];  // absent when only the accumulators are written
+    if (a.h16) hv0 = h2f(a.h16[(size_t)m_begin * DFSSM_LORA_R + hi0]);  // stand-alone op with LoRA
   }
 
   // ---- this workgroup's bits (registers, loaded once for every row block) and epilogue rows,
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   const bool conv_row = MODE == DFSSM_MODE_IN && a.conv_state && nrow && ch >= 0 && ch < a.conv_c;
   if (nrow) {
     if (a.wscale) ws_raw = a.wscale[n];
-    if (MODE != DFSSM_MODE_SCAFFOLD) {
+    if (MODE != DFSSM_MODE_SCAFFOLD || a.lA) {
       la = *(const u32x4*)(a.lA + (size_t)n * DFSSM_LORA_R);
       as_raw = a.lAs[n];
     }
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
       }
       if (tid < MP * DFSSM_LORA_R) {
         const int m = tid >> 4;
-        hl[m][tid & 15] = (a.h && m < MB) ? a.h[(size_t)(m0 + m) * DFSSM_LORA_R + (tid & 15)] : 0.0f;
+        const size_t hidx = (size_t)(m0 + m) * DFSSM_LORA_R + (tid & 15);
+        hl[m][tid & 15] = m >= MB ? 0.0f : (a.h ? a.h[hidx] : (a.h16 ? h2f(a.h16[hidx]) : 0.0f));
       }
       if (tid < MP) xsl[tid] = tid < MB ? (a.xs ? a.xs[m0 + tid] : (a.xs16 ? h2f(a.xs16[m0 + tid]) : 0.0f)) : 0.0f;
     } else if (m0 > m_begin) {
@@ -174,6 +176,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         }
         if (i0 == 0) {
           if (a.h) hv = a.h[(size_t)m0 * DFSSM_LORA_R + hi];
+          else if (a.h16) hv = h2f(a.h16[(size_t)m0 * DFSSM_LORA_R + hi]);
           if (a.xs) xsv = a.xs[m0 + xi];
           else if (a.xs16) xsv = h2f(a.xs16[m0 + xi]);
           lds_barrier();  // the previous block's partials (in qs) have been read
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
         const int accv = MI == 2 ? T : 2 * T - Ssum[mb];
         if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = accv;
         const float y = r16(r16(r16((float)accv) * xsl[mb]) * h2f(ws_raw ^ (uint16_t)zero));
-        if (MODE == DFSSM_MODE_SCAFFOLD) {
+        if (MODE == DFSSM_MODE_SCAFFOLD && !a.lA) {
           if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(y);
           continue;
         }
@@ -274,6 +277,10 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int rr = 0; rr < DFSSM_LORA_R; ++rr) lo += (double)hl[mb][rr] * aqd[rr];
         float out = r16((float)lo + y);
+        if (MODE == DFSSM_MODE_SCAFFOLD) {  // stand-alone op with LoRA: y + LoRA term
+          if (a.out) a.out[(size_t)m * a.ld_out + n] = f2h(out);
+          continue;
+        }
         uint16_t* op = a.out + (size_t)m * a.ld_out + n;
         if (MODE == DFSSM_MODE_IN) {
           if (conv_row) {

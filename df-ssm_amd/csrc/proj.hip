@@ -371,10 +371,56 @@ __global__ __launch_bounds__(kNTs) void scaffold_kernel(ScaffoldArgs a) {
     if (n < a.N) {
       const int acc = 2 * (T[0][m][lane] + T[1][m][lane] + T[2][m][lane] + T[3][m][lane]) - S[m];
       if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = acc;
-      if (a.y_out)
-        a.y_out[(size_t)m * a.N + n] = f2h(r16(r16((float)acc) * h2f(a.xscale[m])) * h2f(a.wscale[n]));
+      if (a.y_out) {
+        const float y = r16(r16(r16((float)acc) * h2f(a.xscale[m])) * h2f(a.wscale[n]));
+        float out = y;
+        if (a.lA) {  // LoRA term: sum_r h[m][r] * fp16(A_i8[n][r] * A_s[n]) (exact products, fp64)
+          const u32x4 la = *(const u32x4*)(a.lA + (size_t)n * DFSSM_LORA_R);
+          const float as = h2f(a.lAs[n]);
+          double lo = 0.0;
+#pragma unroll
+          for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
+            const float aq = r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * as);
+            lo += (double)h2f(a.h16[(size_t)m * DFSSM_LORA_R + rr]) * (double)aq;
+          }
+          out = r16((float)lo + y);
+        }
+        a.y_out[(size_t)m * a.N + n] = f2h(out);
+      }
     }
   }
+}
+
+// LoRA intermediates of the stand-alone scaffold op: workgroup (r, m) of K / 8 threads,
+// h[m][r] = fp16(sum_k xn[m][k] * lBq[r][k]); fp16 x fp16 products are exact in fp32 and summed
+// in fp64 (the sum of prep_kernel and the one-launch layer).
+__global__ __launch_bounds__(kPT) void lora_h_kernel(LoraHArgs a) {
+  __shared__ double red[kPW];
+  const int r = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+  const u32x4 xv = *(const u32x4*)(a.xn + (size_t)m * a.K + 8 * tid);
+  const u32x4 bv = *(const u32x4*)(a.lBq + (size_t)r * a.K + 8 * tid);
+  double acc = 0.0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = h2f((uint16_t)(xv[e >> 1] >> (16 * (e & 1))));
+    const float b = h2f((uint16_t)(bv[e >> 1] >> (16 * (e & 1))));
+    acc += (double)(x * b);
+  }
+  const int nw = (int)blockDim.x >> 6;
+  acc = wave_sum_dpp_f64(acc);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    a.h[(size_t)m * DFSSM_LORA_R + r] = f2h((float)t);
+  }
+}
+
+hipError_t launch_lora_h(const LoraHArgs& a, int M, hipStream_t s) {
+  if (a.K > kMaxK || a.K % 512) return hipErrorInvalidValue;  // K / 8 threads: whole waves
+  hipLaunchKernelGGL(lora_h_kernel, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
+  return hipGetLastError();
 }
 
 // Re-tile row-major (N, K/32) sign-bit words into [N_pad/64][K/128][64][4].

@@ -66,6 +66,34 @@ def _dev(a: np.ndarray, dev) -> torch.Tensor:
     return torch.from_numpy(a).to(dev)
 
 
+# Bits of the workspace error flag (set by the kernels, read and cleared by DFSSMModel).
+ERR_TOKEN_RANGE = 1    # a token id outside [0, vocab) reached the embedding gather (row 0 was used)
+ERR_WAIT_TIMEOUT = 4   # a bounded wait inside the one-launch layer timed out (workgroups not co-resident)
+
+
+def describe_error_flag(flag: int) -> str:
+    """Human-readable causes of a nonzero workspace error flag."""
+    causes = []
+    if flag & ERR_TOKEN_RANGE:
+        causes.append("token id out of range [0, vocab) in a device token tensor (embedding row 0 was used)")
+    if flag & ERR_WAIT_TIMEOUT:
+        causes.append("a wait between workgroups of the one-launch layer timed out (the GPU did not run all "
+                      "its workgroups at once, e.g. because another process or stream shared it)")
+    rest = flag & ~(ERR_TOKEN_RANGE | ERR_WAIT_TIMEOUT)
+    if rest:
+        causes.append(f"unknown error bits {rest:#x}")
+    return "; ".join(causes)
+
+
+def _check_token_range(t: torch.Tensor, vocab: int) -> None:
+    """Raise IndexError unless every id of t is in [0, vocab); on a device tensor this syncs."""
+    if t.numel() == 0:
+        return
+    lo, hi = int(t.min()), int(t.max())
+    if lo < 0 or hi >= vocab:
+        raise IndexError(f"token id out of range [0, {vocab}): min {lo}, max {hi}")
+
+
 class StateDensityField:
     """Density-field state at inference (df_ssd_scan, training/df_ssm_mamba2_distill_dfw.py:114-173):
     thresholds (num_banks, K*K) per-bank sorted thresholds (SprayBank.thresholds, :79-91; rows are
@@ -183,18 +211,41 @@ class DFSSMModel:
         # the table (int8 + row scale, or fp16 as the exporter writes it) re-tiled for the head
         row_bytes = D if c.emb_code == EMB_I8 else 2 * D
         emb_src = _dev(w.emb, dev)
-        self.embedding = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, row_bytes), dtype=torch.int8,
-                                     device=dev)
-        _C.check(_C.lib().dfssm_tile_embedding(emb_src.data_ptr(), self.embedding.data_ptr(), c.vocab_size,
+        self.embedding_tiled = torch.empty(_C.lib().dfssm_tiled_emb_bytes(c.vocab_size, row_bytes),
+                                           dtype=torch.int8, device=dev)
+        _C.check(_C.lib().dfssm_tile_embedding(emb_src.data_ptr(), self.embedding_tiled.data_ptr(), c.vocab_size,
                                                row_bytes, _C.stream()), "tile_embedding")
+        self._emb_view = None
         del emb_src
         self.embedding_scale = _dev(w.emb_scale, dev) if c.emb_code == EMB_I8 else None
         self.norm_f_weight = _dev(w.norm_f.astype(np.float32), dev)
         self._descs = descs
-        self._model = _C.Model(dims, descs, self.embedding.data_ptr(),
+        self._model = _C.Model(dims, descs, self.embedding_tiled.data_ptr(),
                                self.embedding_scale.data_ptr() if self.embedding_scale is not None else None,
                                self.norm_f_weight.data_ptr())
         torch.cuda.synchronize(dev)
+
+    @property
+    def embedding(self) -> torch.Tensor:
+        """The (vocab, d_model) fp16 table, as the reference's attribute (df_ssm_inference.py:65,
+        used as norm_out @ embedding.T at :224). The kernels read a re-tiled copy
+        (embedding_tiled, [V/64][row bytes/16][64 rows][16 B]); this row-major view is built from
+        it on first access (a further vocab x d_model x 2 bytes of HBM). For an int8 table
+        (format extension) it is fp16(E_i8 * row scale); the head itself computes
+        fp16(fp32(sum_k xf_k E_i8[v, k]) * scale[v]), which may differ from xf @ embedding.T by
+        the fp16 rounding of the table."""
+        if self._emb_view is None:
+            c = self.cfg
+            rb = c.d_model if c.emb_code == EMB_I8 else 2 * c.d_model
+            vp = (c.vocab_size + 63) // 64 * 64
+            t = self.embedding_tiled.view(torch.uint8).view(vp // 64, rb // 16, 64, 16)
+            rows = t.permute(0, 2, 1, 3).reshape(vp, rb)[:c.vocab_size].contiguous()
+            if c.emb_code == EMB_I8:
+                e = rows.view(torch.int8).float() * self.embedding_scale.float()[:, None]
+                self._emb_view = e.half()
+            else:
+                self._emb_view = rows.view(torch.float16)
+        return self._emb_view
 
     # ------------------------------------------------------------------ state
     def _alloc_state(self):
@@ -308,14 +359,14 @@ class DFSSMModel:
         tok = torch.as_tensor(token_ids).view(-1)
         if tok.numel() != self.batch_size:
             raise ValueError(f"expected {self.batch_size} token ids, got {tok.numel()}")
-        if tok.device.type == "cpu":
-            if int(tok.min()) < 0 or int(tok.max()) >= self.cfg.vocab_size:
-                raise IndexError("token id out of range")
+        _check_token_range(tok, self.cfg.vocab_size)
         self._tok.copy_(tok.to(self.device, torch.int64))
         if self._graph is None:
             self._capture_graph()
         self._graph.replay()
-        return self.logits.clone()
+        out = self.logits.clone()
+        self.check_errors()
+        return out
 
     def _gen_graph(self, S: int):
         if S not in self._gen_graphs:
@@ -338,8 +389,7 @@ class DFSSMModel:
             prompt = prompt.view(-1, 1)
         if prompt.shape[0] != self.batch_size or prompt.shape[1] < 1:
             raise ValueError(f"prompt must be (batch={self.batch_size}, T >= 1), got {tuple(prompt.shape)}")
-        if prompt.device.type == "cpu" and (int(prompt.min()) < 0 or int(prompt.max()) >= self.cfg.vocab_size):
-            raise IndexError("token id out of range")
+        _check_token_range(prompt, self.cfg.vocab_size)
         prompt = prompt.to(self.device, torch.int64).contiguous()
         rows = min(self.PREFILL_MAX_ROWS, self.batch_size * prompt.shape[1])
         rows = max(rows, self.batch_size)
@@ -354,13 +404,17 @@ class DFSSMModel:
             self.workspace.data_ptr(), self._pf_ws.data_ptr(), self._pf_rows,
             self.logits.data_ptr() if want_logits else None, self._next.data_ptr(), 1, _C.stream()), "prefill")
         self._tok.copy_(prompt[:, -1])
-        return self.logits.clone() if want_logits else None
+        out = self.logits.clone() if want_logits else None
+        self.check_errors()
+        return out
 
     def ingest(self, prompt: torch.Tensor, step_by_step: bool = False) -> None:
         """Consume a (batch, T) prompt; afterwards self._next holds the greedy token after the
         prompt and self.x its embedding. By default one layer-major prefill pass; with
         step_by_step, T decode steps (graph replays), which give the same bits."""
-        prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
+        prompt = torch.as_tensor(prompt)
+        _check_token_range(prompt, self.cfg.vocab_size)
+        prompt = prompt.to(self.device, torch.int64)
         if prompt.dim() == 1:
             prompt = prompt.view(-1, 1)
         if not step_by_step:
@@ -371,6 +425,7 @@ class DFSSMModel:
         for t in range(prompt.shape[1]):
             self._tok.copy_(prompt[:, t])
             self._graph.replay()
+        self.check_errors()
 
     def decode(self, n_steps: int, steps_per_graph: int = 8) -> torch.Tensor:
         """n_steps greedy steps continuing from the current state (x holds the embedding of
@@ -385,7 +440,9 @@ class DFSSMModel:
             g.replay()
             out.append(hist.t().clone())
             done += s
-        return torch.cat(out, dim=1)[:, :n_steps]
+        toks = torch.cat(out, dim=1)[:, :n_steps]
+        self.check_errors()
+        return toks
 
     # ------------------------------------------------------------------ sampling
     def _sampler(self, temperature, top_p, penalty, mode, seed):
@@ -465,16 +522,21 @@ class DFSSMModel:
         block_len-token chunk boundary as in training (apply_state_density_field).
         """
         B = self.batch_size
-        self.reset_state()
         if prompt is None:
             prompt = torch.zeros(B, 1, dtype=torch.int64)
-        prompt = torch.as_tensor(prompt).to(self.device, torch.int64)
+        prompt = torch.as_tensor(prompt)
         if prompt.dim() == 1:
             prompt = prompt.view(-1, 1)
+        if prompt.dim() != 2 or prompt.shape[0] != B or prompt.shape[1] < 1:
+            raise ValueError(f"prompt must be (batch={B}, T >= 1), got {tuple(prompt.shape)}")
+        _check_token_range(prompt, self.cfg.vocab_size)  # before any kernel reads the ids
+        self.reset_state()
+        prompt = prompt.to(self.device, torch.int64)
         if state_df is not None:
             if temperature is not None:
                 raise ValueError("state_df is supported with greedy decoding only")
             toks, elapsed = self._generate_state_df(n_tokens, prompt, state_df)
+            self.check_errors()
             self.last_elapsed = elapsed
             if verbose:
                 print(f"batch={B}  {n_tokens} steps (density-field state)  {n_tokens * B} total tokens")
@@ -483,6 +545,7 @@ class DFSSMModel:
         if temperature is not None:
             toks, elapsed = self._generate_sampled(n_tokens, prompt, temperature, top_p, repetition_penalty,
                                                    penalty_mode, seed)
+            self.check_errors()
             self.last_elapsed = elapsed
             if verbose:
                 print(f"batch={B}  {n_tokens} sampled steps  {n_tokens * B} total tokens")
@@ -504,6 +567,7 @@ class DFSSMModel:
         rest = self.decode(n_tokens - 1, S) if n_tokens > 1 else None
         torch.cuda.synchronize(self.device)
         elapsed = time.perf_counter() - start
+        self.check_errors()
         total = n_tokens * B
         if verbose:
             print(f"batch={B}  {n_tokens} steps  {total} total tokens")
@@ -515,9 +579,25 @@ class DFSSMModel:
         return None
 
     def error_flag(self) -> int:
-        """Nonzero if an out-of-range token id reached the embedding kernel."""
+        """The workspace error flag (synchronizes): 0, or an OR of ERR_TOKEN_RANGE (1: a token id
+        outside [0, vocab) reached the embedding gather, which then read row 0) and
+        ERR_WAIT_TIMEOUT (4: a bounded wait between workgroups of the one-launch layer timed out,
+        so that layer's output is wrong). The flag stays set until clear_error_flag()."""
         off = self._err - self.workspace.data_ptr()
         return int(self.workspace[off:off + 4].view(torch.int32).item())
+
+    def clear_error_flag(self) -> None:
+        off = self._err - self.workspace.data_ptr()
+        self.workspace[off:off + 4].zero_()
+
+    def check_errors(self) -> None:
+        """Read the workspace error flag (synchronizes); if it is set, clear it and raise
+        DFSSMError naming the cause. generate(), decode(), forward(), prefill() and ingest()
+        call it after their work."""
+        flag = self.error_flag()
+        if flag:
+            self.clear_error_flag()
+            raise _C.DFSSMError(f"decode kernels reported error flag {flag:#x}: {describe_error_flag(flag)}")
 
 
 if __name__ == "__main__":

@@ -53,12 +53,14 @@ _SIGS = {
     "dfssm_version": (c_int, []),
     "dfssm_error_string": (ctypes.c_char_p, [c_int]),
     "dfssm_check_dims": (c_int, [ctypes.POINTER(Dims)]),
+    "dfssm_one_launch_plan": (c_int, [ctypes.POINTER(Dims), c_int, c_int]),
     "dfssm_tiled_bits_bytes": (c_size_t, [c_int, c_int]),
     "dfssm_tiled_emb_bytes": (c_size_t, [c_int, c_int]),
     "dfssm_tile_bits": (c_int, [P, P, c_int, c_int, P]),
     "dfssm_tile_embedding": (c_int, [P, P, c_int, c_int, P]),
     "dfssm_dequant_lora_b": (c_int, [P, P, c_int, P, P]),
     "dfssm_scaffold_gemm": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
+    "dfssm_scaffold_lora_gemm": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, P]),
     "dfssm_rmsnorm_quantize": (c_int, [P, P, c_int, c_int, P, P, P, P]),
     "dfssm_conv_step": (c_int, [P, P, c_int, P, P, c_int, c_int, P]),
     "dfssm_ssm_step": (c_int, [P, P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),

@@ -40,6 +40,29 @@ def scaffold_gemm(tiled_bits: torch.Tensor, q: torch.Tensor, N: int, xscale=None
     return (acc, y) if want_y else acc
 
 
+def scaffold_lora_gemm(tiled_bits: torch.Tensor, wscale: torch.Tensor, q: torch.Tensor, xscale: torch.Tensor,
+                       xn: torch.Tensor, lA: torch.Tensor, lA_s: torch.Tensor, lBq: torch.Tensor, N: int):
+    """One projection with its LoRA (dfssm_scaffold_lora_gemm): returns (acc int32 (M, N),
+    y fp16 (M, N), lora_h fp16 (M, 16)). q (M, K) int8 with fp16 scales xscale (M,), xn (M, K) fp16,
+    lA (N, 16) int8, lA_s (N,) fp16, lBq (16, K) fp16, wscale (N,) fp16."""
+    _need(q, torch.int8, "q")
+    _need(xn, torch.float16, "xn")
+    _need(lBq, torch.float16, "lBq")
+    _need(lA, torch.int8, "lA")
+    M, K = q.shape
+    if xn.shape != (M, K) or lBq.shape != (16, K) or lA.shape != (N, 16):
+        raise ValueError("shape mismatch: q/xn (M, K), lBq (16, K), lA (N, 16)")
+    acc = torch.empty(M, N, dtype=torch.int32, device=q.device)
+    y = torch.empty(M, N, dtype=torch.float16, device=q.device)
+    h = torch.empty(M, 16, dtype=torch.float16, device=q.device)
+    _C.check(_C.lib().dfssm_scaffold_lora_gemm(
+        tiled_bits.data_ptr(), wscale.contiguous().data_ptr(), q.contiguous().data_ptr(),
+        xscale.contiguous().data_ptr(), xn.contiguous().data_ptr(), lA.contiguous().data_ptr(),
+        lA_s.contiguous().data_ptr(), lBq.contiguous().data_ptr(), M, N, K, h.data_ptr(), acc.data_ptr(),
+        y.data_ptr(), _C.stream()), "scaffold_lora_gemm")
+    return acc, y, h
+
+
 def rmsnorm_quantize(x: torch.Tensor, w: torch.Tensor):
     """x (M, K) fp16, w (K) fp32 -> (xn fp16 (M, K), q int8 (M, K), scale fp16 (M,))."""
     _need(x, torch.float16, "x")

@@ -78,6 +78,15 @@ const char* dfssm_error_string(int code);
 /* 0 if the kernels support `dims`, else DFSSM_E_DIMS / DFSSM_E_BATCH. */
 int dfssm_check_dims(const dfssm_dims* dims);
 
+/* Workgroups of the one-launch layer (batch <= 4) on a device with `cus` compute units where
+ * `blocks_per_cu` of its 1024-thread workgroups fit at once, or 0 when a layer runs as five
+ * kernels instead. The one-launch layer waits between its workgroups, so it is used only when all
+ * of them are resident together (one per CU, blocks_per_cu >= 1 for the instantiation launched).
+ * dfssm_layer_step makes this decision with the current device's values; exposed so that the
+ * rule can be checked without a GPU. No counterpart in the reference (its layers are separate
+ * kernel launches, df_ssm_inference.py:161-207). */
+int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
+
 /* ---- load-time layout ------------------------------------------------------------------ */
 /* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, row_bytes) table
  * (row_bytes = d_model for int8, 2 * d_model for fp16). */
@@ -102,6 +111,22 @@ int dfssm_tile_embedding(const void* src, void* dst, int vocab, int row_bytes, v
 int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
                         const uint16_t* wscale, int M, int N, int K, int32_t* acc_out,
                         uint16_t* y_out, void* stream);
+
+/* Scaffold projection with its rank-16 LoRA correction (one projection of a layer, as an
+ * operator): acc as dfssm_scaffold_gemm (exact int32, written if acc_out is non-NULL),
+ *   lora_h[m][r] = fp16(sum_k xn[m][k] * lBq[r][k])                       (x_norm @ lora_B.T)
+ *   y[m][n] = fp16(fp32(sum_r lora_h[m][r] * fp16(lA[n][r] * lA_s[n])) + fp16(fp16(fp16(acc) *
+ *             xscale[m]) * wscale[n]))                                   (proj.addmm_(..., lora_A.T))
+ * with the sums over exactly representable products in fp64. Replaces _scaffold_matmul plus the
+ * LoRA addmm_ of df_ssm_inference.py:154-158,169-173 (in_proj) and :199-204 (out_proj). xn (M, K)
+ * fp16 are the normalized activations the LoRA reads (q their int8 quantization with scales
+ * xscale); lBq (16, K) is the load-time fp16 LoRA-B table (dfssm_dequant_lora_b); lA (N, 16) int8
+ * and lA_s (N) fp16 as stored in the file. lora_h (M, 16) fp16 receives the intermediates.
+ * M = 1..64 (1..4 on the packed-bit VALU GEMV, 5..64 on the int8 matrix cores). */
+int dfssm_scaffold_lora_gemm(const uint32_t* tiled_bits, const uint16_t* wscale, const int8_t* q,
+                             const uint16_t* xscale, const uint16_t* xn, const int8_t* lA, const uint16_t* lA_s,
+                             const uint16_t* lBq, int M, int N, int K, uint16_t* lora_h, int32_t* acc_out,
+                             uint16_t* y_out, void* stream);
 
 /* RMSNorm + int8 quantization of M rows (the prologue of every projection):
  * xn = fp16((x * r) * w), q = int8 activations, s = fp16 scales.

@@ -107,3 +107,65 @@ class RefCPUModel:
             tok = int(np.argmax(self.forward(tok)))
             out.append(tok)
         return out, time.perf_counter() - t0
+
+
+def cpu_description() -> dict:
+    """CPU model, sockets and physical cores per socket from /proc/cpuinfo; CPUs this process may
+    run on from its affinity mask."""
+    model, phys, cores = "unknown", set(), {}
+    cur = {}
+    try:
+        text = open("/proc/cpuinfo").read()
+    except OSError:
+        text = ""
+    for block in text.split("\n\n"):
+        cur = {}
+        for ln in block.splitlines():
+            if ":" in ln:
+                k, v = ln.split(":", 1)
+                cur[k.strip()] = v.strip()
+        if "model name" in cur:
+            model = cur["model name"]
+        if "physical id" in cur:
+            phys.add(cur["physical id"])
+            if "cpu cores" in cur:
+                cores[cur["physical id"]] = int(cur["cpu cores"])
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    per_socket = max(cores.values()) if cores else (os.cpu_count() or 1)
+    return {"model": model, "sockets": max(1, len(phys)), "cores_per_socket": per_socket,
+            "logical_cpus": os.cpu_count(), "allowed_cpus": allowed}
+
+
+def main(argv=None) -> int:
+    """Time the reference CPU decode on a .dfssm file: the protocol of generate() above, printed as
+    one JSON line. OpenMP threads come from the environment (OMP_NUM_THREADS, OMP_PROC_BIND,
+    OMP_PLACES), read when the library loads."""
+    import argparse
+    import json
+    import sys
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--model", required=True)
+    ap.add_argument("--prompt", required=True, help="comma-separated token ids")
+    ap.add_argument("--tokens", type=int, default=128)
+    a = ap.parse_args(argv)
+    repo = os.path.dirname(_HERE)
+    sys.path.insert(0, os.path.join(repo, "df-ssm_amd"))
+    from dfssm.format import read_dfssm
+    if not available():
+        print(json.dumps({"error": "reference CPU kernels unavailable (not built or no AVX-512 VNNI)"}))
+        return 1
+    w = read_dfssm(a.model)
+    prompt = [int(t) for t in a.prompt.split(",")]
+    m = RefCPUModel(w)
+    toks, secs = m.generate(prompt, a.tokens)
+    print(json.dumps({"tokens": a.tokens, "seconds": secs, "tok_s": a.tokens / secs,
+                      "threads": int(os.environ.get("OMP_NUM_THREADS", "0") or 0),
+                      "first_tokens": toks[:8]}))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
