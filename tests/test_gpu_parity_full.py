@@ -56,8 +56,9 @@ def test_scaffold_lora_op_bit_exact(N, K, M):
 
     tb = ops.tile_bits(torch.from_numpy(bits.view(np.int32)).to(DEV), N, K)
     lBq = torch.empty(16, K, dtype=torch.float16, device=DEV)
-    _C.check(_C.lib().dfssm_dequant_lora_b(torch.from_numpy(lB).to(DEV).data_ptr(), _h(lBs).data_ptr(), K,
-                                           lBq.data_ptr(), _C.stream()))
+    tB, tBs = torch.from_numpy(lB).to(DEV), _h(lBs)  # kept alive until the kernel has run
+    _C.check(_C.lib().dfssm_dequant_lora_b(tB.data_ptr(), tBs.data_ptr(), K, lBq.data_ptr(), _C.stream()))
+    torch.cuda.synchronize()
     acc, y, h = ops.scaffold_lora_gemm(tb, _h(ws), torch.from_numpy(q).to(DEV), _h(xs), _h(xn),
                                        torch.from_numpy(lA).to(DEV), _h(lAs), lBq, N)
     acc_r = O.scaffold_acc(bits, q)
