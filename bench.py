@@ -382,6 +382,69 @@ def phase_sweep(B, path, layers=12):
     log(f"phase sweep batch {B}: {layers} layers x 5 kernels + head done")
 
 
+TIMELINE_STAMPS = {0: "start", 1: "A: prologue done (GEMV workgroups)", 2: "A: GEMV done", 3: "A: LoRA h in",
+                   4: "A: epilogue / LoRA rank stored", 5: "B: poll start", 6: "B: item inputs in",
+                   7: "B: SSM done", 8: "C: prologue start", 9: "C: prologue done (g in)", 10: "C: GEMV done",
+                   11: "C: LoRA h in", 12: "C: epilogue / LoRA rank stored", 13: "end"}
+
+
+def timeline(B, path, graphs=4):
+    """Per-phase wall-clock timeline of the one-launch layer (batch <= 4) from the profiling build
+    libdfssm_hip_timeline.so (s_memrealtime stamps per workgroup, 10 ns resolution), measured on the
+    last 64 layer launches of `graphs` replays of 8-step decode graphs (warm, as in the timed
+    decode). Per stamp: the earliest, median and latest workgroup, in us after the launch's first
+    workgroup started, as the median over launches; and the gap from one launch's last workgroup
+    to the next launch's first."""
+    import numpy as np
+    import torch
+    from dfssm import _C
+    from dfssm import build as dfb
+    from dfssm.synth import make_prompts
+    if not os.path.exists(dfb.LIB_TIMELINE):
+        raise SystemExit(f"{dfb.LIB_TIMELINE} not built (python -m dfssm.build)")
+    _C.LIB_PATH = dfb.LIB_TIMELINE
+    lib = _C.lib()
+    lib.dfssm_timeline_read.restype = ctypes.c_int
+    lib.dfssm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    m, _ = build_model(B, path)
+    m.ingest(torch.from_numpy(make_prompts(B, m.cfg.vocab_size, 8)))
+    g, _ = m._gen_graph(STEPS_PER_GRAPH)
+    for _ in range(graphs):
+        g.replay()
+    torch.cuda.synchronize()
+    buf = np.zeros((64, 256, 16), np.uint64)
+    _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
+    t = buf.astype(np.int64)
+    starts = np.where(t[:, :, 0] > 0, t[:, :, 0], np.iinfo(np.int64).max).min(axis=1)
+    ends = t[:, :, 13].max(axis=1)
+    order = np.argsort(starts)
+    rows = {k: [] for k in TIMELINE_STAMPS}
+    gaps, lengths = [], []
+    for i, sl in enumerate(order):
+        if starts[sl] == np.iinfo(np.int64).max:
+            continue
+        lengths.append((ends[sl] - starts[sl]) * 0.01)
+        if i > 0:
+            gaps.append((starts[sl] - ends[order[i - 1]]) * 0.01)
+        for k in TIMELINE_STAMPS:
+            v = t[sl, :, k]
+            v = (v[v > 0] - starts[sl]) * 0.01
+            if v.size:
+                rows[k].append((v.min(), np.median(v), v.max(), v.size))
+    out = {"batch": B, "launches": len(lengths), "layer_us_median": round(float(np.median(lengths)), 2),
+           "gap_us_median": round(float(np.median(gaps)), 2) if gaps else None, "stamps": {}}
+    log(f"timeline batch {B}: {len(lengths)} launches, layer {out['layer_us_median']} us (first start to last end), "
+        f"gap to the next launch {out['gap_us_median']} us (median; the head runs in one gap per step)")
+    for k, name in TIMELINE_STAMPS.items():
+        if rows[k]:
+            a = np.array(rows[k])
+            med = np.median(a, axis=0)
+            out["stamps"][name] = {"min": round(float(med[0]), 2), "median": round(float(med[1]), 2),
+                                   "max": round(float(med[2]), 2), "workgroups": int(med[3])}
+            log(f"  {name:38s} min {med[0]:6.2f}  med {med[1]:6.2f}  max {med[2]:6.2f} us  ({int(med[3])} WGs)")
+    return out
+
+
 def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
     """Decode throughput and per-kernel timing at batch B (one model instance)."""
     import torch
@@ -532,12 +595,18 @@ def main():
     ap.add_argument("--phase-sweep", type=int, default=0,
                     help="only run the five layer kernels on 12 layers and the head at this batch (counter runs)")
     ap.add_argument("--scaffold", type=int, default=1, help="run the rotated scaffold microbench (0: skip)")
+    ap.add_argument("--timeline", type=int, default=0,
+                    help="only print the per-phase timeline of the one-launch layer at this batch (1..4), "
+                         "from the profiling build libdfssm_hip_timeline.so")
     a = ap.parse_args()
     if a.copy_mib:
         copy_calibration(a.copy_mib)
         return
     if a.phase_sweep:
         phase_sweep(a.phase_sweep, a.model_path)
+        return
+    if a.timeline:
+        print(json.dumps(timeline(a.timeline, a.model_path)), flush=True)
         return
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "

@@ -68,6 +68,29 @@ __device__ __forceinline__ int bix() {
   return t;
 }
 
+// Profiling builds (-DDFSSM_TIMELINE, libdfssm_hip_timeline.so): wall-clock stamps
+// (s_memrealtime, 100 MHz) of the phases of every workgroup, kept in LDS by thread 0 and written
+// at the end of the launch to dfssm_timeline[launch % kTlSlots][workgroup][stamp]; read on the host
+// with dfssm_timeline_read. Product builds compile TL(k) to nothing.
+#ifdef DFSSM_TIMELINE
+constexpr int kTlSlots = 64, kTlWg = 256, kTlStamps = 16;
+__device__ unsigned long long dfssm_timeline[kTlSlots][kTlWg][kTlStamps];
+#define TL_DECL __shared__ unsigned long long tl_s[kTlStamps]
+#define TL(k)                                                                   \
+  do {                                                                          \
+    if (tix() == 0) tl_s[k] = __builtin_amdgcn_s_memrealtime();                 \
+  } while (0)
+#define TL_FLUSH(slot)                                                          \
+  do {                                                                          \
+    if (tix() < kTlStamps && bix() < kTlWg)                                     \
+      dfssm_timeline[(slot) % kTlSlots][bix()][tix()] = tl_s[tix()];            \
+  } while (0)
+#else
+#define TL_DECL
+#define TL(k) do {} while (0)
+#define TL_FLUSH(slot) do {} while (0)
+#endif
+
 template <class T>
 __device__ __forceinline__ T ld_dev(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -624,6 +647,12 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
 template <int M, int RC>
 __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   __shared__ FusedLds<M> L;
+  TL_DECL;
+#ifdef DFSSM_TIMELINE
+  if (tix() < kTlStamps) tl_s[tix()] = 0ull;
+  __syncthreads();
+#endif
+  TL(0);
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, wg = bix();
   // The launch's epoch is the first load; its tag is derived where it is used (tag_now): the
@@ -656,6 +685,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
   if (wg < gA) {
     prologue<M, false>(L, pa, nullptr, a.D, 0u, a.err);  // no polls in the IN prologue
+    TL(1);
     for (int grp = wg; grp < gA; grp += G) {
       if (grp != wg) {
         load_bits(wa, a.in_bits, grp, a.D);
@@ -663,14 +693,18 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       }
       const uint32_t hv = lora_issue(hA, M);
       gemv_partials<M>(L, wa, a.D);
+      TL(2);
       const uint32_t tag = tag_now();
       lora_finish<M>(L, hA, hv, tag, a.err);
       __syncthreads();
+      TL(3);
       store_conv(epilogue<M, true>(L, a, ea, grp, tag));
+      TL(4);
       __syncthreads();
     }
   } else if (wg < gA + DFSSM_LORA_R) {
     lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err);
+    TL(4);
   }
   // ---- phase B: SSM + gate ----
   u32x4 wc[RC < 64 ? 1 : kFMaxCPW];
@@ -695,19 +729,24 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       }
     }
     const uint32_t tag = tag_now();
+    TL(5);
     for (int k = 0; k < nk; ++k) poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
     __syncthreads();
+    TL(6);
 #pragma unroll
     for (int k = 0; k < kMaxItems; ++k)
       if (k < nk) ssm_item<M>(L, a, k, item_of(a, wg + k * G), hk[k], dk[k], tag);
   }
   // ---- phase C: out_proj + residual (workgroups < gC), LoRA ranks (gC .. gC + 15) ----
+  TL(7);
   if (wg < gC) {
     __syncthreads();  // LDS reuse after phase A
     PIn<M> pc;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
     const uint32_t tag = tag_now();
+    TL(8);
     prologue<M, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);  // the chunks of the wave's GEMV
+    TL(9);
     for (int grp = wg; grp < gC; grp += G) {
       if (grp != wg) {
         if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, grp, a.DI);
@@ -717,17 +756,26 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       const uint32_t hv = lora_issue(hC, M);
       if constexpr (RC < 64) gemv_partials_rg<M, RC>(L, wcr, a.DI);
       else gemv_partials<M>(L, wc, a.DI);
+      TL(10);
       lora_finish<M>(L, hC, hv, tag, a.err);
       __syncthreads();
+      TL(11);
       (void)epilogue<M, false, RC>(L, a, ec, grp, tag);
+      TL(12);
       __syncthreads();
     }
   } else if (wg < gC + DFSSM_LORA_R) {
     __syncthreads();
     lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err);
+    TL(12);
   }
   __syncthreads();  // every wave of this workgroup has read its launch count
   if (tid == 0) st_dev(a.launches + wg, epoch_raw + 1u);
+  TL(13);
+#ifdef DFSSM_TIMELINE
+  __syncthreads();
+  TL_FLUSH(epoch_raw);
+#endif
 }
 
 // The one-launch layer waits between its workgroups, so all G of them must be resident at once:
@@ -832,3 +880,11 @@ hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
 }
 
 }  // namespace dfssm
+
+#ifdef DFSSM_TIMELINE
+// Copies the whole stamp array (kTlSlots x kTlWg x kTlStamps u64) to host memory.
+extern "C" int dfssm_timeline_read(void* host, size_t bytes) {
+  if (bytes < sizeof(dfssm::dfssm_timeline)) return -5;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dfssm::dfssm_timeline), sizeof(dfssm::dfssm_timeline));
+}
+#endif

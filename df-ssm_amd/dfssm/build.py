@@ -23,6 +23,9 @@ REPO = os.path.dirname(ROOT)
 CSRC = os.path.join(ROOT, "csrc")
 BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libdfssm_hip.so")
+# profiling variant: the one-launch layer with per-phase wall-clock stamps (-DDFSSM_TIMELINE)
+LIB_TIMELINE = os.path.join(PKG, "libdfssm_hip_timeline.so")
+TIMELINE_SRCS = ("fused.hip",)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -31,9 +34,9 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-I" + os.path.join(REPO, "include"), "-I" + CSRC]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+def _compile(src: str, timeline: bool = False) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", "_tl.o" if timeline else ".o"))
+    cmd = [HIPCC] + FLAGS + (["-DDFSSM_TIMELINE"] if timeline else []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -46,16 +49,21 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc not found")
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
-    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}")
+    tl_srcs = [p for p in srcs if os.path.basename(p) in TIMELINE_SRCS]
+    jobs = [(p, False) for p in srcs] + [(p, True) for p in tl_srcs]
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        built = list(ex.map(lambda j: _compile(*j), jobs))
+    objs = built[:len(srcs)]
+    tl_objs = [o for p, o in zip(srcs, objs) if p not in tl_srcs] + built[len(srcs):]
+    for out, parts in ((LIB, objs), (LIB_TIMELINE, tl_objs)):
+        tmp = out + ".tmp"
+        r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + parts + ["-o", tmp],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stderr}")
+        os.replace(tmp, out)
+        if verbose:
+            print(f"built {out}")
     return LIB
 
 
