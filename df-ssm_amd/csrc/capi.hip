@@ -2,6 +2,9 @@
 // Declarations and conventions: include/dfssm.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
+
+#include <mutex>
 
 #include "dfssm.h"
 #include "dfssm_kernels.h"
@@ -113,6 +116,10 @@ const char* dfssm_error_string(int code) {
     case DFSSM_E_BATCH: return "batch size not supported (1..64)";
     case DFSSM_E_ALIGN: return "pointer or leading dimension misaligned (16-byte rows required)";
     case DFSSM_E_RANGE: return "index out of range";
+    case DFSSM_E_SCRATCH:
+      return "the decode workspace of these dimensions exceeds the static workspace (DFSSM_STATIC_WORKSPACE_BYTES)";
+    case DFSSM_E_CAPTURE:
+      return "the first call for these dimensions on a device must not be captured (it clears the static workspace)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }
@@ -628,6 +635,90 @@ int dfssm_prefill(const dfssm_model* model, const int64_t* tokens, int n_tokens,
   rc = hip_status(launch_last_rows((const uint16_t*)(pw + pf_layout(r, r.B * tc).x), x, r.B, tc, r.D, s));
   if (rc) return rc;
   return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
+}
+
+}  // extern "C"
+
+// ---- decode step without a caller workspace (no allocation) ---------------------------------
+// The decode workspace lives in `scratch`, a file-scope device array of
+// DFSSM_STATIC_WORKSPACE_BYTES that every GPU the library runs on holds until the process ends.
+// Host code never passes `scratch` itself (its name is a host-side stand-in, not a device
+// address): the device address comes from hipGetSymbolAddress, once per device, and is kept per
+// device. The part of the workspace that must start at zero (tickets, error flag, launch counts
+// and exchange words of the one-launch layer) is cleared by a fill kernel when a device is first
+// used and whenever the model dimensions change (the layout depends on them); nothing is cleared
+// on later calls with the same dimensions, which share the array's contents in stream order.
+static __device__ __align__(256) unsigned char scratch[DFSSM_STATIC_WORKSPACE_BYTES];
+
+namespace {
+
+constexpr int kStaticMaxDevices = 64;
+struct StaticWs {
+  void* ptr = nullptr;
+  bool cleared = false;
+  dfssm_dims dims{};
+};
+StaticWs g_static[kStaticMaxDevices];
+std::mutex g_static_mu;
+
+__global__ void take_flag_kernel(int* flag, int* out) {
+  if (threadIdx.x == 0) {
+    *out = *flag;
+    *flag = 0;
+  }
+}
+
+// Device address of this device's static workspace, cleared for `dims` if it was last used with
+// other dimensions (or never). Returns a DFSSM code.
+int static_workspace(const dfssm_dims* dims, hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  if (dev < 0 || dev >= kStaticMaxDevices) return DFSSM_E_RANGE;
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  StaticWs& st = g_static[dev];
+  if (!st.ptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e);
+    if (!p) return DFSSM_E_NULL;
+    st.ptr = p;
+  }
+  if (!st.cleared || memcmp(&st.dims, dims, sizeof(dfssm_dims)) != 0) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_status(e);
+    if (cs != hipStreamCaptureStatusNone) return DFSSM_E_CAPTURE;
+    const int rc = dfssm_workspace_init(dims, st.ptr, stream);  // a fill kernel, no memset
+    if (rc) return rc;
+    st.dims = *dims;
+    st.cleared = true;
+  }
+  *out = st.ptr;
+  return DFSSM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dfssm_decode_step_static(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
+                             const dfssm_state* state, uint16_t* logits, int64_t* next, int fuse_next_embed,
+                             int* error_out, void* stream) {
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (!x || !state || !next) return DFSSM_E_NULL;
+  const size_t need = dfssm_workspace_bytes(&model->dims);
+  if (need == 0) return DFSSM_E_DIMS;
+  if (need > (size_t)DFSSM_STATIC_WORKSPACE_BYTES) return DFSSM_E_SCRATCH;
+  hipStream_t s = as_stream(stream);
+  void* ws = nullptr;
+  rc = static_workspace(&model->dims, s, &ws);
+  if (rc) return rc;
+  rc = dfssm_decode_step(model, tokens, x, state, ws, logits, next, fuse_next_embed, stream);
+  if (rc || !error_out) return rc;
+  hipLaunchKernelGGL(take_flag_kernel, dim3(1), dim3(64), 0, s, dfssm_workspace_error_flag(&model->dims, ws), error_out);
+  return hip_status(hipGetLastError());
 }
 
 int dfssm_state_density_field(float* h, float* sd_error, int64_t rows, int d_state, const float* thresholds,

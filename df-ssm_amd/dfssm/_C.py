@@ -72,6 +72,7 @@ _SIGS = {
     "dfssm_layer_phase": (c_int, [ctypes.POINTER(Model), c_int, c_int, P, ctypes.POINTER(State), P, P]),
     "dfssm_lmhead_argmax": (c_int, [ctypes.POINTER(Model), P, P, P, P, P, P]),
     "dfssm_decode_step": (c_int, [ctypes.POINTER(Model), P, P, ctypes.POINTER(State), P, P, P, c_int, P]),
+    "dfssm_decode_step_static": (c_int, [ctypes.POINTER(Model), P, P, ctypes.POINTER(State), P, P, c_int, P, P]),
     "dfssm_state_density_field": (c_int, [P, P, ctypes.c_int64, c_int, P, c_int, c_int, P]),
     "dfssm_sample": (c_int, [ctypes.POINTER(Model), P, P, P, ctypes.POINTER(SampleParams), P, P, P, P]),
     "dfssm_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(Dims), c_int]),

@@ -34,6 +34,8 @@ extern "C" {
 #define DFSSM_E_BATCH (-3)       /* batch size not supported */
 #define DFSSM_E_ALIGN (-4)       /* pointer or leading dimension misaligned */
 #define DFSSM_E_RANGE (-5)       /* index (layer, token count, size) out of range */
+#define DFSSM_E_SCRATCH (-6)     /* the static workspace is too small for these dimensions */
+#define DFSSM_E_CAPTURE (-7)     /* the call must not run under stream capture */
 
 typedef struct dfssm_dims {
   int32_t n_layer, d_model, d_inner, d_state, nheads, headdim, ngroups, vocab_size;
@@ -187,6 +189,24 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
 int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
                       const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
                       int fuse_next_embed, void* stream);
+
+/* ---- decode step without a workspace argument (allocates nothing) ----------------------- */
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): dfssm_decode_step with
+ * its workspace in a library-owned static device array of DFSSM_STATIC_WORKSPACE_BYTES, which
+ * each GPU the library runs on holds until the process ends. Dimensions whose
+ * dfssm_workspace_bytes exceeds it are rejected with DFSSM_E_SCRATCH (24 MiB covers batch <= 32
+ * at the 1.3B and 2.7B shapes). All calls on one GPU share that GPU's array: calls that overlap
+ * on one GPU (other streams, other threads) race; calls ordered on one stream do not. The first
+ * call on a device, and the first after the dimensions change, clears the array's counters with a
+ * fill kernel on `stream` and must not be captured (else DFSSM_E_CAPTURE); later calls may be.
+ * error_out (device int, may be NULL) receives the workspace error flag of this call (as
+ * dfssm_workspace_error_flag: 1 = token id out of range, 4 = a wait of the one-launch layer timed
+ * out), which is then cleared. Every other argument is as in dfssm_decode_step. */
+#define DFSSM_STATIC_WORKSPACE_BYTES (24u << 20)
+int dfssm_decode_step_static(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
+                             const dfssm_state* state, uint16_t* logits, int64_t* next, int fuse_next_embed,
+                             int* error_out, void* stream);
 
 /* ---- sampling ------------------------------------------------------------------------ */
 typedef struct dfssm_sample_params {
