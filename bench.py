@@ -69,6 +69,10 @@ def algorithmic_bytes(cfg, B):
     return weights, state, per_phase
 
 
+LAYER_KERNELS = {"auto": 0, "fused": 1, "five": 2, "item": 3}  # dfssm_set_layer_kernel codes
+LAYER_KERNEL = "auto"
+
+
 def build_model(B, path, shape="1p3b"):
     import torch
     from df_ssm_inference import DFSSMModel
@@ -86,6 +90,10 @@ def build_model(B, path, shape="1p3b"):
     m = DFSSMModel(path, device="cuda:0", batch_size=B)
     torch.cuda.synchronize()
     log(f"loaded {path} for batch {B} ({time.time() - t:.1f}s)")
+    if LAYER_KERNEL != "auto":
+        from dfssm import _C
+        _C.lib().dfssm_set_layer_kernel(LAYER_KERNELS[LAYER_KERNEL])
+        log(f"layer kernel: {LAYER_KERNEL}")
     return m, w
 
 
@@ -382,6 +390,20 @@ def phase_sweep(B, path, layers=12):
     log(f"phase sweep batch {B}: {layers} layers x 5 kernels + head done")
 
 
+TIMELINE1_STAMPS = {0: "start", 16: "A: x loaded (control wave 0)", 17: "A: weights in LDS (stream wave 0)",
+                    14: "A: norm, sum of squares barrier (B1)", 18: "A: norm, xn done (control wave 0)",
+                    19: "B: last B|C poll issued (control wave 0)", 15: "A: norm, xn + max barrier (B2)",
+                    20: "A: quantizer + LoRA partial (control wave 0)", 21: "A: B|C rows published (stream wave 3)",
+                    22: "C: last g poll issued (control wave 0)", 1: "A: quantizer + planes done (B3)",
+                    23: "A: LoRA partials polled (control wave 0)", 24: "A: GEMV done (stream wave 0)",
+                    2: "A: LoRA partials in, GEMV done (B4)", 3: "A: LoRA h summed (B5)",
+                    12: "A: z rows done (stream wave 0)", 4: "B: B|C poll returned", 5: "B: B|C in (B6)",
+                    6: "B: SSM done, g published (B7)", 11: "C: g poll returned", 7: "C: all g in (B8)",
+                    25: "C: g loaded (control wave 0)", 26: "C: norm, sum of squares barrier (B9)",
+                    31: "C: norm, done (control wave 0)", 27: "C: norm, xn + max barrier (B10)",
+                    29: "C: quantizer (control wave 0)", 28: "C: quantizer + LoRA partial (control wave 1)",
+                    30: "C: quantizer (stream wave 0)", 8: "C: quantizer + planes done (B11)",
+                    9: "C: LoRA partials in, GEMV done (B12)", 10: "C: LoRA h summed (B13)", 13: "end"}
 TIMELINE_STAMPS = {0: "start", 1: "A: prologue done (GEMV workgroups)", 2: "A: GEMV done", 3: "A: LoRA h in",
                    4: "A: epilogue / LoRA rank stored", 5: "B: poll start", 6: "B: item inputs in",
                    7: "B: SSM done", 8: "C: prologue start", 9: "C: prologue done (g in)", 10: "C: GEMV done",
@@ -404,21 +426,29 @@ def timeline(B, path, graphs=4):
         raise SystemExit(f"{dfb.LIB_TIMELINE} not built (python -m dfssm.build)")
     _C.LIB_PATH = dfb.LIB_TIMELINE
     lib = _C.lib()
-    lib.dfssm_timeline_read.restype = ctypes.c_int
-    lib.dfssm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    for fn in (lib.dfssm_timeline_read, lib.dfssm_timeline1_read):
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     m, _ = build_model(B, path)
     m.ingest(torch.from_numpy(make_prompts(B, m.cfg.vocab_size, 8)))
     g, _ = m._gen_graph(STEPS_PER_GRAPH)
     for _ in range(graphs):
         g.replay()
     torch.cuda.synchronize()
-    buf = np.zeros((64, 256, 16), np.uint64)
-    _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
+    # the layer kernel that ran left its stamps: the item-organised layer (timeline1) or the
+    # phase-organised one
+    buf = np.zeros((64, 256, 32), np.uint64)
+    _C.check(lib.dfssm_timeline1_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline1_read")
+    names, kernel = TIMELINE1_STAMPS, "layer_item_kernel"
+    if not buf.any():
+        buf = np.zeros((64, 256, 16), np.uint64)
+        _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
+        names, kernel = TIMELINE_STAMPS, "layer_fused_kernel"
     t = buf.astype(np.int64)
     starts = np.where(t[:, :, 0] > 0, t[:, :, 0], np.iinfo(np.int64).max).min(axis=1)
     ends = t[:, :, 13].max(axis=1)
     order = np.argsort(starts)
-    rows = {k: [] for k in TIMELINE_STAMPS}
+    rows = {k: [] for k in names}
     gaps, lengths = [], []
     for i, sl in enumerate(order):
         if starts[sl] == np.iinfo(np.int64).max:
@@ -426,22 +456,21 @@ def timeline(B, path, graphs=4):
         lengths.append((ends[sl] - starts[sl]) * 0.01)
         if i > 0:
             gaps.append((starts[sl] - ends[order[i - 1]]) * 0.01)
-        for k in TIMELINE_STAMPS:
+        for k in names:
             v = t[sl, :, k]
             v = (v[v > 0] - starts[sl]) * 0.01
             if v.size:
                 rows[k].append((v.min(), np.median(v), v.max(), v.size))
-    out = {"batch": B, "launches": len(lengths), "layer_us_median": round(float(np.median(lengths)), 2),
+    out = {"kernel": kernel, "batch": B, "launches": len(lengths), "layer_us_median": round(float(np.median(lengths)), 2),
            "gap_us_median": round(float(np.median(gaps)), 2) if gaps else None, "stamps": {}}
-    log(f"timeline batch {B}: {len(lengths)} launches, layer {out['layer_us_median']} us (first start to last end), "
+    log(f"timeline {kernel} batch {B}: {len(lengths)} launches, layer {out['layer_us_median']} us (first start to last end), "
         f"gap to the next launch {out['gap_us_median']} us (median; the head runs in one gap per step)")
-    for k, name in TIMELINE_STAMPS.items():
-        if rows[k]:
-            a = np.array(rows[k])
-            med = np.median(a, axis=0)
-            out["stamps"][name] = {"min": round(float(med[0]), 2), "median": round(float(med[1]), 2),
-                                   "max": round(float(med[2]), 2), "workgroups": int(med[3])}
-            log(f"  {name:38s} min {med[0]:6.2f}  med {med[1]:6.2f}  max {med[2]:6.2f} us  ({int(med[3])} WGs)")
+    meds = {k: np.median(np.array(rows[k]), axis=0) for k in names if rows[k]}
+    for k in sorted(meds, key=lambda k: (k == 13, meds[k][1])):  # in time order, the end last
+        med, name = meds[k], names[k]
+        out["stamps"][name] = {"min": round(float(med[0]), 2), "median": round(float(med[1]), 2),
+                               "max": round(float(med[2]), 2), "workgroups": int(med[3])}
+        log(f"  {name:46s} min {med[0]:6.2f}  med {med[1]:6.2f}  max {med[2]:6.2f} us  ({int(med[3])} WGs)")
     return out
 
 
@@ -598,7 +627,11 @@ def main():
     ap.add_argument("--timeline", type=int, default=0,
                     help="only print the per-phase timeline of the one-launch layer at this batch (1..4), "
                          "from the profiling build libdfssm_hip_timeline.so")
+    ap.add_argument("--layer-kernel", choices=sorted(LAYER_KERNELS), default="auto",
+                    help="layer kernel at batch <= 4 (dfssm_set_layer_kernel; auto: the library's default)")
     a = ap.parse_args()
+    global LAYER_KERNEL
+    LAYER_KERNEL = a.layer_kernel
     if a.copy_mib:
         copy_calibration(a.copy_mib)
         return

@@ -34,7 +34,7 @@ Derived derive(const dfssm_dims* d) {
 
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
-      proj_t, g_t, h_t, dt_t, total;
+      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -64,8 +64,16 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.gtick = off;    off = align_up(off + (size_t)r.head_groups * 4);
   w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
   w.g_t = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
-  w.h_t = off;      off = align_up(off + 2 * (size_t)r.B * 16 * 4);
+  w.h_t = off;      off = align_up(off + (size_t)kXRep * kHStride * 4);
   w.dt_t = off;     off = align_up(off + 2 * (size_t)r.B * r.H * 8);
+  w.bc_t = off;     off = align_up(off + (size_t)kXRep * kBcStride * 4);
+  // item-organised layer: LoRA partials of in_proj / out_proj, packed g of every item
+  w.lp_a = off;     off = align_up(off + (size_t)kXRep * kLpStride * 8);
+  w.lp_c = off;     off = align_up(off + (size_t)kXRep * kLpStride * 8);
+  w.g_p = off;      off = align_up(off + (size_t)kXRep * kGStride * 8);
+  // its own per-workgroup launch counts (its grid differs from the phase-organised layer's)
+  w.launches1 = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
+  w.bc_t1 = off;    off = align_up(off + (size_t)kXRep * kBcStride * 4);  // its B | C words
   w.total = off;
   return w;
 }
@@ -93,6 +101,16 @@ PfLayout pf_layout(const Derived& r, int rows) {
 }
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e; }
+
+// Which layer kernel dfssm_layer_step uses (dfssm_set_layer_kernel).
+int g_layer_kernel = DFSSM_LAYER_AUTO;
+constexpr bool kAutoItem = false;  // what DFSSM_LAYER_AUTO picks: the item-organised layer or not
+
+// Whether the current setting runs the item-organised one-launch layer for these dimensions.
+bool use_item_layer(int B, int D, int DI, int H, int P) {
+  const bool want = g_layer_kernel == DFSSM_LAYER_ITEM || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoItem);
+  return want && item_layer_grid(B, D, DI, H, P) > 0;
+}
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 bool kdim_ok(int k) { return k > 0 && k % 512 == 0 && k <= 5120; }
@@ -139,7 +157,18 @@ int dfssm_check_dims(const dfssm_dims* d) {
 int dfssm_one_launch_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
   if (!d || dfssm_check_dims(d) != DFSSM_OK) return 0;
   const Derived r = derive(d);
+  const int item = item_plan(cus, blocks_per_cu, r.B, r.D, r.DI, r.H, r.P);
+  if (item > 0) return item;
   return fused_plan(cus, blocks_per_cu, blocks_per_cu, r.B, r.IPO, r.D, r.DI, r.H, r.P, nullptr);
+}
+
+int dfssm_set_layer_kernel(int which) {
+  if (which != DFSSM_LAYER_AUTO && which != DFSSM_LAYER_FUSED && which != DFSSM_LAYER_FIVE &&
+      which != DFSSM_LAYER_ITEM)
+    return DFSSM_E_RANGE;
+  const int prev = g_layer_kernel;
+  g_layer_kernel = which;
+  return prev;
 }
 
 size_t dfssm_tiled_bits_bytes(int rows, int k) {
@@ -345,10 +374,19 @@ static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const d
   a.projT = (uint32_t*)(ws + w.proj_t);
   a.gT = (uint32_t*)(ws + w.g_t);
   a.hT = (uint32_t*)(ws + w.h_t);
+  a.bcT = (uint32_t*)(ws + w.bc_t);
+  a.lpA = (uint64_t*)(ws + w.lp_a);
+  a.lpC = (uint64_t*)(ws + w.lp_c);
+  a.gP = (uint64_t*)(ws + w.g_p);
   a.dtT = (uint64_t*)(ws + w.dt_t);
   a.launches = (uint32_t*)(ws + w.launches);
   a.err = (int*)(ws + w.err);
   a.D = r.D; a.DI = r.DI; a.N = r.N; a.H = r.H; a.P = r.P; a.IPO = r.IPO; a.C = r.C;
+  if (use_item_layer(r.B, r.D, r.DI, r.H, r.P)) {
+    a.launches = (uint32_t*)(ws + w.launches1);
+    a.bcT = (uint32_t*)(ws + w.bc_t1);
+    return hip_status(launch_item_layer(a, r.B, as_stream(stream)));
+  }
   return hip_status(launch_fused_layer(a, r.B, as_stream(stream)));
 }
 
@@ -447,8 +485,10 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
   int rc = check_layer_args(model, layer, x, state, workspace);
   if (rc) return rc;
   const Derived r = derive(&model->dims);
-  if (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P))
-    return fused_layer(model, layer, x, state, workspace, stream);
+  const bool one_launch = g_layer_kernel != DFSSM_LAYER_FIVE &&
+                          (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P) ||
+                           use_item_layer(r.B, r.D, r.DI, r.H, r.P));
+  if (one_launch) return fused_layer(model, layer, x, state, workspace, stream);
   for (int phase = 0; phase < DFSSM_LAYER_PHASES; ++phase) {
     const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
     if (rc) return rc;

@@ -214,15 +214,35 @@ struct FusedArgs {
   // epoch mod 2^16
   uint32_t* projT;           // (M, IPO): gate z sigma(z) | conv'd xBC (dt rows unused)
   uint32_t* gT;              // (M, DI): gated SSM output
-  uint32_t* hT;              // (2, M, 16): LoRA intermediates of in_proj / out_proj
+  uint32_t* hT;              // kXRep copies (stride kHStride words) of (2, M, 16): LoRA intermediates of
+                             // in_proj / out_proj; consumer workgroup w polls copy w % kXRep
+  uint32_t* bcT;             // kXRep copies (stride kBcStride words) of (M, 2 d_state): conv'd B | C
   uint64_t* dtT;             // (M, H, 2): softplus dt and exp(dt A) per head, (tag << 32) | fp32 bits
   uint32_t* launches;        // (G) launch count of each workgroup
   int* err;                  // error flags (bit 2: a wait timed out)
+  // item-organised layer (layer1.hip) only:
+  uint64_t* lpA;             // kXRep copies (stride kLpStride) of (M, G) LoRA partials of in_proj, two words each
+  uint64_t* lpC;             // kXRep copies (stride kLpStride) of (M, 16 SC) LoRA partials of out_proj
+  uint64_t* gP;              // kXRep copies (stride kGStride) of (M, items, 6): gated SSM output,
+                             // three fp16 values and the tag per word
   int D, DI, N, H, P, IPO, C;
 };
+// Words that many workgroups poll (the LoRA intermediates, B | C) are written in kXRep copies at
+// different addresses, so that their polls spread over memory channels instead of queueing on one
+// cache line.
+constexpr int kXRep = 8;
+constexpr int kHStride = 1024;   // words between copies of hT (>= 2 * 4 * 16)
+constexpr int kBcStride = 1088;  // words between copies of bcT (>= 4 * 256)
 constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
 constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
 
+// The item-organised one-launch layer (layer1.hip): grid = one workgroup per SSM item (head,
+// 16-row block), all co-resident; 0 = not usable on this device / shape.
+constexpr int kLpStride = 4 * 256 * 2 + 64;  // words between copies of lpA / lpC
+constexpr int kGStride = 4 * 256 * 6 + 64;   // words between copies of gP
+int item_layer_grid(int M, int D, int DI, int H, int P);
+hipError_t launch_item_layer(const FusedArgs& a, int M, hipStream_t s);
+int item_plan(int cus, int per_cu, int M, int D, int DI, int H, int P);
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);
 // Grid of the one-launch layer on a device with `cus` CUs where per_cu32 / per_cu64 workgroups of
 // the 32- / 64-row-group instantiations fit per CU; 0 = use the five-kernel form. *rc_out = RC.

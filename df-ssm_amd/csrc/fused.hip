@@ -344,13 +344,14 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
 #pragma unroll
     for (int w = 1; w < kFW; ++w) amax = fmaxf(amax, L.rf[m][w]);
     const float xs = quant_scale(amax);
+    const float rinv = quant_rcp(xs);
     if (tid == 0) L.xs[m] = xs;
     int qsum = 0;
     for (int c = CW * wave; c < CH; c += (c % CW == CW - 1) ? CW * (kFW - 1) + 1 : 1) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int k0 = 128 * c + 64 * hh;
-        const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
+        const int q = quant_i8(h2f(L.xn[k0 + lane]), rinv);
         qsum += q;
         planes_store64(&L.planes[m][k0 / 32][0], q, lane);
       }
@@ -386,11 +387,11 @@ __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT,
     __syncthreads();  // the sum-of-squares partials of this row have been read by every wave
     if (lane == 0) L.rd[m][wave] = hw;
     __syncthreads();
-    if (tid == 0) {
+    if (tid < kXRep) {  // one copy per thread
       double t = 0.0;
 #pragma unroll
       for (int w = 0; w < kFW; ++w) t += L.rd[m][w];
-      st_dev(hout + m * DFSSM_LORA_R + r, tagged(tag, f2h((float)t)));
+      st_dev(hout + tid * kHStride + m * DFSSM_LORA_R + r, tagged(tag, f2h((float)t)));
     }
   });
 }
@@ -530,7 +531,8 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
       const float sg = r16(1.0f / (1.0f + dev_expf(-out)));
       out = r16(out * sg);
     } else if (ch < a.C) {
-      // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later)
+      // depthwise conv (k = 4) + SiLU; the (M, C, 3) fp16 state shifts left (stored later); the B
+      // and C channels go to the polled copies (bcT), the x channels to projT
       const uint16_t xo = f2h(out);
       cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, (uint16_t)(er.cs01 >> 16), (uint16_t)er.cs2, xo};
       const float xv = h2f(xo);
@@ -549,7 +551,14 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
       st_dev(w + 1, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, abar));
       return cp;
     }
-    st_dev(a.projT + (size_t)m * a.IPO + n, tagged(tag, f2h(out)));
+    const uint32_t word = tagged(tag, f2h(out));
+    const int bc = ch - a.DI;  // B | C channel index, or < 0
+    if (bc >= 0) {
+#pragma unroll
+      for (int c = 0; c < kXRep; ++c) st_dev(a.bcT + c * kBcStride + m * 2 * a.N + bc, word);
+    } else {
+      st_dev(a.projT + (size_t)m * a.IPO + n, word);
+    }
   } else {
     a.x[(size_t)m * a.D + n] = f2h(h2f((uint16_t)er.xres) + out);
   }
@@ -590,7 +599,7 @@ __device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item&
   bool ok = true;
   if (wave == 2 * k) {
     uint32_t w[2];
-    pollv<2>(pr + 2 * a.DI + 4 * lane, tag, w, ok, a.err);
+    pollv<2>(a.bcT + (bix() % kXRep) * kBcStride + t.m * 2 * a.N + 4 * lane, tag, w, ok, a.err);
     L.item[k].bc[2 * lane] = w[0];
     L.item[k].bc[2 * lane + 1] = w[1];
   } else if (wave == 2 * k + 1) {
@@ -666,8 +675,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   };
   const int gA = (a.IPO + 63) / 64, gC = a.D / RC;
   const int NI = a.H * (a.P / 16), items = M * NI;
-  uint32_t* hA = a.hT;
+  uint32_t* hA = a.hT;                       // copy 0 (the LoRA workgroups write every copy)
   uint32_t* hC = a.hT + M * DFSSM_LORA_R;
+  const uint32_t* hA_mine = hA + (wg % kXRep) * kHStride;  // the copy this workgroup polls
+  const uint32_t* hC_mine = hC + (wg % kXRep) * kHStride;
 
   // ---- loads that do not depend on the activations ----
   u32x4 wa[kFMaxCPW];
@@ -691,11 +702,11 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
         load_bits(wa, a.in_bits, grp, a.D);
         ea = load_epi<M, true>(a, grp);
       }
-      const uint32_t hv = lora_issue(hA, M);
+      const uint32_t hv = lora_issue(hA_mine, M);
       gemv_partials<M>(L, wa, a.D);
       TL(2);
       const uint32_t tag = tag_now();
-      lora_finish<M>(L, hA, hv, tag, a.err);
+      lora_finish<M>(L, hA_mine, hv, tag, a.err);
       __syncthreads();
       TL(3);
       store_conv(epilogue<M, true>(L, a, ea, grp, tag));
@@ -753,11 +764,11 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
         else load_bits(wc, a.out_bits, grp, a.DI);
         ec = load_epi<M, false, RC>(a, grp);
       }
-      const uint32_t hv = lora_issue(hC, M);
+      const uint32_t hv = lora_issue(hC_mine, M);
       if constexpr (RC < 64) gemv_partials_rg<M, RC>(L, wcr, a.DI);
       else gemv_partials<M>(L, wc, a.DI);
       TL(10);
-      lora_finish<M>(L, hC, hv, tag, a.err);
+      lora_finish<M>(L, hC_mine, hv, tag, a.err);
       __syncthreads();
       TL(11);
       (void)epilogue<M, false, RC>(L, a, ec, grp, tag);

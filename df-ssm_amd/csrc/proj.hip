@@ -121,6 +121,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
     amax = fmaxf(amax, L.red_f[i]);
   }
   const float xs = quant_scale(amax);
+  const float rinv = quant_rcp(xs);
   // q over all columns when sum q is wanted, else only where written: the bytes and bit planes
   // of the 64-column wave blocks that start in slice rr (slices narrower than 64 columns, K < 1024,
   // leave every other workgroup nothing to write). Global stores come last: a wave with a store
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
   for (int k0 = 64 * w; k0 < K; k0 += NT) {
     const bool mine = k0 >= lo && k0 < hi;  // wave-uniform
     if (!want_sum && !mine) continue;
-    const int q = quant_i8(h2f(L.xn[k0 + lane]), xs);
+    const int q = quant_i8(h2f(L.xn[k0 + lane]), rinv);
     qsum += q;
     if (mine) {
       if (a.q_out) a.q_out[(size_t)m * a.ld_q + k0 + lane] = (int8_t)q;

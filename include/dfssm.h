@@ -89,6 +89,20 @@ int dfssm_check_dims(const dfssm_dims* dims);
  * kernel launches, df_ssm_inference.py:161-207). */
 int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
 
+/* Layer kernel selection for dfssm_layer_step / dfssm_decode_step (process-wide; returns the
+ * previous setting, or DFSSM_E_RANGE). At batch <= 4: DFSSM_LAYER_FUSED runs the
+ * phase-organised one-launch layer where the shape allows it, else five kernels;
+ * DFSSM_LAYER_ITEM runs the item-organised one-launch layer (one workgroup per SSM item, grid a
+ * power of two <= 256) where the shape allows it, else as DFSSM_LAYER_FUSED;
+ * DFSSM_LAYER_FIVE always runs five kernels; DFSSM_LAYER_AUTO (default) is the faster of the
+ * two one-launch layers on the benchmark shape (currently DFSSM_LAYER_FUSED). All give
+ * bit-identical results; the setting exists to compare them. No counterpart in the reference. */
+#define DFSSM_LAYER_AUTO 0
+#define DFSSM_LAYER_FUSED 1
+#define DFSSM_LAYER_FIVE 2
+#define DFSSM_LAYER_ITEM 3
+int dfssm_set_layer_kernel(int which);
+
 /* ---- load-time layout ------------------------------------------------------------------ */
 /* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, row_bytes) table
  * (row_bytes = d_model for int8, 2 * d_model for fp16). */

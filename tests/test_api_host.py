@@ -24,7 +24,7 @@ def _dims(**kw):
     ({"batch": 4}, 256, 1, 256),
     ({"batch": 5}, 256, 1, 0),         # batch >= 5 always runs five kernels
     ({}, 140, 1, 0),                   # 133 in_proj groups + 16 LoRA workgroups do not fit
-    ({}, 2048, 1, 1024),               # grid capped at 1024 workgroups
+    ({}, 2048, 1, 256),                # item-organised layer: one workgroup per SSM item
     ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 256, 1, 256),
     ({"batch": 65}, 256, 1, 0),
 ])

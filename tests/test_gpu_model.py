@@ -110,19 +110,26 @@ def test_1p3b_greedy(w13, B, T, n):
     assert gpu.error_flag() == 0
 
 
+@pytest.mark.parametrize("kernel", [3, 1])   # DFSSM_LAYER_ITEM, DFSSM_LAYER_FUSED
 @pytest.mark.parametrize("B", [1, 3])
-def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
-    """dfssm_layer_step (one launch at batch <= 4) against dfssm_layer_phase 0..4 (the five-kernel
-    form) on the same inputs: x, SSM state and conv state identical bit for bit."""
+def test_one_launch_layer_equals_five_kernels(tiny_weights, B, kernel):
+    """dfssm_layer_step (one launch at batch <= 4: the item-organised layer, or the
+    phase-organised one) against dfssm_layer_phase 0..4 (the five-kernel form) on the same
+    inputs: x, SSM state and conv state identical bit for bit."""
     from dfssm import _C
     w = tiny_weights
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
     gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, 5)))  # non-trivial state
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
-    for li in range(w.cfg.n_layer):
-        _C.check(lib.dfssm_layer_step(gpu._model, li, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
-                                      _C.stream()))
+    prev = lib.dfssm_set_layer_kernel(kernel)
+    try:
+        for li in range(w.cfg.n_layer):
+            _C.check(lib.dfssm_layer_step(gpu._model, li, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
+                                          _C.stream()))
+        torch.cuda.synchronize()
+    finally:
+        lib.dfssm_set_layer_kernel(prev)
     x1, h1, c1 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
     gpu.x.copy_(x0); gpu.h_state.copy_(h0); gpu.conv_state.copy_(c0)
     for li in range(w.cfg.n_layer):
@@ -136,8 +143,9 @@ def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
     assert gpu.error_flag() == 0
 
 
+@pytest.mark.parametrize("kernel", [3, 1])
 @pytest.mark.parametrize("B", [1, 4])
-def test_one_launch_layer_wide_model(B):
+def test_one_launch_layer_wide_model(B, kernel):
     """d_model 4096 (128 out_proj groups of 32 rows, the widest grid use): the one-launch layer
     against the five-kernel form, bit for bit."""
     from dfssm import _C
@@ -150,7 +158,13 @@ def test_one_launch_layer_wide_model(B):
     gpu.ingest(torch.from_numpy(make_prompts(B, c.vocab_size, 3)))
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
-    _C.check(lib.dfssm_layer_step(gpu._model, 0, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(), _C.stream()))
+    prev = lib.dfssm_set_layer_kernel(kernel)
+    try:
+        _C.check(lib.dfssm_layer_step(gpu._model, 0, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
+                                      _C.stream()))
+        torch.cuda.synchronize()
+    finally:
+        lib.dfssm_set_layer_kernel(prev)
     x1, h1, c1 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
     gpu.x.copy_(x0); gpu.h_state.copy_(h0); gpu.conv_state.copy_(c0)
     for ph in range(5):
