@@ -34,7 +34,7 @@ Derived derive(const dfssm_dims* d) {
 
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
-      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, total;
+      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -74,6 +74,9 @@ WsLayout ws_layout(const dfssm_dims* d) {
   // its own per-workgroup launch counts (its grid differs from the phase-organised layer's)
   w.launches1 = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
   w.bc_t1 = off;    off = align_up(off + (size_t)kXRep * kBcStride * 4);  // its B | C words
+  // multi-layer launch of the phase-organised layer: x handed from layer to layer
+  w.x_t = off;      off = align_up(off + (size_t)2 * kXRep * kXStride * 4);
+  w.ltab = off;     off = align_up(off + (size_t)r.L * sizeof(FusedArgs));  // its per-layer arguments
   w.total = off;
   return w;
 }
@@ -104,7 +107,11 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e
 
 // Which layer kernel dfssm_layer_step uses (dfssm_set_layer_kernel).
 int g_layer_kernel = DFSSM_LAYER_AUTO;
-constexpr bool kAutoItem = false;  // what DFSSM_LAYER_AUTO picks: the item-organised layer or not
+// What DFSSM_LAYER_AUTO picks at batch <= 4: the phase-organised layer, one launch per layer
+// (measured at 1.3B, batch 1: 845 us per step; all layers in one launch 850 us; the
+// item-organised layer 917 us).
+constexpr bool kAutoItem = false;
+constexpr bool kAutoMulti = false;
 
 // Whether the current setting runs the item-organised one-launch layer for these dimensions.
 bool use_item_layer(int B, int D, int DI, int H, int P) {
@@ -164,7 +171,7 @@ int dfssm_one_launch_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
 
 int dfssm_set_layer_kernel(int which) {
   if (which != DFSSM_LAYER_AUTO && which != DFSSM_LAYER_FUSED && which != DFSSM_LAYER_FIVE &&
-      which != DFSSM_LAYER_ITEM)
+      which != DFSSM_LAYER_ITEM && which != DFSSM_LAYER_MULTI)
     return DFSSM_E_RANGE;
   const int prev = g_layer_kernel;
   g_layer_kernel = which;
@@ -354,8 +361,8 @@ static int check_layer_args(const dfssm_model* model, int layer, uint16_t* x, co
 }
 
 // The whole layer in one launch (batch <= 4).
-static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
-                       void* workspace, void* stream) {
+static FusedArgs fused_args(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                            void* workspace) {
   const Derived r = derive(&model->dims);
   const dfssm_layer& Lw = model->layers[layer];
   const WsLayout w = ws_layout(&model->dims);
@@ -379,15 +386,89 @@ static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const d
   a.lpC = (uint64_t*)(ws + w.lp_c);
   a.gP = (uint64_t*)(ws + w.g_p);
   a.dtT = (uint64_t*)(ws + w.dt_t);
+  a.xT = (uint32_t*)(ws + w.x_t);
   a.launches = (uint32_t*)(ws + w.launches);
   a.err = (int*)(ws + w.err);
+  a.layer = layer;
+  a.n_layer = r.L;
   a.D = r.D; a.DI = r.DI; a.N = r.N; a.H = r.H; a.P = r.P; a.IPO = r.IPO; a.C = r.C;
+  return a;
+}
+
+// The whole layer in one launch (batch <= 4).
+static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                       void* workspace, void* stream) {
+  const Derived r = derive(&model->dims);
+  FusedArgs a = fused_args(model, layer, x, state, workspace);
   if (use_item_layer(r.B, r.D, r.DI, r.H, r.P)) {
-    a.launches = (uint32_t*)(ws + w.launches1);
-    a.bcT = (uint32_t*)(ws + w.bc_t1);
+    const WsLayout w = ws_layout(&model->dims);
+    a.launches = (uint32_t*)((char*)workspace + w.launches1);
+    a.bcT = (uint32_t*)((char*)workspace + w.bc_t1);
     return hip_status(launch_item_layer(a, r.B, as_stream(stream)));
   }
   return hip_status(launch_fused_layer(a, r.B, as_stream(stream)));
+}
+
+// Strides between the layers of every per-layer pointer the phase-organised layer reads, when
+// each field's layers are equally spaced (one allocation per field, as the Python loader
+// makes them); false otherwise.
+static bool layer_strides(const dfssm_model* model, FusedStrides& st) {
+  const Derived r = derive(&model->dims);
+  const dfssm_layer* L = model->layers;
+  bool ok = true;
+  auto one = [&](auto get) {
+    const long long s = r.L > 1 ? (long long)((const char*)get(L[1]) - (const char*)get(L[0])) : 0;
+    for (int l = 2; l < r.L && ok; ++l)
+      if ((const char*)get(L[l]) - (const char*)get(L[0]) != s * l) ok = false;
+    return s;
+  };
+  st.in_bits = one([](const dfssm_layer& x) { return (const void*)x.in_bits; });
+  st.in_ws = one([](const dfssm_layer& x) { return (const void*)x.in_scale; });
+  st.in_lA = one([](const dfssm_layer& x) { return (const void*)x.in_lA; });
+  st.in_lAs = one([](const dfssm_layer& x) { return (const void*)x.in_lA_s; });
+  st.in_lBq = one([](const dfssm_layer& x) { return (const void*)x.in_lBq; });
+  st.out_bits = one([](const dfssm_layer& x) { return (const void*)x.out_bits; });
+  st.out_ws = one([](const dfssm_layer& x) { return (const void*)x.out_scale; });
+  st.out_lA = one([](const dfssm_layer& x) { return (const void*)x.out_lA; });
+  st.out_lAs = one([](const dfssm_layer& x) { return (const void*)x.out_lA_s; });
+  st.out_lBq = one([](const dfssm_layer& x) { return (const void*)x.out_lBq; });
+  st.conv_w = one([](const dfssm_layer& x) { return (const void*)x.conv_w; });
+  st.conv_b = one([](const dfssm_layer& x) { return (const void*)x.conv_b; });
+  st.A_log = one([](const dfssm_layer& x) { return (const void*)x.A_log; });
+  st.Dp = one([](const dfssm_layer& x) { return (const void*)x.D; });
+  st.dt_bias = one([](const dfssm_layer& x) { return (const void*)x.dt_bias; });
+  st.norm_w = one([](const dfssm_layer& x) { return (const void*)x.norm_w; });
+  st.ln_w = one([](const dfssm_layer& x) { return (const void*)x.ln_w; });
+  st.h = (long long)r.B * r.H * r.P * r.N * (long long)sizeof(float);
+  st.conv = (long long)r.B * r.C * 3 * (long long)sizeof(uint16_t);
+  return ok;
+}
+
+// Whether dfssm_decode_step runs every layer in one launch (strides of the per-layer pointers
+// in st when it does).
+static bool all_layers_one_launch(const dfssm_model* model, FusedStrides& st) {
+  const Derived r = derive(&model->dims);
+  const bool want = g_layer_kernel == DFSSM_LAYER_MULTI || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoMulti);
+  return want && r.L <= kMaxLayers && fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P, true) &&
+         layer_strides(model, st);
+}
+
+// Every layer of a decode step in one launch of the phase-organised layer, when the setting,
+// the shape and the weight layout allow it; returns DFSSM_E_DIMS (nothing launched) otherwise.
+static int fused_all_layers(const dfssm_model* model, uint16_t* x, const dfssm_state* state, void* workspace,
+                            void* stream) {
+  const Derived r = derive(&model->dims);
+  FusedStrides st{};
+  if (!all_layers_one_launch(model, st)) return DFSSM_E_DIMS;
+  const FusedArgs a = fused_args(model, 0, x, state, workspace);
+  FusedArgs* tab = (FusedArgs*)((char*)workspace + ws_layout(&model->dims).ltab);
+  return hip_status(launch_fused_layers(a, st, tab, r.B, as_stream(stream)));
+}
+
+int dfssm_decode_one_launch(const dfssm_model* model) {
+  if (check_model(model)) return 0;
+  FusedStrides st{};
+  return all_layers_one_launch(model, st) ? 1 : 0;
 }
 
 int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
@@ -540,9 +621,14 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
     rc = dfssm_embed(model, tokens, x, workspace, stream);
     if (rc) return rc;
   }
-  for (int l = 0; l < model->dims.n_layer; ++l) {
-    rc = dfssm_layer_step(model, l, x, state, workspace, stream);
-    if (rc) return rc;
+  rc = fused_all_layers(model, x, state, workspace, stream);
+  if (rc == DFSSM_E_DIMS) {
+    for (int l = 0; l < model->dims.n_layer; ++l) {
+      rc = dfssm_layer_step(model, l, x, state, workspace, stream);
+      if (rc) return rc;
+    }
+  } else if (rc) {
+    return rc;
   }
   return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
 }

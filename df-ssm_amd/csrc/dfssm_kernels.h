@@ -225,8 +225,22 @@ struct FusedArgs {
   uint64_t* lpC;             // kXRep copies (stride kLpStride) of (M, 16 SC) LoRA partials of out_proj
   uint64_t* gP;              // kXRep copies (stride kGStride) of (M, items, 6): gated SSM output,
                              // three fp16 values and the tag per word
+  // phase-organised layer: the launch's layers and their tags. Every launch takes the tags
+  // epoch * n_layer + layer + 1 (mod 2^16) of its own layers, so that no word left by another
+  // launch or layer carries a tag a poll waits for.
+  int layer, n_layer;
+  uint32_t* xT;              // multi-layer launch: 2 x kXRep copies (stride kXStride words) of (M, D)
+                             // tagged x words, layer l's output in buffer l % 2
   int D, DI, N, H, P, IPO, C;
 };
+
+// Byte distance between consecutive layers of every per-layer pointer of FusedArgs: the
+// multi-layer launch runs layer l on the pointers of layer 0 advanced by l strides.
+struct FusedStrides {
+  long long in_bits, in_ws, in_lA, in_lAs, in_lBq, out_bits, out_ws, out_lA, out_lAs, out_lBq, conv_w, conv_b,
+      A_log, Dp, dt_bias, norm_w, ln_w, h, conv;
+};
+constexpr int kXStride = 4 * 5120 + 64;  // words between copies of xT (>= 4 * d_model)
 // Words that many workgroups poll (the LoRA intermediates, B | C) are written in kXRep copies at
 // different addresses, so that their polls spread over memory channels instead of queueing on one
 // cache line.
@@ -243,11 +257,16 @@ constexpr int kGStride = 4 * 256 * 6 + 64;   // words between copies of gP
 int item_layer_grid(int M, int D, int DI, int H, int P);
 hipError_t launch_item_layer(const FusedArgs& a, int M, hipStream_t s);
 int item_plan(int cus, int per_cu, int M, int D, int DI, int H, int P);
-bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);
+bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P, bool multi = false);
 // Grid of the one-launch layer on a device with `cus` CUs where per_cu32 / per_cu64 workgroups of
 // the 32- / 64-row-group instantiations fit per CU; 0 = use the five-kernel form. *rc_out = RC.
 int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int DI, int H, int P, int* rc_out);
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s);
+// Layers a.layer .. a.n_layer - 1 in one launch (the phase-organised layer looped over layers,
+// x handed from each layer's phase C to the next layer's phase A as tagged words).
+// tab: device memory for n_layer FusedArgs (filled by the launch's first kernel).
+constexpr int kMaxLayers = 256;
+hipError_t launch_fused_layers(const FusedArgs& a, const FusedStrides& st, FusedArgs* tab, int M, hipStream_t s);
 hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, hipStream_t s);
 
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);

@@ -8,7 +8,9 @@
 //      x, L2-resident), the packed-bit GEMV, dequantization, LoRA, and per row type: the gate
 //      z sigma(z) (z rows), conv + SiLU (x, B, C rows), softplus dt and exp(dt A) (dt rows).
 //      Workgroups gA..gA+15 compute the 16 LoRA intermediates (one rank each); the GEMV
-//      workgroups pick them up just before their epilogue.
+//      workgroups pick them up just before their epilogue. (Slice partials published by the
+//      GEMV workgroups themselves, as the item-organised layer does, measured slower here: the
+//      GEMV workgroups reach their RMSNorm ~2 us after the LoRA workgroups would.)
 //   B  SSM + gate: item (sequence, head, 16-row block); two waves per item poll the words the
 //      item needs (gate, x, B, C, dt) into LDS, then every wave updates one fp32 state row and
 //      writes its g.
@@ -20,6 +22,10 @@
 // the quantizer's bit planes are built once per 64 values with 8 ballots, stored whole.
 // The weights and the state do not depend on the activations, so each workgroup issues those
 // loads first.
+//
+// Workgroup barriers order LDS only (lds_barrier): waves of a workgroup never hand each other
+// data through global memory, and a full barrier would first wait for every global store of the
+// wave to be acknowledged.
 //
 // Data passed between workgroups of one launch travels as 32-bit words (tag << 16) | fp16 value,
 // stored and loaded with device-scope (agent) coherent accesses, which do not hit stale lines of
@@ -51,6 +57,14 @@ constexpr int kCR = (2 * (kFMaxK / 128) + kFT / RG - 1) / (kFT / RG);
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kSpinMax = 1u << 18;
 constexpr int kMaxItems = kFW / 2;  // SSM items per workgroup (two polling waves each)
+// at batch M: at most 2 M items per workgroup (the plan checks it), so that the per-item
+// registers held through phase B's polls scale with the batch
+template <int M>
+constexpr int kItemsOf = 2 * M < kMaxItems ? 2 * M : kMaxItems;
+// Multi-layer launch: whether a workgroup issues its loads of the next layer's weights before it
+// waits for that layer's input (true), or only after (false: measured the same per step at batch
+// 1, with less memory traffic while the previous layer's phase C runs).
+constexpr bool kPrefetchNextLayer = false;
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -293,7 +307,7 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
     }
     const double wsum = wave_sum_dpp_f64(part);
     if (lane == 0) L.rd[m][wave] = wsum;
-    __syncthreads();  // also: every wave is done with the previous row's xn
+    lds_barrier();  // also: every wave is done with the previous row's xn
     double ss = 0.0;
 #pragma unroll
     for (int w = 0; w < kFW; ++w) ss += L.rd[m][w];
@@ -339,7 +353,7 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
   norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float mx) {
     const float wmax = wave_max_dpp_f32(mx);
     if (lane == 0) L.rf[m][wave] = wmax;
-    __syncthreads();  // publishes xn and the partial maxima
+    lds_barrier();  // publishes xn and the partial maxima
     float amax = L.rf[m][0];
 #pragma unroll
     for (int w = 1; w < kFW; ++w) amax = fmaxf(amax, L.rf[m][w]);
@@ -363,16 +377,17 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
 
 // LoRA intermediate of rank r for every row (LoRA workgroups): h[m][r] =
 // fp16(sum_k xn_k * Bq[r][k]), fp16 x fp16 products exact in fp32, summed in fp64, stored as a
-// tagged word hout[m * 16 + r].
+// tagged word hout[m * 16 + r] with `tag`. OUT (or a polled x): the activations are polled from
+// gT until they carry `ptag`.
 template <int M, bool OUT>
 __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT, int K, const float* norm_w,
-                          const uint16_t* lBq, int r, uint32_t* hout, uint32_t tag, int* err) {
+                          const uint16_t* lBq, int r, uint32_t* hout, uint32_t tag, int* err, uint32_t ptag) {
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const bool has_v = tid < K / 8;
   PIn<M> pi;
   load_pin<M, OUT>(pi, x, K, norm_w);
   const u32x4 b8 = has_v ? *(const u32x4*)(lBq + (size_t)r * K + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
-  norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float) {
+  norm_rows<M, OUT>(L, pi, gT, K, ptag, err, [&](int m, float) {
     double hacc = 0.0;
     if (has_v) {
       const u32x4 xv8 = *(const u32x4*)&L.xn[8 * tid];  // this thread's own columns
@@ -384,9 +399,9 @@ __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT,
       }
     }
     const double hw = wave_sum_dpp_f64(hacc);
-    __syncthreads();  // the sum-of-squares partials of this row have been read by every wave
+    lds_barrier();  // the sum-of-squares partials of this row have been read by every wave
     if (lane == 0) L.rd[m][wave] = hw;
-    __syncthreads();
+    lds_barrier();
     if (tid < kXRep) {  // one copy per thread
       double t = 0.0;
 #pragma unroll
@@ -502,9 +517,11 @@ __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc
 // row: acc = sum over waves s of (2 T_s - sum q_s) and the LoRA term sum_r h_r aq_r as DPP row
 // sums (exact: integers, and exactly representable products in fp64); thread s = m then
 // finalizes sequence m. IN: z rows store the gate z sigma(z), x/B/C rows conv + SiLU, dt rows
-// softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x.
+// softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x (also kept in
+// *xkeep and, for a next layer of the same launch, published to every copy at xpub).
 template <int M, bool IN, int RG = 64>
-__device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag) {
+__device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag,
+                             uint32_t* xpub = nullptr, uint32_t* xkeep = nullptr) {
   ConvPend cp{nullptr, 0, 0, 0};
   const int tid = tix(), s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
@@ -560,7 +577,13 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
       st_dev(a.projT + (size_t)m * a.IPO + n, word);
     }
   } else {
-    a.x[(size_t)m * a.D + n] = f2h(h2f((uint16_t)er.xres) + out);
+    const uint16_t xv = f2h(h2f((uint16_t)er.xres) + out);
+    a.x[(size_t)m * a.D + n] = xv;
+    if (xkeep) *xkeep = xv;
+    if (xpub) {  // the next layer's input, to every copy
+#pragma unroll
+      for (int c = 0; c < kXRep; ++c) st_dev(xpub + (size_t)c * kXStride + (size_t)m * a.D + n, tagged(tag, xv));
+    }
   }
   return cp;
 }
@@ -652,27 +675,100 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
   }
 }
 
-// RC: rows per out_proj group (32, or 64 when D / 32 + 16 groups do not fit the grid).
+// Multi-layer launch, start of layer l > first: wave 0 waits until the first x word of every
+// out_proj group (row RC g of every sequence) of the previous layer carries `tag`, polling one
+// word per group (the whole of x is polled afterwards, by the threads that use it). This keeps the
+// workgroups that are done early from flooding memory with polls of all of x (or of their SSM
+// items' words) while the previous layer's phase C runs. The caller passes a barrier next.
 template <int M, int RC>
-__global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
+__device__ __forceinline__ void wait_prev_layer(const uint32_t* xsrc, int D, uint32_t tag, int* err) {
+  if (tix() >= 64) return;
+  const int lane = tix(), gC = D / RC;
+  constexpr int kW = (M * (kFMaxK / 32) + 63) / 64;  // words per lane
+  for (int j = 0; j < kW; ++j) {
+    const int idx = lane + 64 * j;
+    if (idx >= M * gC) break;
+    const uint32_t* p = xsrc + (size_t)(idx / gC) * D + (size_t)(idx % gC) * RC;
+    uint32_t v = ld_dev(p);
+    for (uint32_t it = 0; (v >> 16) != tag; ++it) {
+      if (it == kSpinMax) {
+        atomicOr(err, 4);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+      v = ld_dev(p);
+    }
+  }
+}
+
+// Layer l of a multi-layer launch: every per-layer pointer advanced by l strides.
+__device__ __forceinline__ FusedArgs at_layer(const FusedArgs& a, const FusedStrides& st, int l) {
+  FusedArgs b = a;
+  const long long k = l;
+#define DFSSM_ADV(f) b.f = (decltype(b.f))((const char*)a.f + st.f * k)
+  DFSSM_ADV(in_bits); DFSSM_ADV(in_ws); DFSSM_ADV(in_lA); DFSSM_ADV(in_lAs); DFSSM_ADV(in_lBq);
+  DFSSM_ADV(out_bits); DFSSM_ADV(out_ws); DFSSM_ADV(out_lA); DFSSM_ADV(out_lAs); DFSSM_ADV(out_lBq);
+  DFSSM_ADV(conv_w); DFSSM_ADV(conv_b); DFSSM_ADV(A_log); DFSSM_ADV(Dp); DFSSM_ADV(dt_bias);
+  DFSSM_ADV(norm_w); DFSSM_ADV(ln_w); DFSSM_ADV(h); DFSSM_ADV(conv);
+#undef DFSSM_ADV
+  b.layer = l;
+  return b;
+}
+
+// The arguments of every layer of a multi-layer launch, written to device memory (thread l:
+// layer l) so that the launch loads each layer's from there instead of keeping the strides and
+// the base pointers live in registers through all layers.
+__global__ void layer_table_kernel(FusedArgs a0, FusedStrides st, FusedArgs* tab) {
+  const int l = blockIdx.x * blockDim.x + threadIdx.x;
+  if (l < a0.n_layer) tab[l] = at_layer(a0, st, l);
+}
+
+// RC: rows per out_proj group (32, or 64 when D / 32 + 16 groups do not fit the grid).
+// MULTI: layers a0.layer .. a0.n_layer - 1 in one launch. A workgroup goes on to the next layer
+// as soon as its own part of a layer is done (its weight and state loads for that layer then
+// overlap the end of the previous one); phase A of layer l > a0.layer polls x from the tagged
+// words that phase C of layer l - 1 publishes (buffer (l - 1) % 2 of xT). Every word a layer
+// writes for other workgroups is read by them before the writes of the next layer can start:
+// those all wait for the next layer's x, which phase C publishes only after every SSM item of
+// the layer is done, and every workgroup that reads x or LoRA words in phase A owns an item.
+// The out_proj group of a workgroup (at most one, as the plan requires) keeps its x rows in
+// registers from one layer to the next instead of reading them back.
+template <int M, int RC, bool MULTI>
+__global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const FusedArgs* __restrict__ tab) {
   __shared__ FusedLds<M> L;
   TL_DECL;
-#ifdef DFSSM_TIMELINE
-  if (tix() < kTlStamps) tl_s[tix()] = 0ull;
-  __syncthreads();
-#endif
-  TL(0);
+  // The launch's epoch is the first load; its tags are derived where they are used (tag_now):
+  // the empty asm keeps the compiler from computing them right after a branch join near the
+  // kernel start, where it can only wait for every load issued so far (the weight stream
+  // included).
+  const uint32_t epoch_raw = ld_dev(a0.launches + bix());
+  const int l_end = MULTI ? a0.n_layer : a0.layer + 1;
+  uint32_t xkeep = 0u;  // MULTI: this thread's x value of its out_proj row, from the last layer
+  for (int l = a0.layer; l < l_end; ++l) {
+  // indices re-derived in every layer (opaque, so not hoisted and kept live across layers)
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, wg = bix();
-  // The launch's epoch is the first load; its tag is derived where it is used (tag_now): the
-  // empty asm keeps the compiler from computing it right after a branch join near the kernel
-  // start, where it can only wait for every load issued so far (the weight stream included).
-  const uint32_t epoch_raw = ld_dev(a.launches + wg);
-  auto tag_now = [&]() {
+  const FusedArgs a = MULTI ? tab[l] : a0;  // (scalar loads of this layer's arguments)
+  auto tag_of_layer = [&](int layer) {
     uint32_t v = epoch_raw;
     asm volatile("" : "+v"(v));
-    return (v + 1u) & 0xffffu;
+    return (v * (uint32_t)a0.n_layer + (uint32_t)layer + 1u) & 0xffffu;
   };
+  auto tag_now = [&]() { return tag_of_layer(l); };
+  const bool poll_x = MULTI && l > a0.layer;  // x of this layer from the previous one's words
+  const uint32_t* x_src = a0.xT + (size_t)(((l - 1) & 1) * kXRep + wg % kXRep) * kXStride;
+  uint32_t* x_pub = MULTI && l + 1 < l_end ? a0.xT + (size_t)((l & 1) * kXRep) * kXStride : nullptr;
+#ifdef DFSSM_TIMELINE
+  if (tix() < kTlStamps) tl_s[tix()] = 0ull;
+  lds_barrier();
+#endif
+  TL(0);
+  if constexpr (MULTI && !kPrefetchNextLayer) {
+    if (poll_x) {
+      wait_prev_layer<M, RC>(x_src, a.D, tag_of_layer(l - 1), a.err);
+      lds_barrier();
+    }
+  }
   const int gA = (a.IPO + 63) / 64, gC = a.D / RC;
   const int NI = a.H * (a.P / 16), items = M * NI;
   uint32_t* hA = a.hT;                       // copy 0 (the LoRA workgroups write every copy)
@@ -692,10 +788,17 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   // state row of this workgroup's first SSM item (the other items' rows load before phase B's polls)
   // (unconditional, from a clamped item: see load_pin)
   const f32x2 h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg < items ? wg : items - 1)));
+  if constexpr (MULTI && kPrefetchNextLayer) {
+    if (poll_x) {
+      wait_prev_layer<M, RC>(x_src, a.D, tag_of_layer(l - 1), a.err);
+      lds_barrier();
+    }
+  }
 
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
   if (wg < gA) {
-    prologue<M, false>(L, pa, nullptr, a.D, 0u, a.err);  // no polls in the IN prologue
+    if (poll_x) prologue<M, true>(L, pa, x_src, a.D, tag_of_layer(l - 1), a.err);
+    else prologue<M, false>(L, pa, nullptr, a.D, 0u, a.err);  // x loaded ahead, no polls
     TL(1);
     for (int grp = wg; grp < gA; grp += G) {
       if (grp != wg) {
@@ -707,14 +810,18 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       TL(2);
       const uint32_t tag = tag_now();
       lora_finish<M>(L, hA_mine, hv, tag, a.err);
-      __syncthreads();
+      lds_barrier();
       TL(3);
       store_conv(epilogue<M, true>(L, a, ea, grp, tag));
       TL(4);
-      __syncthreads();
+      lds_barrier();
     }
   } else if (wg < gA + DFSSM_LORA_R) {
-    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err);
+    if (poll_x)
+      lora_rank<M, true>(L, nullptr, x_src, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err,
+                         tag_of_layer(l - 1));
+    else
+      lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err, 0u);
     TL(4);
   }
   // ---- phase B: SSM + gate ----
@@ -725,14 +832,15 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, wg, a.DI);
     else load_bits(wc, a.out_bits, wg, a.DI);
     ec = load_epi<M, false, RC>(a, wg);
+    if (poll_x) ec.xres = xkeep;  // written by this thread in the previous layer
   }
-  const int nk = wg < items ? (items - 1 - wg) / G + 1 : 0;  // <= kMaxItems
+  const int nk = wg < items ? (items - 1 - wg) / G + 1 : 0;  // <= kItemsOf<M>
   if (nk > 0) {
-    f32x2 hk[kMaxItems];
-    float dk[kMaxItems];
+    f32x2 hk[kItemsOf<M>];
+    float dk[kItemsOf<M>];
     hk[0] = h0;
 #pragma unroll
-    for (int k = 0; k < kMaxItems; ++k) {
+    for (int k = 0; k < kItemsOf<M>; ++k) {
       if (k < nk) {
         const Item t = item_of(a, wg + k * G);
         if (k > 0) hk[k] = __builtin_nontemporal_load((const f32x2*)state_row(a, t));
@@ -742,16 +850,16 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     const uint32_t tag = tag_now();
     TL(5);
     for (int k = 0; k < nk; ++k) poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
-    __syncthreads();
+    lds_barrier();
     TL(6);
 #pragma unroll
-    for (int k = 0; k < kMaxItems; ++k)
+    for (int k = 0; k < kItemsOf<M>; ++k)
       if (k < nk) ssm_item<M>(L, a, k, item_of(a, wg + k * G), hk[k], dk[k], tag);
   }
   // ---- phase C: out_proj + residual (workgroups < gC), LoRA ranks (gC .. gC + 15) ----
   TL(7);
   if (wg < gC) {
-    __syncthreads();  // LDS reuse after phase A
+    lds_barrier();  // LDS reuse after phase A
     PIn<M> pc;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
     const uint32_t tag = tag_now();
@@ -769,24 +877,25 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       else gemv_partials<M>(L, wc, a.DI);
       TL(10);
       lora_finish<M>(L, hC_mine, hv, tag, a.err);
-      __syncthreads();
+      lds_barrier();
       TL(11);
-      (void)epilogue<M, false, RC>(L, a, ec, grp, tag);
+      (void)epilogue<M, false, RC>(L, a, ec, grp, tag, x_pub, MULTI ? &xkeep : nullptr);
       TL(12);
-      __syncthreads();
+      lds_barrier();
     }
   } else if (wg < gC + DFSSM_LORA_R) {
-    __syncthreads();
-    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err);
+    lds_barrier();
+    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err, tag_now());
     TL(12);
   }
-  __syncthreads();  // every wave of this workgroup has read its launch count
-  if (tid == 0) st_dev(a.launches + wg, epoch_raw + 1u);
+  lds_barrier();  // LDS reuse by the next layer; every wave has read the launch count
   TL(13);
 #ifdef DFSSM_TIMELINE
-  __syncthreads();
-  TL_FLUSH(epoch_raw);
+  lds_barrier();
+  TL_FLUSH(epoch_raw * (uint32_t)a0.n_layer + (uint32_t)l);
 #endif
+  }
+  if (tix() == 0) st_dev(a0.launches + bix(), epoch_raw + 1u);
 }
 
 // The one-launch layer waits between its workgroups, so all G of them must be resident at once:
@@ -795,10 +904,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
 // kernel). The grid must also hold the phase-A and phase-C workgroups plus their 16 LoRA
 // workgroups, and every workgroup that reads x in phase A must also own an SSM item: phase C
 // overwrites x once it has seen every item's output, which then implies that all reads of x are
-// done. A workgroup polls at most kMaxItems items (two waves each). The state width (d_state 128 =
-// two columns per lane) and P % 16 == 0 are checked with the model dims.
-// Rows per out_proj group (RC): 32 when D / 32 groups and the 16 LoRA workgroups fit the grid, else
-// 64 (16-row groups measured 1% slower per step at batch 1: 128 pollers of the gated words).
+// done. A workgroup polls at most 2 M (and kMaxItems) items (two waves each). The state width
+// (d_state 128 = two columns per lane) and P % 16 == 0 are checked with the model dims.
+// Rows per out_proj group (RC): 32 when D / 32 groups and the 16 LoRA workgroups fit the grid,
+// else 64 (16-row groups measured 1% slower per step at batch 1: 128 pollers of the gated words).
 // Returns G, or 0 when the layer must run as five kernels.
 int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int DI, int H, int P, int* rc_out) {
   const int G = cus < kFusedMaxGrid ? cus : kFusedMaxGrid;
@@ -808,26 +917,26 @@ int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int D
   if (per_cu < 1 || (long long)per_cu * cus < G) return 0;  // not all workgroups co-resident
   const int gA = (IPO + 63) / 64, gC = D / rc, items = M * H * (P / 16);
   if (gA > kFusedMaxGroups || D > kFMaxK || DI > kFMaxK || G < gA + DFSSM_LORA_R || G < gC + DFSSM_LORA_R ||
-      items < gA + DFSSM_LORA_R || items > kMaxItems * G)
+      items < gA + DFSSM_LORA_R || items > 2 * M * G || items > kMaxItems * G)
     return 0;
   if (rc_out) *rc_out = rc;
   return G;
 }
 
-template <int M, int RC>
+template <int M, int RC, bool MULTI>
 static int occupancy_of() {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<M, RC>),
-                                                   kFT, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(&layer_fused_kernel<M, RC, MULTI>), kFT, 0) != hipSuccess)
     return 0;
   return per_cu;
 }
 
 // Device facts for the plan, queried once per device: CU count and, per batch M = 1..4, the
-// occupancy of both row-group instantiations.
+// occupancy of both row-group instantiations, single-layer [0] and multi-layer [1].
 struct FusedDev {
   int cus = -1;
-  int per_cu[5][2] = {};
+  int per_cu[5][2][2] = {};
 };
 
 static const FusedDev* fused_dev() {
@@ -838,23 +947,24 @@ static const FusedDev* fused_dev() {
   if (d.cus < 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
-    d.per_cu[1][0] = occupancy_of<1, 32>(); d.per_cu[1][1] = occupancy_of<1, 64>();
-    d.per_cu[2][0] = occupancy_of<2, 32>(); d.per_cu[2][1] = occupancy_of<2, 64>();
-    d.per_cu[3][0] = occupancy_of<3, 32>(); d.per_cu[3][1] = occupancy_of<3, 64>();
-    d.per_cu[4][0] = occupancy_of<4, 32>(); d.per_cu[4][1] = occupancy_of<4, 64>();
+#define DFSSM_OCC(MM)                                                                     \
+  d.per_cu[MM][0][0] = occupancy_of<MM, 32, false>(); d.per_cu[MM][1][0] = occupancy_of<MM, 64, false>(); \
+  d.per_cu[MM][0][1] = occupancy_of<MM, 32, true>(); d.per_cu[MM][1][1] = occupancy_of<MM, 64, true>();
+    DFSSM_OCC(1) DFSSM_OCC(2) DFSSM_OCC(3) DFSSM_OCC(4)
+#undef DFSSM_OCC
     d.cus = cus;
   }
   return &d;
 }
 
-static int fused_grid(int M, int IPO, int D, int DI, int H, int P, int* rc) {
+static int fused_grid(int M, int IPO, int D, int DI, int H, int P, int* rc, bool multi = false) {
   const FusedDev* d = fused_dev();
   if (!d || M < 1 || M > 4) return 0;
-  return fused_plan(d->cus, d->per_cu[M][0], d->per_cu[M][1], M, IPO, D, DI, H, P, rc);
+  return fused_plan(d->cus, d->per_cu[M][0][multi], d->per_cu[M][1][multi], M, IPO, D, DI, H, P, rc);
 }
 
-bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P) {
-  return fused_grid(M, IPO, D, DI, H, P, nullptr) > 0;
+bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P, bool multi) {
+  return fused_grid(M, IPO, D, DI, H, P, nullptr, multi) > 0;
 }
 
 // out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.
@@ -874,10 +984,33 @@ hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s) {
   int rc = 0;
   const int G = fused_grid(M, a.IPO, a.D, a.DI, a.H, a.P, &rc);
   if (G < 1) return hipErrorNotSupported;
-#define DFSSM_FUSED(MM)                                                                          \
-  case MM:                                                                                       \
-    if (rc == 32) hipLaunchKernelGGL((layer_fused_kernel<MM, 32>), dim3(G), dim3(kFT), 0, s, a);   \
-    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64>), dim3(G), dim3(kFT), 0, s, a);          \
+  const FusedArgs* none = nullptr;
+#define DFSSM_FUSED(MM)                                                                              \
+  case MM:                                                                                           \
+    if (rc == 32) hipLaunchKernelGGL((layer_fused_kernel<MM, 32, false>), dim3(G), dim3(kFT), 0, s, a, none); \
+    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64, false>), dim3(G), dim3(kFT), 0, s, a, none);        \
+    break;
+  switch (M) {
+    DFSSM_FUSED(1)
+    DFSSM_FUSED(2)
+    DFSSM_FUSED(3)
+    DFSSM_FUSED(4)
+    default: return hipErrorInvalidValue;
+  }
+#undef DFSSM_FUSED
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_layers(const FusedArgs& a, const FusedStrides& st, FusedArgs* tab, int M, hipStream_t s) {
+  int rc = 0;
+  const int G = fused_grid(M, a.IPO, a.D, a.DI, a.H, a.P, &rc, true);
+  if (G < 1 || a.xT == nullptr || tab == nullptr || a.layer < 0 || a.layer >= a.n_layer || a.n_layer > kMaxLayers)
+    return hipErrorNotSupported;
+  hipLaunchKernelGGL(layer_table_kernel, dim3(1), dim3(kMaxLayers), 0, s, a, st, tab);
+#define DFSSM_FUSED(MM)                                                                              \
+  case MM:                                                                                           \
+    if (rc == 32) hipLaunchKernelGGL((layer_fused_kernel<MM, 32, true>), dim3(G), dim3(kFT), 0, s, a, tab); \
+    else hipLaunchKernelGGL((layer_fused_kernel<MM, 64, true>), dim3(G), dim3(kFT), 0, s, a, tab);        \
     break;
   switch (M) {
     DFSSM_FUSED(1)

@@ -70,6 +70,7 @@ _SIGS = {
     "dfssm_workspace_error_flag": (P, [ctypes.POINTER(Dims), P]),
     "dfssm_embed": (c_int, [ctypes.POINTER(Model), P, P, P, P]),
     "dfssm_layer_step": (c_int, [ctypes.POINTER(Model), c_int, P, ctypes.POINTER(State), P, P]),
+    "dfssm_decode_one_launch": (c_int, [ctypes.POINTER(Model)]),
     "dfssm_layer_phase": (c_int, [ctypes.POINTER(Model), c_int, c_int, P, ctypes.POINTER(State), P, P]),
     "dfssm_lmhead_argmax": (c_int, [ctypes.POINTER(Model), P, P, P, P, P, P]),
     "dfssm_decode_step": (c_int, [ctypes.POINTER(Model), P, P, ctypes.POINTER(State), P, P, P, c_int, P]),

@@ -94,14 +94,22 @@ int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
  * phase-organised one-launch layer where the shape allows it, else five kernels;
  * DFSSM_LAYER_ITEM runs the item-organised one-launch layer (one workgroup per SSM item, grid a
  * power of two <= 256) where the shape allows it, else as DFSSM_LAYER_FUSED;
- * DFSSM_LAYER_FIVE always runs five kernels; DFSSM_LAYER_AUTO (default) is the faster of the
- * two one-launch layers on the benchmark shape (currently DFSSM_LAYER_FUSED). All give
- * bit-identical results; the setting exists to compare them. No counterpart in the reference. */
+ * DFSSM_LAYER_MULTI lets dfssm_decode_step run all layers of a step in one launch of the
+ * phase-organised layer (when every per-layer weight pointer is equally spaced from layer to
+ * layer, as one allocation per field gives), else as DFSSM_LAYER_FUSED; DFSSM_LAYER_FIVE always
+ * runs five kernels per layer; DFSSM_LAYER_AUTO (default) is the fastest on the benchmark
+ * shape (DFSSM_LAYER_FUSED). All give bit-identical results; the setting exists to compare them.
+ * No counterpart in the reference. */
 #define DFSSM_LAYER_AUTO 0
 #define DFSSM_LAYER_FUSED 1
 #define DFSSM_LAYER_FIVE 2
 #define DFSSM_LAYER_ITEM 3
+#define DFSSM_LAYER_MULTI 4
 int dfssm_set_layer_kernel(int which);
+/* 1 when dfssm_decode_step runs all layers of a step in one launch with the current setting on
+ * the current device (batch <= 4, a shape the phase-organised layer takes, per-layer weights
+ * equally spaced), else 0. No counterpart in the reference. */
+int dfssm_decode_one_launch(const dfssm_model* model);
 
 /* ---- load-time layout ------------------------------------------------------------------ */
 /* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, row_bytes) table

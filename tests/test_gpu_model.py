@@ -143,6 +143,45 @@ def test_one_launch_layer_equals_five_kernels(tiny_weights, B, kernel):
     assert gpu.error_flag() == 0
 
 
+def _decode_run(w, B, kernel, steps, prompt_len=5):
+    """`steps` greedy decode steps through dfssm_decode_step with layer-kernel setting `kernel`:
+    per step the logits and next tokens, then x and both states."""
+    from dfssm import _C
+    lib = _C.lib()
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, prompt_len)))
+    prev = lib.dfssm_set_layer_kernel(kernel)
+    try:
+        one = lib.dfssm_decode_one_launch(gpu._model)
+        out = []
+        for _ in range(steps):
+            lg, nx = gpu.decode_step_eager(None)
+            out.append((lg.clone(), nx.clone()))
+        torch.cuda.synchronize()
+    finally:
+        lib.dfssm_set_layer_kernel(prev)
+    assert gpu.error_flag() == 0
+    return one, out, gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 4])
+def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
+    """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
+    from layer to layer as tagged words) against the five-kernel form, 6 steps: logits, tokens,
+    x and both states identical bit for bit."""
+    print(f"multi-layer launch B={B}", flush=True)
+    one, out_m, x_m, h_m, c_m = _decode_run(tiny_weights, B, 4, 6)
+    assert one == 1, "the multi-layer launch did not apply"
+    one5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
+    assert one5 == 0
+    for t, ((lm, nm), (l5, n5)) in enumerate(zip(out_m, out_5)):
+        assert torch.equal(lm.view(torch.int16), l5.view(torch.int16)), f"step {t}: logits differ"
+        assert torch.equal(nm, n5), f"step {t}: tokens differ"
+    assert torch.equal(x_m.view(torch.int16), x_5.view(torch.int16))
+    assert torch.equal(h_m, h_5)
+    assert torch.equal(c_m.view(torch.int16), c_5.view(torch.int16))
+
+
 @pytest.mark.parametrize("kernel", [3, 1])
 @pytest.mark.parametrize("B", [1, 4])
 def test_one_launch_layer_wide_model(B, kernel):
