@@ -55,7 +55,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.hpart = off;    off = align_up(off + (r.B <= 4 ? (size_t)r.head_groups * (r.D / 512) * r.B * 64 * 8 : 0));
   w.hdig = off;     off = align_up(off + (r.B > 4 ? head_digit_bytes(r.B, r.D) : 0));  // batched int8 head
-  w.samp = off;     off = align_up(off + (size_t)r.B * 2 * ((r.V + 3) / 4 * 4) * 4);  // sampler rows z | e
+  w.samp = off;     off = align_up(off + (size_t)r.B * 2 * sample_row_floats(r.V) * 4);  // sampler rows
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
   // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by

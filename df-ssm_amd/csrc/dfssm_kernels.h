@@ -163,8 +163,15 @@ struct SampleArgs {
   int mode;                  // 0: gen_test.py order, 1: training-script order (see sample.hip)
   uint64_t seed;
   int V;
-  float* escratch;           // (M, 2, ld) workspace rows z | exp(z - max z), ld = V rounded up to 4
+  float* escratch;           // (M, 2, sample_row_floats(V)) workspace rows: the slice partials, then
+                             // e = exp(z - max z) (V rounded up to 4 floats, then zeros)
 };
+// Floats per sampler scratch row: V rounded up to 4, at least 1024 (the partials of one slice
+// workgroup take 3 KiB).
+__host__ __device__ inline int sample_row_floats(int V) {
+  const int ld = (V + 3) / 4 * 4;
+  return ld > 1024 ? ld : 1024;
+}
 
 struct HeadArgs {
   const uint16_t* x;         // (M, D) fp16 residual

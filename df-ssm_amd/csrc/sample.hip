@@ -21,15 +21,36 @@
 //            with one random number per draw.
 // The kept set is found without sorting: a 4-pass radix select (8 bits per pass, MSB first) over
 // the fp32 bit patterns of e_i (positive floats order as integers) with exact 64-bit bin sums of
-// E_i in LDS, then the tied tokens at the boundary key are kept in index order as far as the
-// mass allows. z and e live in two workspace rows of the sequence (L2-resident between passes),
-// read wave-contiguously: thread t owns the 16-byte vectors t, t + 1024, ...
+// E_i, then the tied tokens at the boundary key are kept in index order as far as the mass allows.
+// Three kernels: sample_slice_kernel<0> and <1> split each sequence's vocabulary over NW
+// workgroups (contiguous slices): the maxima of z, then e (to the sequence's e row), the exact
+// partial normalizers and the partial first-pass histograms (the pass over every token, whose
+// few populated bins make the per-wave atomics collide most); sample_kernel (one workgroup of
+// 1024 threads per sequence) adds the partials and runs passes 2..4, the ties and the draw over
+// the e row (L2-resident), read wave-contiguously: thread t owns the 16-byte vectors t, t + 1024,
+// ... The partials occupy the sequence's first scratch row.
 #include "common.h"
 #include "dfssm_kernels.h"
 
 namespace dfssm {
 
-constexpr int kST = 1024;                  // threads per sequence
+constexpr int kST = 1024;                  // threads per sequence (selection and draw)
+constexpr int kSW = 256;                   // threads per slice workgroup
+constexpr int kMaxSlices = 64;             // slice workgroups per sequence
+
+// Slice workgroups per sequence: at most kMaxSlices, and the partials (maxima, normalizers and
+// 256-bin histograms) must fit the first scratch row of rs = sample_row_floats(V) floats.
+__host__ __device__ inline int sample_slices(int rs) {
+  const int n = (rs * 4 - 1024) / 2048;
+  return n < 1 ? 1 : (n > kMaxSlices ? kMaxSlices : n);
+}
+// partials in the first row: maxima (float[NW]) at byte 0, normalizers (u64[NW]) at byte 256,
+// histograms (u64[NW][256]) at byte 1024
+__device__ __forceinline__ float* part_max(float* row0) { return row0; }
+__device__ __forceinline__ unsigned long long* part_z(float* row0) { return (unsigned long long*)((char*)row0 + 256); }
+__device__ __forceinline__ unsigned long long* part_hist(float* row0) {
+  return (unsigned long long*)((char*)row0 + 1024);
+}
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -89,71 +110,90 @@ __device__ __forceinline__ long long block_sum_ll(long long v, long long* red) {
   return t;
 }
 
+// PHASE 0: the maximum of z over the slice; PHASE 1: e = exp(z - max z) of the slice to the e row
+// (the last slice also zeroes the padding up to ld), its exact normalizer and first-pass histogram.
+// Slice w of NW: tokens [w SL, min(V, (w + 1) SL)), SL = ceil(V / NW).
+template <int PHASE>
+__global__ __launch_bounds__(kSW) void sample_slice_kernel(SampleArgs a) {
+  __shared__ unsigned long long hist[kSW / 64][256];
+  __shared__ float redf[kSW / 64];
+  __shared__ long long redl[kSW / 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int sw = blockIdx.x, b = blockIdx.y, V = a.V;
+  const int ld = (V + 3) / 4 * 4, rs = sample_row_floats(V);
+  const int NW = sample_slices(rs), SL = (V + NW - 1) / NW;
+  const int lo = sw * SL, hi = lo + SL < V ? lo + SL : V;
+  const uint16_t* lg = a.logits + (size_t)b * V;
+  const int* cn = a.counts + (size_t)b * V;
+  float* row0 = a.escratch + (size_t)b * 2 * rs;
+  float* er = row0 + rs;
+  if (PHASE == 0) {
+    float m = -INFINITY;
+    for (int i = lo + tid; i < hi; i += kSW) m = fmaxf(m, penalized(h2f(lg[i]), cn[i], a));
+    const float wm = wave_max_dpp_f32(m);
+    if (lane == 0) redf[w] = wm;
+    __syncthreads();
+    if (tid == 0) {
+      float t = redf[0];
+      for (int k = 1; k < kSW / 64; ++k) t = fmaxf(t, redf[k]);
+      part_max(row0)[sw] = t;
+    }
+    return;
+  }
+  for (int q = tid; q < (kSW / 64) * 256; q += kSW) (&hist[0][0])[q] = 0ull;
+  float m = part_max(row0)[0];
+  for (int k = 1; k < NW; ++k) m = fmaxf(m, part_max(row0)[k]);
+  __syncthreads();
+  long long zs = 0;
+  for (int i = lo + tid; i < hi; i += kSW) {
+    const float e = dev_expf(penalized(h2f(lg[i]), cn[i], a) - m);
+    er[i] = e;
+    const unsigned long long E = fixed40(e);
+    zs += (long long)E;
+    if (E != 0ull) atomicAdd(&hist[w][__builtin_bit_cast(uint32_t, e) >> 24], E);
+  }
+  if (sw == NW - 1)
+    for (int i = V + tid; i < ld; i += kSW) er[i] = 0.0f;
+  const long long Zw = block_sum_ll<kSW>(zs, redl);  // (its barriers also publish hist)
+  if (tid == 0) part_z(row0)[sw] = (unsigned long long)Zw;
+  if (tid < 256) {  // 256 bins, one per thread
+    unsigned long long t = 0;
+    for (int k = 0; k < kSW / 64; ++k) t += hist[k][tid];
+    part_hist(row0)[(size_t)sw * 256 + tid] = t;
+  }
+}
+
 __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
   __shared__ unsigned long long hist[kST / 64][256];  // one histogram per wave: fewer colliding atomics
-  __shared__ float redf[kST / 64];
   __shared__ long long redl[kST / 64];
-  __shared__ unsigned long long sel[2];  // radix prefix, mass above it
+  __shared__ unsigned long long sel[2];  // mass above the chosen bin (d > 0), (d = 0)
+  __shared__ unsigned long long wtot[4];
+  __shared__ int dsel;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int b = blockIdx.x, V = a.V;
   const int ld = (V + 3) / 4 * 4;
   const int nv4 = (ld / 4 + kST - 1) / kST;  // vectors per thread
-  const uint16_t* lg = a.logits + (size_t)b * V;
-  const int* cn = a.counts + (size_t)b * V;
-  float* zr = a.escratch + (size_t)b * 2 * ld;  // z, and e = exp(z - max z)
-  float* er = zr + ld;
-
-  // z (padding: -inf) to the z row, and its maximum
-  float m = -INFINITY;
-#pragma unroll 1
-  for (int c = 0; c < nv4; c += 4) {
-    uint16_t l16[16];
-    int cc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int i = tok_of(c, j);
-      l16[j] = lg[i < V ? i : V - 1];
-      cc[j] = cn[i < V ? i : V - 1];
+  const int rs = sample_row_floats(V), NW = sample_slices(rs);
+  float* row0 = a.escratch + (size_t)b * 2 * rs;  // the slices' partials
+  float* er = row0 + rs;                          // e = exp(z - max z)
+  // the exact normalizer, the sum of the slices' (every partial is an integer: any order)
+  __shared__ unsigned long long zsum, hsum[4][256];
+  if (w == 0) {
+    unsigned long long zp = lane < NW ? part_z(row0)[lane] : 0ull;
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)zp, off, 64);
+      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(zp >> 32), off, 64);
+      zp += ((unsigned long long)hi << 32) | lo;
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float z4[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int i = tok_of(c, 4 * k + t);
-        z4[t] = (c + k < nv4 && i < V) ? penalized(h2f(l16[4 * k + t]), cc[4 * k + t], a) : -INFINITY;
-        m = fmaxf(m, z4[t]);
-      }
-      const int q = tid + kST * (c + k);
-      if (c + k < nv4 && 4 * q < ld) *(f32x4*)(zr + 4 * q) = f32x4{z4[0], z4[1], z4[2], z4[3]};
-    }
+    if (lane == 0) zsum = zp;
   }
-  {
-    const float wm = wave_max_dpp_f32(m);
-    if (lane == 0) redf[w] = wm;
-    __syncthreads();
-    m = redf[0];
-    for (int k = 1; k < kST / 64; ++k) m = fmaxf(m, redf[k]);
+  {  // the first pass's histogram: thread t adds bin t % 256 over slices t / 256, + 4, ...
+    unsigned long long hp = 0;
+    for (int k = tid >> 8; k < NW; k += 4) hp += part_hist(row0)[(size_t)k * 256 + (tid & 255)];
+    hsum[tid >> 8][tid & 255] = hp;
   }
-  // e = exp(z - max z) to the e row (padding 0), and the exact normalizer
-  long long zs = 0;
-#pragma unroll 1
-  for (int c = 0; c < nv4; c += 4) {
-    float v[16];
-    load4(zr, ld, c, v);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float e4[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        e4[t] = dev_expf(v[4 * k + t] - m);
-        zs += (c + k < nv4 && tok_of(c, 4 * k + t) < V) ? (long long)fixed40(e4[t]) : 0ll;
-      }
-      const int q = tid + kST * (c + k);
-      if (c + k < nv4 && 4 * q < ld) *(f32x4*)(er + 4 * q) = f32x4{e4[0], e4[1], e4[2], e4[3]};
-    }
-  }
-  const unsigned long long Z = (unsigned long long)block_sum_ll<kST>(zs, redl);
+  __syncthreads();
+  const unsigned long long Z = zsum;
   const unsigned long long thr = (unsigned long long)((double)a.top_p * (double)Z);
   uint32_t kb = 0;  // boundary key and last kept index among its ties; all kept: 0 and V
   int ib = V;
@@ -164,75 +204,146 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
       const int shift = 24 - 8 * pass;
       for (int q = tid; q < (kST / 64) * 256; q += kST) (&hist[0][0])[q] = 0ull;
       __syncthreads();
+      if (pass == 0 && tid < 256)  // the first pass's histogram: the slices' partials, summed above
+        hist[0][tid] = (hsum[0][tid] + hsum[1][tid]) + (hsum[2][tid] + hsum[3][tid]);
 #pragma unroll 1
-      for (int c = 0; c < nv4; c += 4) {
+      for (int c = 0; c < (pass == 0 ? 0 : nv4); c += 4) {
         float v[16];
         load4(er, ld, c, v);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const uint32_t key = __builtin_bit_cast(uint32_t, v[j]);
-          const unsigned long long E = fixed40(v[j]);
-          if (c + j / 4 < nv4 && tok_of(c, j) < V && (key & pmask) == prefix && E != 0ull)
-            atomicAdd(&hist[w][(key >> shift) & 255u], E);
+          if (c + j / 4 < nv4 && tok_of(c, j) < V && (key & pmask) == prefix) {  // few match past pass 1
+            const unsigned long long E = fixed40(v[j]);
+            if (E != 0ull) atomicAdd(&hist[w][(key >> shift) & 255u], E);
+          }
         }
       }
       __syncthreads();
-      if (tid < 256) {  // the waves' histograms summed into histogram 0
-        unsigned long long t = hist[0][tid];
-        for (int k = 1; k < kST / 64; ++k) t += hist[k][tid];
-        hist[0][tid] = t;
-      }
-      __syncthreads();
-      if (tid == 0) {  // the digit whose bin holds the first token past the mass limit
-        unsigned long long R = above;
-        int d = 255;
-        for (; d > 0; --d) {
-          if (R + hist[0][d] > thr) break;
-          R += hist[0][d];
+      // the digit d whose bin holds the first token past the mass limit, scanning bins from 255
+      // down: the largest d >= 1 with above + (mass of bins >= d) > thr, else 0; the new mass
+      // above = above + (mass of bins > d). Thread t < 256 holds bin t: the waves' histograms
+      // summed, then suffix sums within each wave (shuffles) and across the four waves (LDS).
+      unsigned long long h = 0, incl = 0;
+      if (tid < 256) {
+        for (int k = 0; k < kST / 64; ++k) h += hist[k][tid];
+        incl = h;
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t lo = (uint32_t)__shfl_down((int)(uint32_t)incl, off, 64);
+          const uint32_t hi = (uint32_t)__shfl_down((int)(uint32_t)(incl >> 32), off, 64);
+          if (lane + off < 64) incl += ((unsigned long long)hi << 32) | lo;
         }
-        sel[0] = prefix | ((uint32_t)d << shift);
-        sel[1] = R;
+        if (lane == 0) wtot[w] = incl;  // bins 64 w .. 64 w + 63
+        if (tid == 0) dsel = 0;
       }
       __syncthreads();
-      prefix = (uint32_t)sel[0];
-      above = sel[1];
+      if (tid < 256) {
+        for (int k = w + 1; k < 4; ++k) incl += wtot[k];
+        const unsigned long long in = above + incl, ex = in - h;  // bins >= tid, bins > tid
+        if (tid == 0) sel[1] = ex;                                // the d = 0 case
+        if (tid >= 1 && in > thr && ex <= thr) {                  // at most one such bin
+          dsel = tid;
+          sel[0] = ex;
+        }
+      }
+      __syncthreads();
+      const int d = dsel;
+      above = d > 0 ? sel[0] : sel[1];
+      prefix |= (uint32_t)d << shift;
       pmask |= 255u << shift;
+      __syncthreads();  // sel and dsel are rewritten by the next pass
     }
     kb = prefix;
     // the tokens with key kb, in index order, stay while the mass above them is <= thr: all of
-    // them unless more tie than the mass allows; then the nkeep-th smallest index among them by
-    // bisection over the index (rare: equal fp32 probabilities at the cut)
+    // them unless more tie than the mass allows; then ib = the index of the nkeep-th of them
+    // (ties are common: fp16 logits take few distinct values). Index order is slab order, then
+    // thread order within a slab: one pass counts each thread's ties per slab, the slab totals
+    // give the slab holding the nkeep-th tie, a scan over that slab's threads the thread, and the
+    // thread its token.
     const unsigned long long eb = fixed40(__builtin_bit_cast(float, kb));
     const long long nkeep = eb ? (long long)((thr - above) / eb) + 1 : (long long)V;  // eb > 0 by construction
-    int lo_i = 0, hi_i = V - 1;  // invariant: the answer is in [lo_i, hi_i]
-    for (int it = 0; it < 32; ++it) {
-      const int mid = it == 0 ? V - 1 : (lo_i + hi_i) / 2;
-      long long cnt = 0;
-#pragma unroll 1
-      for (int c = 0; c < nv4; c += 4) {
+    constexpr int kSl = kSampleMaxVocab / (4 * kST);
+    int tcnt[kSl];
+#pragma unroll
+    for (int k = 0; k < kSl; ++k) tcnt[k] = 0;
+#pragma unroll
+    for (int c = 0; c < kSl; c += 4) {
+      if (c < nv4) {
         float v[16];
         load4(er, ld, c, v);
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          cnt += (c + j / 4 < nv4 && tok_of(c, j) <= mid && tok_of(c, j) < V &&
-                  __builtin_bit_cast(uint32_t, v[j]) == kb) ? 1 : 0;
+          tcnt[c + j / 4] += (c + j / 4 < nv4 && tok_of(c, j) < V && __builtin_bit_cast(uint32_t, v[j]) == kb) ? 1 : 0;
       }
-      cnt = block_sum_ll<kST>(cnt, redl);  // ties with index <= mid
-      if (it == 0) {
-        if (cnt <= nkeep) break;  // every tie is kept: ib = V
-        continue;
+    }
+    __shared__ int slab_ties[kST / 64][kSl];
+    __shared__ int tie_pick[2];  // slab, rank of the wanted tie within it (1-based)
+#pragma unroll
+    for (int k = 0; k < kSl; ++k) {
+      const int ws = wave_sum_dpp_i32(tcnt[k]);
+      if (lane == 0) slab_ties[w][k] = ws;
+    }
+    __shared__ int slab_tot[kSl];
+    __syncthreads();
+    if (tid < kSl) {
+      int t = 0;
+      for (int q = 0; q < kST / 64; ++q) t += slab_ties[q][tid];
+      slab_tot[tid] = t;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      long long cum = 0;
+      int ks = -1;
+      long long rank = 0;
+      for (int k = 0; k < kSl && ks < 0; ++k) {
+        if (cum + slab_tot[k] >= nkeep) {
+          ks = k;
+          rank = nkeep - cum;
+        }
+        cum += slab_tot[k];
       }
-      if (cnt >= nkeep) hi_i = mid; else lo_i = mid + 1;
-      if (lo_i == hi_i) {
-        ib = lo_i;
-        break;
+      tie_pick[0] = ks;  // -1: no more ties than nkeep, every tie is kept
+      tie_pick[1] = (int)rank;
+    }
+    __syncthreads();
+    const int ks = tie_pick[0], rank = tie_pick[1];
+    if (ks >= 0) {  // exclusive scan of the threads' ties in slab ks (thread order = index order)
+      int mine = 0;
+#pragma unroll
+      for (int k = 0; k < kSl; ++k)
+        if (k == ks) mine = tcnt[k];
+      int incl = mine;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
       }
+      if (lane == 63) slab_ties[w][0] = incl;
+      __syncthreads();
+      int base = 0;
+      for (int q = 0; q < w; ++q) base += slab_ties[q][0];
+      const int excl = base + incl - mine;
+      if (mine > 0 && excl < rank && rank <= excl + mine) {  // exactly one thread
+        const int q = tid + kST * ks, last = ld / 4 - 1;
+        const f32x4 x = *(const f32x4*)(er + 4 * (q < last ? q : last));
+        int seen = excl;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float xt = x[t];  // through a scalar (see the draw below)
+          if (4 * q + t < V && __builtin_bit_cast(uint32_t, xt) == kb && ++seen == rank) tie_pick[1] = -(4 * q + t) - 1;
+        }
+      }
+      __syncthreads();
+      ib = -tie_pick[1] - 1;
     }
   }
   // inverse-CDF draw in index order (slab k = tokens 4096 k .. 4096 k + 4095, then thread, then
   // element): kept mass per slab (exact in fp64: slab sums < 2^53), the slab, the thread by a
   // scan of the slab's per-thread masses, the token within the thread
   constexpr int kSlabs = kSampleMaxVocab / (4 * kST);
+  __shared__ double slab_w[kST / 64][kSlabs];
+  __shared__ unsigned long long slab_t[kSlabs];
+  __shared__ int pick[2];  // slab, thread
+  __shared__ unsigned long long rem_s;
   double slab[kSlabs];
 #pragma unroll
   for (int k = 0; k < kSlabs; ++k) slab[k] = 0.0;
@@ -249,10 +360,6 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
       }
     }
   }
-  __shared__ double slab_w[kST / 64][kSlabs];
-  __shared__ unsigned long long slab_t[kSlabs];
-  __shared__ int pick[2];  // slab, thread
-  __shared__ unsigned long long rem_s;
 #pragma unroll
   for (int k = 0; k < kSlabs; ++k) {
     const double ws = wave_sum_dpp_f64(slab[k]);
@@ -323,6 +430,9 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
 
 hipError_t launch_sample(const SampleArgs& a, int batch, hipStream_t s) {
   if (a.V < 1 || a.V > kSampleMaxVocab) return hipErrorInvalidValue;
+  const int NW = sample_slices(sample_row_floats(a.V));
+  hipLaunchKernelGGL(sample_slice_kernel<0>, dim3(NW, batch), dim3(kSW), 0, s, a);
+  hipLaunchKernelGGL(sample_slice_kernel<1>, dim3(NW, batch), dim3(kSW), 0, s, a);
   hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kST), 0, s, a);
   return hipGetLastError();
 }
