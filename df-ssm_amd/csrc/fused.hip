@@ -233,13 +233,18 @@ __device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
 __device__ __forceinline__ uint32_t tagged(uint32_t tag, uint16_t v) { return (tag << 16) | v; }
 
 // Poll a tagged word until it carries `tag`; returns its fp16 bits. After a timeout (`ok`
-// false) polls return at once.
+// false) polls return at once. One load in flight per poll: keeping two in flight (staggered)
+// made the phase hand-offs slower, the extra poll traffic delaying the producers' stores, and
+// sleeping 64 or 256 clocks between polls measured the same as 64.
+__device__ __forceinline__ void poll_timeout(bool& ok, int* err) {
+  ok = false;
+  atomicOr(err, 4);
+}
 __device__ __forceinline__ uint32_t poll1(const uint32_t* p, uint32_t tag, bool& ok, int* err) {
   uint32_t v = ld_dev(p);
   for (uint32_t it = 0; ok && (v >> 16) != tag; ++it) {
     if (it == kSpinMax) {
-      ok = false;
-      atomicOr(err, 4);
+      poll_timeout(ok, err);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -265,8 +270,7 @@ __device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t 
     for (int j = 0; j < N; ++j) good = good && tag_ok2(v[j], tag);
     if (good) break;
     if (it == kSpinMax) {
-      ok = false;
-      atomicOr(err, 4);
+      poll_timeout(ok, err);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -625,29 +629,31 @@ __device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item&
     pollv<2>(a.bcT + (bix() % kXRep) * kBcStride + t.m * 2 * a.N + 4 * lane, tag, w, ok, a.err);
     L.item[k].bc[2 * lane] = w[0];
     L.item[k].bc[2 * lane + 1] = w[1];
-  } else if (wave == 2 * k + 1) {
+  } else if (wave == 2 * k + 1 && lane < 34) {
+    // lanes 0..31 poll 32-bit words (tag in the high half), lanes 32 and 33 64-bit words (tag in
+    // the high word), all in one loop so that neither set waits for the other's round trips
     const int r0 = t.head * a.P + 16 * t.pb;
-    if (lane < 32) {
-      const uint32_t* p = lane < 16 ? pr + a.DI + r0 + lane : pr + r0 + (lane - 16);
-      const uint32_t v = poll1(p, tag, ok, a.err);
-      if (lane < 16) L.item[k].x[lane] = (uint16_t)v;
-      else L.item[k].gate[lane - 16] = (uint16_t)v;
-    } else if (lane < 34) {
-      const uint64_t* p = a.dtT + ((size_t)t.m * a.H + t.head) * 2 + (lane - 32);
-      uint64_t v = ld_dev(p);
-      for (uint32_t it = 0; ok && (uint32_t)(v >> 32) != tag; ++it) {
-        if (it == kSpinMax) {
-          ok = false;
-          atomicOr(a.err, 4);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        v = ld_dev(p);
+    const bool w32 = lane < 32;
+    // every lane loads both kinds (from valid addresses): no divergent loads inside the loop
+    const uint32_t* p32 = (lane & 31) < 16 ? pr + a.DI + r0 + (lane & 15) : pr + r0 + (lane & 15);
+    const uint64_t* p64 = a.dtT + ((size_t)t.m * a.H + t.head) * 2 + (lane & 1);
+    auto ready = [&](uint32_t x, uint64_t y) { return w32 ? (x >> 16) == tag : (uint32_t)(y >> 32) == tag; };
+    uint32_t va = ld_dev(p32);
+    uint64_t vb = ld_dev(p64);
+    for (uint32_t it = 0; ok && !ready(va, vb); ++it) {
+      if (it == kSpinMax) {
+        poll_timeout(ok, a.err);
+        break;
       }
-      const float f = __builtin_bit_cast(float, (uint32_t)v);
-      if (lane == 32) L.item[k].dt = f;
-      else L.item[k].abar = f;
+      __builtin_amdgcn_s_sleep(1);
+      va = ld_dev(p32);
+      vb = ld_dev(p64);
     }
+    const uint64_t r = w32 ? (uint64_t)va : vb;
+    if (lane < 16) L.item[k].x[lane] = (uint16_t)r;
+    else if (lane < 32) L.item[k].gate[lane - 16] = (uint16_t)r;
+    else if (lane == 32) L.item[k].dt = __builtin_bit_cast(float, (uint32_t)r);
+    else L.item[k].abar = __builtin_bit_cast(float, (uint32_t)r);
   }
 }
 
