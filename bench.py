@@ -169,7 +169,7 @@ def time_decode(m, prompts, steps, warmup):
 def time_sampled(m, prompts, steps, warmup, T=0.7, top_p=0.9, penalty=1.2):
     """Decode with the sampling head (gen_test.py's settings: temperature 0.7, top-p 0.9,
     repetition penalty 1.2) instead of the argmax: graphs of 8 steps, HIP events. Returns ms
-    per step and the sampler kernel's own time per launch (graph of 48 launches on fixed logits)."""
+    per step and the sampler's own time per call, all its kernels (graph of 48 calls on fixed logits)."""
     import torch
     from dfssm import _C
     m.reset_state()

@@ -163,14 +163,14 @@ struct SampleArgs {
   int mode;                  // 0: gen_test.py order, 1: training-script order (see sample.hip)
   uint64_t seed;
   int V;
-  float* escratch;           // (M, 2, sample_row_floats(V)) workspace rows: the slice partials, then
-                             // e = exp(z - max z) (V rounded up to 4 floats, then zeros)
+  float* escratch;           // (M, 2, sample_row_floats(V)) workspace rows: the sums of the slice
+                             // workgroups (maxima, normalizer, histograms, masses), then
+                             // e = exp(z - max z)
 };
-// Floats per sampler scratch row: V rounded up to 4, at least 1024 (the partials of one slice
-// workgroup take 3 KiB).
+// Floats per sampler scratch row: V rounded up to 4, at least 2560 (the sums take 9472 bytes).
 __host__ __device__ inline int sample_row_floats(int V) {
   const int ld = (V + 3) / 4 * 4;
-  return ld > 1024 ? ld : 1024;
+  return ld > 2560 ? ld : 2560;
 }
 
 struct HeadArgs {

@@ -1,6 +1,6 @@
 // Sampling head (gfx950): temperature, repetition penalty and top-p (nucleus) sampling of the
-// next token from the fp16 logits, one workgroup of 1024 threads per sequence, with the chosen
-// token counted in the sequence's occurrence counts and, optionally, embedded as the next input.
+// next token from the fp16 logits, with the chosen token counted in the sequence's occurrence
+// counts.
 //
 // Reference semantics: eval/gen_test.py:54-95 (logits / T, then logits[seen] / r for every token
 // seen so far, softmax, sort descending, drop a token when the probability mass ranked above it
@@ -21,35 +21,60 @@
 //            with one random number per draw.
 // The kept set is found without sorting: a 4-pass radix select (8 bits per pass, MSB first) over
 // the fp32 bit patterns of e_i (positive floats order as integers) with exact 64-bit bin sums of
-// E_i, then the tied tokens at the boundary key are kept in index order as far as the mass allows.
-// Three kernels: sample_slice_kernel<0> and <1> split each sequence's vocabulary over NW
-// workgroups (contiguous slices): the maxima of z, then e (to the sequence's e row), the exact
-// partial normalizers and the partial first-pass histograms (the pass over every token, whose
-// few populated bins make the per-wave atomics collide most); sample_kernel (one workgroup of
-// 1024 threads per sequence) adds the partials and runs passes 2..4, the ties and the draw over
-// the e row (L2-resident), read wave-contiguously: thread t owns the 16-byte vectors t, t + 1024,
-// ... The partials occupy the sequence's first scratch row.
+// E_i; the tokens tied at the boundary key kb are kept in index order as far as the mass allows.
+//
+// Every pass over the vocabulary runs on NW slice workgroups per sequence (contiguous slices of at
+// most 1024 tokens), one launch per pass, so that no pass is bound by one CU's VALU issue:
+//   max    the slice maxima of z; slice 0 clears the sequence's global sums
+//   exp    e_i to the sequence's e row, the normalizer Z and the histogram of the keys' top byte,
+//          summed into global memory with 64-bit atomics (integers: any order)
+//   pass p = 1..3: digit p - 1 from the global histogram of pass p - 1 and the selection the
+//          previous launch stored (computed alike by every workgroup, stored by the first), then
+//          the histogram of byte p of the keys that match the selection
+//   mass   the last digit, i.e. kb; per slice the exact mass of the keys above kb and the count
+//          of keys equal to kb
+//   draw   one workgroup per sequence: the ties kept per slice (in slice order, i.e. index
+//          order), the kept masses per slice, the slice holding R, and within it the token by
+//          block scans of its tied and kept tokens.
 #include "common.h"
 #include "dfssm_kernels.h"
 
 namespace dfssm {
 
-constexpr int kST = 1024;                  // threads per sequence (selection and draw)
-constexpr int kSW = 256;                   // threads per slice workgroup
-constexpr int kMaxSlices = 64;             // slice workgroups per sequence
+constexpr int kSW = 256;          // threads per slice workgroup (and per draw workgroup)
+constexpr int kMaxSlices = 64;    // slice workgroups per sequence
+constexpr int kSliceMin = 512;    // fewer slices for small vocabularies: at least this many tokens each
 
-// Slice workgroups per sequence: at most kMaxSlices, and the partials (maxima, normalizers and
-// 256-bin histograms) must fit the first scratch row of rs = sample_row_floats(V) floats.
-__host__ __device__ inline int sample_slices(int rs) {
-  const int n = (rs * 4 - 1024) / 2048;
+// Slices per sequence: ceil(V / 512), at most 64, so a slice holds at most 1024 tokens (V <= 65536).
+__host__ __device__ inline int sample_slices(int V) {
+  const int n = (V + kSliceMin - 1) / kSliceMin;
   return n < 1 ? 1 : (n > kMaxSlices ? kMaxSlices : n);
 }
-// partials in the first row: maxima (float[NW]) at byte 0, normalizers (u64[NW]) at byte 256,
-// histograms (u64[NW][256]) at byte 1024
-__device__ __forceinline__ float* part_max(float* row0) { return row0; }
-__device__ __forceinline__ unsigned long long* part_z(float* row0) { return (unsigned long long*)((char*)row0 + 256); }
-__device__ __forceinline__ unsigned long long* part_hist(float* row0) {
-  return (unsigned long long*)((char*)row0 + 1024);
+
+// The selection so far: the key prefix of the digits chosen, its mask, and the exact mass of the
+// tokens whose keys rank above the prefix.
+struct Sel {
+  uint32_t prefix, pmask;
+  unsigned long long above;
+};
+
+// The sequence's first scratch row (byte offsets): slice maxima float[64] at 0, the normalizer Z
+// (u64) at 256, the four pass histograms u64[4][256] at 512, the slices' masses above kb u64[64]
+// at 8704, their counts of keys equal to kb int[64] at 9216, and the selections after k digits
+// Sel[k - 1], k = 1..4, at 9472 (9536 bytes; a row has at least 2560 floats). A launch reads the
+// slot the previous one wrote and writes the next: its workgroups never read what it writes.
+struct SampleRow {
+  float* maxs;
+  unsigned long long* Z;
+  unsigned long long* hist;  // [4][256]
+  unsigned long long* mass;
+  int* ties;
+  Sel* sel;  // [4]: after 1, 2, 3, 4 digits
+};
+__device__ __forceinline__ SampleRow sample_row(float* row0) {
+  char* c = (char*)row0;
+  return SampleRow{(float*)c, (unsigned long long*)(c + 256), (unsigned long long*)(c + 512),
+                   (unsigned long long*)(c + 8704), (int*)(c + 9216), (Sel*)(c + 9472)};
 }
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
@@ -80,21 +105,6 @@ __device__ __forceinline__ uint64_t fixed40(float e) {
   return sh >= 0 ? mant << sh : mant >> (-sh);
 }
 
-// Element j of a thread's vector k is token 4 (tid + kST k) + j: every wave-wide access to a
-// scratch row (stride ld floats, a multiple of 4) covers 1 KiB contiguous. A thread holds
-// nv4 = ceil(ld / (4 kST)) vectors; chunks of four are loaded before any is used (vectors past
-// the row re-read its last one; their elements are excluded by index).
-__device__ __forceinline__ void load4(const float* row, int ld, int c, float (&v)[16]) {
-  const int tid = threadIdx.x, last = ld / 4 - 1;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int q = tid + kST * (c + k);
-    const f32x4 x = *(const f32x4*)(row + 4 * (q < last ? q : last));
-    v[4 * k] = x[0]; v[4 * k + 1] = x[1]; v[4 * k + 2] = x[2]; v[4 * k + 3] = x[3];
-  }
-}
-__device__ __forceinline__ int tok_of(int c, int j) { return 4 * ((int)threadIdx.x + kST * (c + j / 4)) + (j & 3); }
-
 template <int NT>
 __device__ __forceinline__ long long block_sum_ll(long long v, long long* red) {
   for (int off = 32; off > 0; off >>= 1) {
@@ -110,317 +120,318 @@ __device__ __forceinline__ long long block_sum_ll(long long v, long long* red) {
   return t;
 }
 
-// PHASE 0: the maximum of z over the slice; PHASE 1: e = exp(z - max z) of the slice to the e row
-// (the last slice also zeroes the padding up to ld), its exact normalizer and first-pass histogram.
-// Slice w of NW: tokens [w SL, min(V, (w + 1) SL)), SL = ceil(V / NW).
-template <int PHASE>
-__global__ __launch_bounds__(kSW) void sample_slice_kernel(SampleArgs a) {
-  __shared__ unsigned long long hist[kSW / 64][256];
+// One radix digit (a 256-thread workgroup; every workgroup of a launch computes the same): from
+// the global histogram `hist` of pass p over the keys matching the selection `r` of passes
+// 0 .. p - 1, with thread t holding bin t, the digit is the largest d >= 1 with
+// r.above + (mass of bins >= d) > thr, else 0; the new mass above is r.above + (mass of bins > d).
+struct SelLds {
+  unsigned long long wtot[kSW / 64];
+  unsigned long long sel;
+  int dsel;
+};
+__device__ Sel select_digit(const unsigned long long* hist, Sel r, int p, unsigned long long thr, SelLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int shift = 24 - 8 * p;
+  const unsigned long long h = hist[tid];
+  unsigned long long incl = h;  // suffix sums: bins >= tid within the wave
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = (uint32_t)__shfl_down((int)(uint32_t)incl, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_down((int)(uint32_t)(incl >> 32), off, 64);
+    if (lane + off < 64) incl += ((unsigned long long)hi << 32) | lo;
+  }
+  if (lane == 0) L.wtot[w] = incl;  // bins 64 w .. 64 w + 63
+  if (tid == 0) L.dsel = 0;
+  __syncthreads();
+  for (int k = w + 1; k < kSW / 64; ++k) incl += L.wtot[k];
+  const unsigned long long in = r.above + incl, ex = in - h;  // bins >= tid, bins > tid
+  if (tid == 0) L.sel = ex;                                   // the d = 0 case
+  __syncthreads();
+  if (tid >= 1 && in > thr && ex <= thr) {                    // at most one such bin
+    L.dsel = tid;
+    L.sel = ex;
+  }
+  __syncthreads();
+  const int d = L.dsel;
+  r.above = L.sel;
+  r.prefix |= (uint32_t)d << shift;
+  r.pmask |= 255u << shift;
+  return r;
+}
+
+// The selection threshold floor(top_p Z); false when every token is kept.
+__device__ __forceinline__ bool selecting(const SampleArgs& a, unsigned long long Z, unsigned long long& thr) {
+  thr = (unsigned long long)((double)a.top_p * (double)Z);
+  return a.top_p < 1.0f && thr < Z;
+}
+
+// The slice of workgroup sw: tokens [lo, hi).
+__device__ __forceinline__ void slice_of(int V, int sw, int& lo, int& hi) {
+  const int NW = sample_slices(V), SL = (V + NW - 1) / NW;
+  lo = sw * SL;
+  hi = lo + SL < V ? lo + SL : V;
+}
+
+// Adds this workgroup's per-wave LDS histograms (every wave has passed a barrier since its last
+// atomic) into the global histogram: the non-zero bins only.
+__device__ __forceinline__ void flush_hist(unsigned long long (&hist)[kSW / 64][256], unsigned long long* g) {
+  const int tid = threadIdx.x;
+  unsigned long long t = 0;
+#pragma unroll
+  for (int k = 0; k < kSW / 64; ++k) t += hist[k][tid];
+  if (t != 0ull) atomicAdd(g + tid, t);
+}
+
+// The maxima of z per slice; slice 0 also clears the sequence's global sums (Z and histograms).
+__global__ __launch_bounds__(kSW) void sample_max_kernel(SampleArgs a) {
   __shared__ float redf[kSW / 64];
-  __shared__ long long redl[kSW / 64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int sw = blockIdx.x, b = blockIdx.y, V = a.V;
-  const int ld = (V + 3) / 4 * 4, rs = sample_row_floats(V);
-  const int NW = sample_slices(rs), SL = (V + NW - 1) / NW;
-  const int lo = sw * SL, hi = lo + SL < V ? lo + SL : V;
+  int lo, hi;
+  slice_of(V, sw, lo, hi);
+  const uint16_t* lg = a.logits + (size_t)b * V;
+  const int* cn = a.counts + (size_t)b * V;
+  const SampleRow R = sample_row(a.escratch + (size_t)b * 2 * sample_row_floats(V));
+  float m = -INFINITY;
+  for (int i = lo + tid; i < hi; i += kSW) m = fmaxf(m, penalized(h2f(lg[i]), cn[i], a));
+  if (sw == 0) {
+    for (int q = tid; q < 4 * 256; q += kSW) R.hist[q] = 0ull;
+    if (tid == 0) *R.Z = 0ull;
+  }
+  const float wm = wave_max_dpp_f32(m);
+  if (lane == 0) redf[w] = wm;
+  __syncthreads();
+  if (tid == 0) {
+    float t = redf[0];
+    for (int k = 1; k < kSW / 64; ++k) t = fmaxf(t, redf[k]);
+    R.maxs[sw] = t;
+  }
+}
+
+// e = exp(z - max z) of the slice to the e row, its exact normalizer and top-byte histogram into
+// the global sums.
+__global__ __launch_bounds__(kSW) void sample_exp_kernel(SampleArgs a) {
+  __shared__ unsigned long long hist[kSW / 64][256];
+  __shared__ long long redl[kSW / 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int sw = blockIdx.x, b = blockIdx.y, V = a.V, NW = sample_slices(V);
+  const int rs = sample_row_floats(V);
+  int lo, hi;
+  slice_of(V, sw, lo, hi);
   const uint16_t* lg = a.logits + (size_t)b * V;
   const int* cn = a.counts + (size_t)b * V;
   float* row0 = a.escratch + (size_t)b * 2 * rs;
   float* er = row0 + rs;
-  if (PHASE == 0) {
-    float m = -INFINITY;
-    for (int i = lo + tid; i < hi; i += kSW) m = fmaxf(m, penalized(h2f(lg[i]), cn[i], a));
-    const float wm = wave_max_dpp_f32(m);
-    if (lane == 0) redf[w] = wm;
-    __syncthreads();
-    if (tid == 0) {
-      float t = redf[0];
-      for (int k = 1; k < kSW / 64; ++k) t = fmaxf(t, redf[k]);
-      part_max(row0)[sw] = t;
-    }
-    return;
+  const SampleRow R = sample_row(row0);
+  __shared__ float mx;
+  if (tid < 64) {  // the slice maxima, all loaded at once (wave 0; NW <= 64)
+    const float wm = wave_max_dpp_f32(tid < NW ? R.maxs[tid] : -INFINITY);
+    if (tid == 0) mx = wm;
   }
   for (int q = tid; q < (kSW / 64) * 256; q += kSW) (&hist[0][0])[q] = 0ull;
-  float m = part_max(row0)[0];
-  for (int k = 1; k < NW; ++k) m = fmaxf(m, part_max(row0)[k]);
   __syncthreads();
-  long long zs = 0;
+  const float m = mx;
+  unsigned long long zs = 0;
   for (int i = lo + tid; i < hi; i += kSW) {
     const float e = dev_expf(penalized(h2f(lg[i]), cn[i], a) - m);
     er[i] = e;
     const unsigned long long E = fixed40(e);
-    zs += (long long)E;
+    zs += E;
     if (E != 0ull) atomicAdd(&hist[w][__builtin_bit_cast(uint32_t, e) >> 24], E);
   }
-  if (sw == NW - 1)
-    for (int i = V + tid; i < ld; i += kSW) er[i] = 0.0f;
-  const long long Zw = block_sum_ll<kSW>(zs, redl);  // (its barriers also publish hist)
-  if (tid == 0) part_z(row0)[sw] = (unsigned long long)Zw;
-  if (tid < 256) {  // 256 bins, one per thread
-    unsigned long long t = 0;
-    for (int k = 0; k < kSW / 64; ++k) t += hist[k][tid];
-    part_hist(row0)[(size_t)sw * 256 + tid] = t;
+  const long long Zw = block_sum_ll<kSW>((long long)zs, redl);  // (its barriers also publish hist)
+  if (tid == 0) atomicAdd(R.Z, (unsigned long long)Zw);
+  flush_hist(hist, R.hist);
+}
+
+// Radix pass p (1..3): the digits of passes 0 .. p - 1, then the histogram of byte p of the
+// slice's keys that match them (skipped when every token is kept).
+__global__ __launch_bounds__(kSW) void sample_pass_kernel(SampleArgs a, int p) {
+  __shared__ unsigned long long hist[kSW / 64][256];
+  __shared__ SelLds sl;
+  const int tid = threadIdx.x, w = tid >> 6;
+  const int sw = blockIdx.x, b = blockIdx.y, V = a.V, rs = sample_row_floats(V);
+  int lo, hi;
+  slice_of(V, sw, lo, hi);
+  float* row0 = a.escratch + (size_t)b * 2 * rs;
+  const float* er = row0 + rs;
+  const SampleRow R = sample_row(row0);
+  float ev[4];  // the slice's e values (at most 1024 tokens), loaded ahead of the selection
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lo + tid + kSW * j;
+    ev[j] = i < hi ? er[i] : 0.0f;
+  }
+  unsigned long long thr;
+  if (!selecting(a, *R.Z, thr)) return;  // uniform over the grid
+  const Sel prev = p > 1 ? R.sel[p - 2] : Sel{0u, 0u, 0ull};
+  for (int q = tid; q < (kSW / 64) * 256; q += kSW) (&hist[0][0])[q] = 0ull;
+  // digit p - 1 (its barriers also publish the cleared hist); the next launch starts from it
+  const Sel s = select_digit(R.hist + 256 * (p - 1), prev, p - 1, thr, sl);
+  if (sw == 0 && tid == 0) R.sel[p - 1] = s;
+  const int shift = 24 - 8 * p;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t key = __builtin_bit_cast(uint32_t, ev[j]);
+    if (lo + tid + kSW * j < hi && (key & s.pmask) == s.prefix) {
+      const unsigned long long E = fixed40(ev[j]);
+      if (E != 0ull) atomicAdd(&hist[w][(key >> shift) & 255u], E);
+    }
+  }
+  __syncthreads();
+  flush_hist(hist, R.hist + 256 * p);
+}
+
+// The boundary key kb from the four histograms (0 when every token is kept); per slice the exact
+// mass of the keys above kb and the count of keys equal to kb.
+__global__ __launch_bounds__(kSW) void sample_mass_kernel(SampleArgs a) {
+  __shared__ SelLds sl;
+  __shared__ long long redl[kSW / 64];
+  const int tid = threadIdx.x;
+  const int sw = blockIdx.x, b = blockIdx.y, V = a.V, rs = sample_row_floats(V);
+  int lo, hi;
+  slice_of(V, sw, lo, hi);
+  float* row0 = a.escratch + (size_t)b * 2 * rs;
+  const float* er = row0 + rs;
+  const SampleRow R = sample_row(row0);
+  float ev[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lo + tid + kSW * j;
+    ev[j] = i < hi ? er[i] : 0.0f;
+  }
+  unsigned long long thr;
+  uint32_t kb = 0;
+  if (selecting(a, *R.Z, thr)) {  // uniform over the grid
+    const Sel s = select_digit(R.hist + 256 * 3, R.sel[2], 3, thr, sl);  // the last digit
+    if (sw == 0 && tid == 0) R.sel[3] = s;                               // the draw starts from it
+    kb = s.prefix;
+  }
+  unsigned long long mg = 0;
+  int nt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t key = __builtin_bit_cast(uint32_t, ev[j]);
+    if (lo + tid + kSW * j < hi) {
+      if (key > kb) mg += fixed40(ev[j]);
+      nt += key == kb ? 1 : 0;
+    }
+  }
+  const long long M = block_sum_ll<kSW>((long long)mg, redl);
+  const long long T = block_sum_ll<kSW>((long long)nt, redl);
+  if (tid == 0) {
+    R.mass[sw] = (unsigned long long)M;
+    R.ties[sw] = (int)T;
   }
 }
 
-__global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
-  __shared__ unsigned long long hist[kST / 64][256];  // one histogram per wave: fewer colliding atomics
-  __shared__ long long redl[kST / 64];
-  __shared__ unsigned long long sel[2];  // mass above the chosen bin (d > 0), (d = 0)
-  __shared__ unsigned long long wtot[4];
-  __shared__ int dsel;
+// Inclusive block scan of 64-bit values over the kSW threads (v < 2^63).
+__device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long v, unsigned long long* red) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int b = blockIdx.x, V = a.V;
-  const int ld = (V + 3) / 4 * 4;
-  const int nv4 = (ld / 4 + kST - 1) / kST;  // vectors per thread
-  const int rs = sample_row_floats(V), NW = sample_slices(rs);
-  float* row0 = a.escratch + (size_t)b * 2 * rs;  // the slices' partials
-  float* er = row0 + rs;                          // e = exp(z - max z)
-  // the exact normalizer, the sum of the slices' (every partial is an integer: any order)
-  __shared__ unsigned long long zsum, hsum[4][256];
-  if (w == 0) {
-    unsigned long long zp = lane < NW ? part_z(row0)[lane] : 0ull;
-    for (int off = 32; off > 0; off >>= 1) {
-      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)zp, off, 64);
-      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(zp >> 32), off, 64);
-      zp += ((unsigned long long)hi << 32) | lo;
-    }
-    if (lane == 0) zsum = zp;
-  }
-  {  // the first pass's histogram: thread t adds bin t % 256 over slices t / 256, + 4, ...
-    unsigned long long hp = 0;
-    for (int k = tid >> 8; k < NW; k += 4) hp += part_hist(row0)[(size_t)k * 256 + (tid & 255)];
-    hsum[tid >> 8][tid & 255] = hp;
-  }
-  __syncthreads();
-  const unsigned long long Z = zsum;
-  const unsigned long long thr = (unsigned long long)((double)a.top_p * (double)Z);
-  uint32_t kb = 0;  // boundary key and last kept index among its ties; all kept: 0 and V
-  int ib = V;
-  if (a.top_p < 1.0f && thr < Z) {
-    uint32_t prefix = 0, pmask = 0;
-    unsigned long long above = 0;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      for (int q = tid; q < (kST / 64) * 256; q += kST) (&hist[0][0])[q] = 0ull;
-      __syncthreads();
-      if (pass == 0 && tid < 256)  // the first pass's histogram: the slices' partials, summed above
-        hist[0][tid] = (hsum[0][tid] + hsum[1][tid]) + (hsum[2][tid] + hsum[3][tid]);
-#pragma unroll 1
-      for (int c = 0; c < (pass == 0 ? 0 : nv4); c += 4) {
-        float v[16];
-        load4(er, ld, c, v);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const uint32_t key = __builtin_bit_cast(uint32_t, v[j]);
-          if (c + j / 4 < nv4 && tok_of(c, j) < V && (key & pmask) == prefix) {  // few match past pass 1
-            const unsigned long long E = fixed40(v[j]);
-            if (E != 0ull) atomicAdd(&hist[w][(key >> shift) & 255u], E);
-          }
-        }
-      }
-      __syncthreads();
-      // the digit d whose bin holds the first token past the mass limit, scanning bins from 255
-      // down: the largest d >= 1 with above + (mass of bins >= d) > thr, else 0; the new mass
-      // above = above + (mass of bins > d). Thread t < 256 holds bin t: the waves' histograms
-      // summed, then suffix sums within each wave (shuffles) and across the four waves (LDS).
-      unsigned long long h = 0, incl = 0;
-      if (tid < 256) {
-        for (int k = 0; k < kST / 64; ++k) h += hist[k][tid];
-        incl = h;
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t lo = (uint32_t)__shfl_down((int)(uint32_t)incl, off, 64);
-          const uint32_t hi = (uint32_t)__shfl_down((int)(uint32_t)(incl >> 32), off, 64);
-          if (lane + off < 64) incl += ((unsigned long long)hi << 32) | lo;
-        }
-        if (lane == 0) wtot[w] = incl;  // bins 64 w .. 64 w + 63
-        if (tid == 0) dsel = 0;
-      }
-      __syncthreads();
-      if (tid < 256) {
-        for (int k = w + 1; k < 4; ++k) incl += wtot[k];
-        const unsigned long long in = above + incl, ex = in - h;  // bins >= tid, bins > tid
-        if (tid == 0) sel[1] = ex;                                // the d = 0 case
-        if (tid >= 1 && in > thr && ex <= thr) {                  // at most one such bin
-          dsel = tid;
-          sel[0] = ex;
-        }
-      }
-      __syncthreads();
-      const int d = dsel;
-      above = d > 0 ? sel[0] : sel[1];
-      prefix |= (uint32_t)d << shift;
-      pmask |= 255u << shift;
-      __syncthreads();  // sel and dsel are rewritten by the next pass
-    }
-    kb = prefix;
-    // the tokens with key kb, in index order, stay while the mass above them is <= thr: all of
-    // them unless more tie than the mass allows; then ib = the index of the nkeep-th of them
-    // (ties are common: fp16 logits take few distinct values). Index order is slab order, then
-    // thread order within a slab: one pass counts each thread's ties per slab, the slab totals
-    // give the slab holding the nkeep-th tie, a scan over that slab's threads the thread, and the
-    // thread its token.
-    const unsigned long long eb = fixed40(__builtin_bit_cast(float, kb));
-    const long long nkeep = eb ? (long long)((thr - above) / eb) + 1 : (long long)V;  // eb > 0 by construction
-    constexpr int kSl = kSampleMaxVocab / (4 * kST);
-    int tcnt[kSl];
-#pragma unroll
-    for (int k = 0; k < kSl; ++k) tcnt[k] = 0;
-#pragma unroll
-    for (int c = 0; c < kSl; c += 4) {
-      if (c < nv4) {
-        float v[16];
-        load4(er, ld, c, v);
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          tcnt[c + j / 4] += (c + j / 4 < nv4 && tok_of(c, j) < V && __builtin_bit_cast(uint32_t, v[j]) == kb) ? 1 : 0;
-      }
-    }
-    __shared__ int slab_ties[kST / 64][kSl];
-    __shared__ int tie_pick[2];  // slab, rank of the wanted tie within it (1-based)
-#pragma unroll
-    for (int k = 0; k < kSl; ++k) {
-      const int ws = wave_sum_dpp_i32(tcnt[k]);
-      if (lane == 0) slab_ties[w][k] = ws;
-    }
-    __shared__ int slab_tot[kSl];
-    __syncthreads();
-    if (tid < kSl) {
-      int t = 0;
-      for (int q = 0; q < kST / 64; ++q) t += slab_ties[q][tid];
-      slab_tot[tid] = t;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      long long cum = 0;
-      int ks = -1;
-      long long rank = 0;
-      for (int k = 0; k < kSl && ks < 0; ++k) {
-        if (cum + slab_tot[k] >= nkeep) {
-          ks = k;
-          rank = nkeep - cum;
-        }
-        cum += slab_tot[k];
-      }
-      tie_pick[0] = ks;  // -1: no more ties than nkeep, every tie is kept
-      tie_pick[1] = (int)rank;
-    }
-    __syncthreads();
-    const int ks = tie_pick[0], rank = tie_pick[1];
-    if (ks >= 0) {  // exclusive scan of the threads' ties in slab ks (thread order = index order)
-      int mine = 0;
-#pragma unroll
-      for (int k = 0; k < kSl; ++k)
-        if (k == ks) mine = tcnt[k];
-      int incl = mine;
-      for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += t;
-      }
-      if (lane == 63) slab_ties[w][0] = incl;
-      __syncthreads();
-      int base = 0;
-      for (int q = 0; q < w; ++q) base += slab_ties[q][0];
-      const int excl = base + incl - mine;
-      if (mine > 0 && excl < rank && rank <= excl + mine) {  // exactly one thread
-        const int q = tid + kST * ks, last = ld / 4 - 1;
-        const f32x4 x = *(const f32x4*)(er + 4 * (q < last ? q : last));
-        int seen = excl;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float xt = x[t];  // through a scalar (see the draw below)
-          if (4 * q + t < V && __builtin_bit_cast(uint32_t, xt) == kb && ++seen == rank) tie_pick[1] = -(4 * q + t) - 1;
-        }
-      }
-      __syncthreads();
-      ib = -tie_pick[1] - 1;
-    }
-  }
-  // inverse-CDF draw in index order (slab k = tokens 4096 k .. 4096 k + 4095, then thread, then
-  // element): kept mass per slab (exact in fp64: slab sums < 2^53), the slab, the thread by a
-  // scan of the slab's per-thread masses, the token within the thread
-  constexpr int kSlabs = kSampleMaxVocab / (4 * kST);
-  __shared__ double slab_w[kST / 64][kSlabs];
-  __shared__ unsigned long long slab_t[kSlabs];
-  __shared__ int pick[2];  // slab, thread
-  __shared__ unsigned long long rem_s;
-  double slab[kSlabs];
-#pragma unroll
-  for (int k = 0; k < kSlabs; ++k) slab[k] = 0.0;
-#pragma unroll
-  for (int c = 0; c < kSlabs; c += 4) {
-    if (c < nv4) {
-      float v[16];
-      load4(er, ld, c, v);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int i = tok_of(c, j);
-        const uint32_t key = __builtin_bit_cast(uint32_t, v[j]);
-        if (c + j / 4 < nv4 && i < V && (key > kb || (key == kb && i <= ib))) slab[c + j / 4] += (double)fixed40(v[j]);
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < kSlabs; ++k) {
-    const double ws = wave_sum_dpp_f64(slab[k]);
-    if (lane == 0) slab_w[w][k] = ws;
-  }
-  __syncthreads();
-  if (tid < kSlabs) {
-    double t = 0.0;
-    for (int k = 0; k < kST / 64; ++k) t += slab_w[k][tid];
-    slab_t[tid] = (unsigned long long)t;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    unsigned long long S = 0;
-    for (int k = 0; k < kSlabs; ++k) S += slab_t[k];
-    const uint64_t h = splitmix64(a.seed ^ (((uint64_t)b << 40) | ((uint64_t)(a.step[b] & 0x7fffffu) << 17) | 0x1ffffull));
-    unsigned long long R = __umul64hi(h, S);  // uniform in [0, S)
-    int k = 0;
-    while (k < kSlabs - 1 && R >= slab_t[k]) R -= slab_t[k++];
-    pick[0] = k;
-    rem_s = R;
-  }
-  __syncthreads();
-  const int ks = pick[0];
-  // this thread's kept masses in slab ks, and the exclusive scan over the threads
-  unsigned long long em[4];
-  unsigned long long mine = 0;
-  {
-    const int q = tid + kST * ks, last = ld / 4 - 1;
-    const f32x4 x = *(const f32x4*)(er + 4 * (q < last ? q : last));
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = 4 * q + t;
-      // through a scalar: hipcc 7.2 bit-casts an element of an ext_vector_type as element 0
-      const float xt = x[t];
-      const uint32_t key = __builtin_bit_cast(uint32_t, xt);
-      em[t] = (ks < nv4 && i < V && (key > kb || (key == kb && i <= ib))) ? fixed40(xt) : 0ull;
-      mine += em[t];
-    }
-  }
-  double incl = (double)mine;  // < 2^53: exact
   for (int off = 1; off < 64; off <<= 1) {
-    const double t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), off, 64);
+    if (lane >= off) v += ((unsigned long long)hi << 32) | lo;
   }
-  if (lane == 63) slab_w[w][0] = incl;
   __syncthreads();
-  double wbase = 0.0;
-  for (int k = 0; k < w; ++k) wbase += slab_w[k][0];
-  const unsigned long long excl = (unsigned long long)(wbase + incl) - mine;
-  const unsigned long long R = rem_s;
-  if (mine > 0 && excl <= R && R < excl + mine) {  // exactly one thread
-    unsigned long long acc = excl;
-    int tok = 4 * (tid + kST * ks);
+  if (lane == 63) red[w] = v;
+  __syncthreads();
+  for (int k = 0; k < w; ++k) v += red[k];
+  return v;
+}
+
+// One workgroup per sequence: ties kept per slice, kept masses, the slice holding R and the token.
+__global__ __launch_bounds__(kSW) void sample_draw_kernel(SampleArgs a) {
+  __shared__ unsigned long long red[kSW / 64];
+  __shared__ unsigned long long pick_r;
+  __shared__ int pick_s, pick_kt;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int b = blockIdx.x, V = a.V, NW = sample_slices(V), rs = sample_row_floats(V);
+  float* row0 = a.escratch + (size_t)b * 2 * rs;
+  const float* er = row0 + rs;
+  const SampleRow R = sample_row(row0);
+  const unsigned long long mass = tid < NW ? R.mass[tid] : 0ull;
+  const int ties = tid < NW ? R.ties[tid] : 0;
+  unsigned long long thr;
+  uint32_t kb = 0;
+  long long nkeep = (long long)V;  // ties kept in index order (all when every token is kept)
+  if (selecting(a, *R.Z, thr)) {
+    const Sel s = R.sel[3];  // after all four digits
+    kb = s.prefix;
+    const unsigned long long eb = fixed40(__builtin_bit_cast(float, kb));  // > 0 by construction
+    nkeep = eb ? (long long)((thr - s.above) / eb) + 1 : (long long)V;
+  }
+  const unsigned long long eb = fixed40(__builtin_bit_cast(float, kb));
+  if (tid < 64) {  // wave 0: slice lanes (NW <= 64)
+    if (tid == 0) {  // (overwritten below by the one picking lane, later in the same wave)
+      pick_s = 0;
+      pick_r = 0ull;
+      pick_kt = 0;
+    }
+    int tin = ties;  // ties in slices <= lane
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(tin, off, 64);
+      if (lane >= off) tin += t;
+    }
+    const long long before = tin - ties;
+    long long kt = nkeep - before;
+    kt = kt < 0 ? 0 : (kt > ties ? ties : kt);
+    const unsigned long long kept = mass + eb * (unsigned long long)kt;
+    unsigned long long incl = kept;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)incl, off, 64);
+      const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(incl >> 32), off, 64);
+      if (lane >= off) incl += ((unsigned long long)hi << 32) | lo;
+    }
+    const unsigned long long S = ((unsigned long long)(uint32_t)__shfl((int)(uint32_t)(incl >> 32), 63, 64) << 32) |
+                                 (uint32_t)__shfl((int)(uint32_t)incl, 63, 64);
+    const uint64_t h = splitmix64(a.seed ^ (((uint64_t)b << 40) | ((uint64_t)(a.step[b] & 0x7fffffu) << 17) | 0x1ffffull));
+    const unsigned long long Rd = __umul64hi(h, S);  // uniform in [0, S)
+    const unsigned long long ex = incl - kept;
+    if (lane < NW && ex <= Rd && Rd < incl) {  // exactly one slice
+      pick_s = lane;
+      pick_r = Rd - ex;
+      pick_kt = (int)kt;
+    }
+  }
+  __syncthreads();
+  const int ps = pick_s, kt = pick_kt;
+  const unsigned long long Rr = pick_r;
+  int lo, hi;
+  slice_of(V, ps, lo, hi);
+  // thread t owns tokens lo + 4 t .. lo + 4 t + 3 of the slice (index order = thread order)
+  float ev[4];
+  int ntie = 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {  // the first token whose cumulative mass exceeds R
-      if (R < acc + em[t]) {
-        tok = 4 * (tid + kST * ks) + t;
+  for (int j = 0; j < 4; ++j) {
+    const int i = lo + 4 * tid + j;
+    ev[j] = i < hi ? er[i] : 0.0f;
+    ntie += (i < hi && __builtin_bit_cast(uint32_t, ev[j]) == kb) ? 1 : 0;
+  }
+  const int trank = (int)(block_scan_u64((unsigned long long)ntie, red) - (unsigned long long)ntie);  // ties before
+  unsigned long long em[4], mine = 0;
+  {
+    int r = trank;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = lo + 4 * tid + j;
+      const uint32_t key = __builtin_bit_cast(uint32_t, ev[j]);
+      bool keep = i < hi && key > kb;
+      if (i < hi && key == kb) keep = r++ < kt;
+      em[j] = keep ? fixed40(ev[j]) : 0ull;
+      mine += em[j];
+    }
+  }
+  const unsigned long long incl = block_scan_u64(mine, red), excl = incl - mine;
+  if (mine > 0 && excl <= Rr && Rr < incl) {  // exactly one thread
+    unsigned long long acc = excl;
+    int tok = lo + 4 * tid;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // the first token whose cumulative mass exceeds R
+      if (Rr < acc + em[j]) {
+        tok = lo + 4 * tid + j;
         break;
       }
-      acc += em[t];
+      acc += em[j];
     }
     a.next[b] = tok;
     a.counts[(size_t)b * V + tok] += 1;
@@ -430,10 +441,12 @@ __global__ __launch_bounds__(kST) void sample_kernel(SampleArgs a) {
 
 hipError_t launch_sample(const SampleArgs& a, int batch, hipStream_t s) {
   if (a.V < 1 || a.V > kSampleMaxVocab) return hipErrorInvalidValue;
-  const int NW = sample_slices(sample_row_floats(a.V));
-  hipLaunchKernelGGL(sample_slice_kernel<0>, dim3(NW, batch), dim3(kSW), 0, s, a);
-  hipLaunchKernelGGL(sample_slice_kernel<1>, dim3(NW, batch), dim3(kSW), 0, s, a);
-  hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kST), 0, s, a);
+  const dim3 g(sample_slices(a.V), batch);
+  hipLaunchKernelGGL(sample_max_kernel, g, dim3(kSW), 0, s, a);
+  hipLaunchKernelGGL(sample_exp_kernel, g, dim3(kSW), 0, s, a);
+  for (int p = 1; p < 4; ++p) hipLaunchKernelGGL(sample_pass_kernel, g, dim3(kSW), 0, s, a, p);
+  hipLaunchKernelGGL(sample_mass_kernel, g, dim3(kSW), 0, s, a);
+  hipLaunchKernelGGL(sample_draw_kernel, dim3(batch), dim3(kSW), 0, s, a);
   return hipGetLastError();
 }
 
