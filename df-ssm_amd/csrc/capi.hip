@@ -151,7 +151,7 @@ const char* dfssm_error_string(int code) {
 
 int dfssm_check_dims(const dfssm_dims* d) {
   if (!d) return DFSSM_E_NULL;
-  if (d->n_layer <= 0 || d->vocab_size <= 0 || d->nheads <= 0) return DFSSM_E_DIMS;
+  if (d->n_layer <= 0 || d->vocab_size <= 0 || d->vocab_size > 65536 || d->nheads <= 0) return DFSSM_E_DIMS;
   if (!kdim_ok(d->d_model) || !kdim_ok(d->d_inner)) return DFSSM_E_DIMS;
   if (d->d_state != 128 || d->ngroups != 1 || (d->emb_code != 0 && d->emb_code != 1)) return DFSSM_E_DIMS;
   if (d->d_inner % d->nheads) return DFSSM_E_DIMS;

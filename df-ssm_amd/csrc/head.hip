@@ -16,6 +16,11 @@
 
 namespace dfssm {
 
+// Vocabulary limit of the heads: at most 1024 table groups of 64 rows (V <= 65536), so that the
+// last workgroup's argmax holds every per-workgroup pair in registers; k slices of 512 per row.
+constexpr int kHeadMaxGroups = 1024;
+constexpr int kHeadMaxKP = 10;  // D <= 5120
+
 // Element j of a 16-byte table chunk, widened: 16 int8 or 8 fp16 per chunk.
 template <bool F16>
 __device__ __forceinline__ double emb_elem(const u32x4& e4, int j) {
@@ -27,6 +32,93 @@ template <bool F16>
 __device__ __forceinline__ uint16_t emb_value(const uint8_t* emb, const uint16_t* scale, int CH, int tg, int tl, int k) {
   if (F16) return ((const uint16_t*)(emb + (((size_t)tg * CH + (k >> 3)) * 64 + tl) * 16))[k & 7];
   return f2h((float)(int8_t)emb[(((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16 + (k & 15)] * h2f(scale[tg * 64 + tl]));
+}
+
+// The last workgroup's argmax over the NG per-workgroup (max, first index) pairs of every row
+// (part_val/part_idx, row-major by row): wave w takes rows w + NWV (r0 + r), r < RW, and every
+// lane loads all its pairs of all those rows (at most K each, clamped in-bounds addresses) before
+// comparing any, so the reduction costs one memory round trip. Writes a.next and toks.
+template <int NWV, int RW, int K>
+__device__ __forceinline__ void argmax_pairs(const HeadArgs& a, int M, int NG, int* toks, int r0 = 0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float pv[RW][K];
+  int pi[RW][K];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int m = wave + NWV * (r0 + r) < M ? wave + NWV * (r0 + r) : M - 1;
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+      const int j = lane + 64 * q < NG ? lane + 64 * q : NG - 1;
+      pv[r][q] = __hip_atomic_load(a.part_val + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pi[r][q] = __hip_atomic_load(a.part_idx + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int m = wave + NWV * (r0 + r);
+    float b = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < K; ++q)
+      if (lane + 64 * q < NG && (pv[r][q] > b || (pv[r][q] == b && pi[r][q] < bi))) {
+        b = pv[r][q];
+        bi = pi[r][q];
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(b, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    }
+    if (lane == 0 && m < M) {
+      // no comparable logit (all NaN): report token 0 rather than an index outside the table
+      if (bi < 0 || bi >= a.V) bi = 0;
+      a.next[m] = (int64_t)bi;
+      toks[m] = bi;
+    }
+  }
+}
+
+// x_next[m] = the embedding of token toks[m], m < M, by NT threads in 16-byte table chunks (16
+// int8 or 8 fp16 values), KB chunks per thread loaded before any is converted and stored.
+template <bool F16, int NT>
+__device__ __forceinline__ void embed_next(const HeadArgs& a, const int* toks, int M, int D) {
+  constexpr int KB = 8;
+  const int CH = F16 ? D / 8 : D / 16, n = M * CH;
+  for (int c0 = (int)threadIdx.x; c0 < n; c0 += NT * KB) {
+    u32x4 ch[KB];
+    uint16_t sc[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int c = c0 + NT * i < n ? c0 + NT * i : n - 1;
+      const int m = c / CH, k = c - m * CH, t = toks[m];
+      ch[i] = *(const u32x4*)(a.emb + (((size_t)(t >> 6) * CH + k) * 64 + (t & 63)) * 16);
+      sc[i] = F16 ? (uint16_t)0 : a.emb_scale[t];
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int c = c0 + NT * i;
+      if (c < n) {
+        const int m = c / CH, k = c - m * CH;
+        if (F16) {
+          *(u32x4*)(a.x_next + (size_t)m * D + 8 * k) = ch[i];
+        } else {
+          const float sv = h2f(sc[i]);
+          uint32_t o[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = ch[i][e >> 1];
+            const int sh = 16 * (e & 1);
+            const float v0 = (float)(int8_t)(w >> sh) * sv, v1 = (float)(int8_t)(w >> (sh + 8)) * sv;
+            o[e] = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+          }
+          u32x4* dst = (u32x4*)(a.x_next + (size_t)m * D + 16 * k);
+          dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+          dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+        }
+      }
+    }
+  }
 }
 
 template <int M, bool F16>
@@ -117,36 +209,10 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
   if (!is_last) return;
   __threadfence();
   __shared__ int next_tok[M];
-  if (wave < M) {
-    const int m = wave;
-    float best = -INFINITY;
-    int bidx = 0x7fffffff;
-    for (int j = lane; j < (int)gridDim.x; j += 64) {
-      const float vv = __hip_atomic_load(a.part_val + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (vv > best || (vv == best && ii < bidx)) { best = vv; bidx = ii; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(bidx, o, 64);
-      if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
-    }
-    if (lane == 0) {
-      // no comparable logit (all NaN): report token 0 rather than an index outside the table
-      if (bidx < 0 || bidx >= a.V) bidx = 0;
-      a.next[m] = (int64_t)bidx;
-      next_tok[m] = bidx;
-    }
-  }
+  argmax_pairs<4, 1, kHeadMaxGroups / 64>(a, M, (int)gridDim.x, next_tok);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) {
-    for (int m = 0; m < M; ++m) {
-      const int t = next_tok[m];
-      for (int k = tid; k < D; k += 256) a.x_next[(size_t)m * D + k] = emb_value<F16>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
-    }
-  }
+  if (a.x_next) embed_next<F16, 256>(a, next_tok, M, D);
 }
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
@@ -311,10 +377,15 @@ __global__ __launch_bounds__(256) void head_i8_kernel(HeadArgs a) {
   int bidx = 0x7fffffff;
   const int v = g * 64 + row;
   if (jg < M && v < a.V) {
+    long long tp[kHeadMaxKP];  // all slices' partials loaded before any is added
+#pragma unroll
+    for (int q = 0; q < kHeadMaxKP; ++q)
+      tp[q] = __hip_atomic_load(a.hpart + (((size_t)g * KP + (q < KP ? q : KP - 1)) * M + jg) * 64 + row,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     long long T = 0;
-    for (int q = 0; q < KP; ++q)
-      T += __hip_atomic_load(a.hpart + (((size_t)g * KP + q) * M + jg) * 64 + row, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int q = 0; q < kHeadMaxKP; ++q)
+      if (q < KP) T += tp[q];
     const uint16_t lh = f2h((float)((double)T * 0x1p-24) * h2f(a.emb_scale[v]));
     if (a.logits) a.logits[(size_t)jg * a.V + v] = lh;
     best = h2f(lh);
@@ -346,35 +417,10 @@ __global__ __launch_bounds__(256) void head_i8_kernel(HeadArgs a) {
   __syncthreads();
   if (!is_last) return;
   __shared__ int next_tok[M];
-  if (wave < M) {
-    const int m = wave;
-    float b = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int j = lane; j < NG; j += 64) {
-      const float vv = __hip_atomic_load(a.part_val + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * NG + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(b, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
-    }
-    if (lane == 0) {
-      if (bi < 0 || bi >= a.V) bi = 0;  // no comparable logit (all NaN): token 0
-      a.next[m] = (int64_t)bi;
-      next_tok[m] = bi;
-    }
-  }
+  argmax_pairs<4, 1, kHeadMaxGroups / 64>(a, M, NG, next_tok);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) {
-    for (int m = 0; m < M; ++m) {
-      const int t = next_tok[m];
-      for (int k = tid; k < D; k += 256) a.x_next[(size_t)m * D + k] = emb_value<false>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
-    }
-  }
+  if (a.x_next) embed_next<false, 256>(a, next_tok, M, D);
 }
 
 template <int M>
@@ -396,7 +442,7 @@ static hipError_t launch_head_mf(const HeadArgs& a, int groups, size_t shm, hipS
 
 hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
   const int groups = (a.V + 63) / 64;
-  if (M < 1 || M > 4) return hipErrorInvalidValue;
+  if (M < 1 || M > 4 || groups > kHeadMaxGroups || a.D > 512 * kHeadMaxKP) return hipErrorInvalidValue;
   if (!a.f16) {
     switch (M) {
       case 1: return launch_head_i8<1>(a, groups, s);
@@ -678,34 +724,10 @@ __global__ __launch_bounds__(128 * NH * KP) __attribute__((amdgpu_waves_per_eu(2
   if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(NGW - 1);
   __syncthreads();
   if (!is_last) return;
-  for (int m = wave; m < M; m += NWP * KP) {
-    float b = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int j = lane; j < NGW; j += 64) {
-      const float vv = __hip_atomic_load(a.part_val + (size_t)m * NGW + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * NGW + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(b, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
-    }
-    if (lane == 0) {
-      if (bi < 0 || bi >= a.V) bi = 0;  // no comparable logit (all NaN): token 0
-      a.next[m] = (int64_t)bi;
-      next_tok[m] = bi;
-    }
-  }
+  argmax_pairs<NWP * KP, (MP + NWP * KP - 1) / (NWP * KP), kHeadMaxGroups / 128>(a, M, NGW, next_tok);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) {
-    for (int m = 0; m < M; ++m) {
-      const int t = next_tok[m];
-      for (int k = tid; k < D; k += 128 * NH * KP) a.x_next[(size_t)m * D + k] = emb_value<false>(a.emb, a.emb_scale, CH, t >> 6, t & 63, k);
-    }
-  }
+  if (a.x_next) embed_next<false, 128 * NH * KP>(a, next_tok, M, D);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -863,38 +885,15 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
   __syncthreads();
   if (!is_last) return;
   __threadfence();
-  for (int m = wave; m < M; m += 4) {
-    float b = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int j = lane; j < (int)gridDim.x; j += 64) {
-      const float vv = __hip_atomic_load(a.part_val + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int ii = __hip_atomic_load(a.part_idx + (size_t)m * gridDim.x + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (vv > b || (vv == b && ii < bi)) { b = vv; bi = ii; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(b, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
-    }
-    if (lane == 0) {
-      if (bi < 0 || bi >= a.V) bi = 0;
-      a.next[m] = (int64_t)bi;
-      next_tok[m] = bi;
-    }
-  }
+  for (int r0 = 0; r0 < MI * 4; r0 += 4)  // four rows per wave at a time (registers)
+    argmax_pairs<4, 4, kHeadMaxGroups / 256>(a, M, (int)gridDim.x, next_tok, r0);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) {
-    for (int m = 0; m < M; ++m) {
-      const int tk = next_tok[m];
-      for (int k = tid; k < D; k += kHT) a.x_next[(size_t)m * D + k] = emb_value<F16>(a.emb, a.emb_scale, CH, tk >> 6, tk & 63, k);
-    }
-  }
+  if (a.x_next) embed_next<F16, kHT>(a, next_tok, M, D);
 }
 
 hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s) {
-  if (M < 1 || M > 64 || a.D % kHK) return hipErrorInvalidValue;
+  if (M < 1 || M > 64 || a.D % kHK || (a.V + 63) / 64 > kHeadMaxGroups) return hipErrorInvalidValue;
   if (!a.f16) {  // int8 table: exact digit-plane GEMM
     if (!a.hdig) return hipErrorInvalidValue;
     const int nh = (M + 15) / 16;

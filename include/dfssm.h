@@ -14,7 +14,7 @@
  *
  * Model-specific constraints (checked by dfssm_check_dims): d_state = 128, ngroups = 1,
  * LoRA rank 16, d_conv = 4, P = d_inner / nheads a multiple of 16, d_model and d_inner multiples
- * of 512 and at most 5120, nheads a multiple of 8, batch 1..64.
+ * of 512 and at most 5120, nheads a multiple of 8, vocab_size at most 65536, batch 1..64.
  */
 #ifndef DFSSM_H
 #define DFSSM_H

@@ -41,7 +41,8 @@ def _dims(**kw):
 @pytest.mark.parametrize("kw,rc", [({}, 0), ({"batch": 4}, 0), ({"batch": 5}, 0), ({"batch": 64}, 0), ({"batch": 65}, -3), ({"batch": 0}, -3),
                                    ({"d_state": 64}, -2), ({"ngroups": 2}, -2), ({"d_model": 2000}, -2),
                                    ({"emb_code": 0}, 0), ({"emb_code": 2}, -2), ({"nheads": 60}, -2),
-                                   ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 0)])
+                                   ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 0),
+                                   ({"vocab_size": 65536}, 0), ({"vocab_size": 65537}, -2)])
 def test_check_dims(kw, rc):
     assert _C.lib().dfssm_check_dims(_dims(**kw)) == rc
 
