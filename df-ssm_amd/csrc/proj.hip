@@ -162,6 +162,143 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
   }
 }
 
+// prep_rows_kernel: the same prologue for many rows (the prompt prefill runs thousands), one
+// workgroup of K/8 threads per kPrepRows consecutive rows. The norm weights and the fp16 LoRA-B
+// values of a thread's 8 columns (16 ranks) stay in registers across the rows, and each row's
+// RMSNorm, quantizer and 16 LoRA intermediates are computed once (prep_kernel's 16 workgroups per
+// row each recompute the norm). The thread -> column map, the per-thread order of the fp64 sums
+// and the reduction trees are prep_kernel's, so every output is identical. Writes q_out, xs_out,
+// h_out and s_out; the decode-only outputs (planes_out, xn_out, xs16_out) are not supported.
+constexpr int kPrepRows = 16;
+constexpr int kPrepRowsT = kMaxK / 8;  // threads per workgroup at most
+
+template <int MODE>
+__global__ __launch_bounds__(kPrepRowsT) void prep_rows_kernel(PrepArgs a, int M) {
+  __shared__ double red_d[kPrepRowsT / 64];
+  __shared__ double red_h[kPrepRowsT / 64][DFSSM_LORA_R];
+  __shared__ float red_f[kPrepRowsT / 64];
+  __shared__ int red_i[kPrepRowsT / 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int K = a.K, nw = (int)blockDim.x >> 6;
+  const int m0 = (int)blockIdx.x * kPrepRows, m1 = m0 + kPrepRows < M ? m0 + kPrepRows : M;
+  const bool want_sum = a.s_out != nullptr;
+  // this row's activations (and its sum-of-squares slot) are loaded one row ahead
+  auto load_row = [&](int m, u32x4& av, double& slot) {
+    const int mm = m < m1 ? m : m1 - 1;
+    av = *(const u32x4*)(a.act + (size_t)mm * a.ld_act + 8 * tid);
+    if (MODE == DFSSM_MODE_OUT) slot = a.sumsq_slots[(size_t)mm * a.n_slots + (tid < a.n_slots ? tid : a.n_slots - 1)];
+  };
+  u32x4 av;
+  double slot = 0.0;
+  load_row(m0, av, slot);
+  const f32x4 w0 = *(const f32x4*)(a.norm_w + 8 * tid);
+  const f32x4 w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
+  const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+  // fp16(B_i8 * B_s) of the 8 columns for every rank, as fp16 pairs (prep_kernel's b0, b1)
+  uint32_t bp[DFSSM_LORA_R][4];
+#pragma unroll
+  for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
+    uint2 b8 = {0u, 0u};
+    float bs = 0.0f;
+    if (a.lB) {
+      b8 = *(const uint2*)(a.lB + (size_t)rr * K + 8 * tid);
+      bs = h2f(a.lBs[rr]);
+    }
+    const uint32_t bw[2] = {b8.x, b8.y};
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float b0 = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
+      const float b1 = r16((float)(int8_t)(bw[(e + 1) >> 2] >> (8 * ((e + 1) & 3))) * bs);
+      bp[rr][e >> 1] = (uint32_t)f2h(b0) | ((uint32_t)f2h(b1) << 16);
+    }
+  }
+  for (int m = m0; m < m1; ++m) {
+    // opaque per row: keeps the 128 conversions of bp to fp32 inside the loop (hoisted, they
+    // would not fit the registers)
+#pragma unroll
+    for (int rr = 0; rr < DFSSM_LORA_R; ++rr)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(bp[rr][j]));
+    const u32x4 cur = av;
+    const double cslot = slot;
+    if (m + 1 < m1) load_row(m + 1, av, slot);
+    double part = 0.0;
+    if (MODE == DFSSM_MODE_IN) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double xv = (double)h2f((uint16_t)(cur[e >> 1] >> (16 * (e & 1))));
+        part += xv * xv;
+      }
+    } else {
+      part = tid < a.n_slots ? cslot : 0.0;
+    }
+    {
+      const double pw = wave_sum_dpp_f64(part);
+      if (lane == 0) red_d[w] = pw;
+    }
+    lds_barrier();
+    double ss = 0.0;
+    for (int i = 0; i < nw; ++i) ss += red_d[i];
+    const float var = (float)ss * (1.0f / (float)K);
+    const float r = 1.0f / sqrt_rn(var + 1e-5f);
+    float xn[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      xn[e] = r16((h2f((uint16_t)(cur[e >> 1])) * r) * wv[e]);
+      xn[e + 1] = r16((h2f((uint16_t)(cur[e >> 1] >> 16)) * r) * wv[e + 1]);
+      mx = fmaxf(mx, fmaxf(fabsf(xn[e]), fabsf(xn[e + 1])));
+    }
+    {
+      const float mw = wave_max_dpp_f32(mx);
+      if (lane == 0) red_f[w] = mw;
+    }
+#pragma unroll
+    for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {  // one rank at a time: columns in order, as prep_kernel
+      double hacc = 0.0;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {  // fp16 x fp16 is exact in fp32
+        hacc += (double)(xn[e] * h2f((uint16_t)bp[rr][e >> 1]));
+        hacc += (double)(xn[e + 1] * h2f((uint16_t)(bp[rr][e >> 1] >> 16)));
+      }
+      const double hw = wave_sum_dpp_f64(hacc);
+      if (lane == 0) red_h[w][rr] = hw;
+    }
+    lds_barrier();  // (every wave has also read red_d: the next row may rewrite it)
+    float amax = red_f[0];
+    for (int i = 0; i < nw; ++i) amax = fmaxf(amax, red_f[i]);
+    if (a.lB && tid < DFSSM_LORA_R) {
+      double ht = 0.0;
+      for (int i = 0; i < nw; ++i) ht += red_h[i][tid];
+      a.h_out[(size_t)m * DFSSM_LORA_R + tid] = r16((float)ht);
+    }
+    const float xs = quant_scale(amax);
+    const float rinv = quant_rcp(xs);
+    uint32_t qw[2] = {0u, 0u};
+    int qsum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int q = quant_i8(xn[e], rinv);
+      qsum += q;
+      qw[e >> 2] |= (uint32_t)(q & 0xff) << (8 * (e & 3));
+    }
+    if (a.q_out) *(uint2*)(a.q_out + (size_t)m * a.ld_q + 8 * tid) = uint2{qw[0], qw[1]};
+    int S = 0;
+    if (want_sum) {  // uniform
+      const int qs = wave_sum_dpp_i32(qsum);
+      if (lane == 0) red_i[w] = qs;
+      lds_barrier();
+      for (int i = 0; i < nw; ++i) S += red_i[i];
+    }
+    if (tid == 0) {
+      if (a.s_out) a.s_out[m] = S;
+      if (a.xs_out) a.xs_out[m] = xs;
+    }
+    // red_f and red_h are rewritten only after the next row's first barrier, red_i after its
+    // second: every wave has read them by then
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // proj_kernel: 1-bit scaffold GEMV for M <= 4 activation rows + fused epilogue.
 // One workgroup (1024 threads, 16 waves) owns 64 output rows; lane l of every wave owns row
@@ -466,6 +603,14 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
   if (mode == DFSSM_MODE_OUT && (!a.sumsq_slots || a.n_slots < 1 || a.n_slots > a.K / 8)) return hipErrorInvalidValue;
   if (a.lB && !a.lBs) return hipErrorInvalidValue;
   if (a.K > kMaxK || a.K % 512) return hipErrorInvalidValue;  // K / 8 threads: whole waves
+  if (M > 64 && !a.planes_out && !a.xn_out && !a.xs16_out && (a.h_out || !a.lB)) {  // many rows: one pass each
+    const dim3 g((M + kPrepRows - 1) / kPrepRows);
+    if (mode == DFSSM_MODE_IN)
+      hipLaunchKernelGGL(prep_rows_kernel<DFSSM_MODE_IN>, g, dim3(a.K / 8), 0, s, a, M);
+    else
+      hipLaunchKernelGGL(prep_rows_kernel<DFSSM_MODE_OUT>, g, dim3(a.K / 8), 0, s, a, M);
+    return hipGetLastError();
+  }
   if (mode == DFSSM_MODE_IN)
     hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
   else
