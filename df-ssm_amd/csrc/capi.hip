@@ -85,8 +85,11 @@ WsLayout ws_layout(const dfssm_dims* d) {
 // residual stream of every row, the projection rows, g, the sum(g^2) slots and the prologue
 // outputs (q, scale, LoRA intermediate).
 struct PfLayout {
-  size_t x, proj, g, slots, q, xs, h, total;
+  size_t x, proj, g, slots, q, xs, h, w8, total;
 };
+// Prefill chunks of at least this many rows run the projections on the wide GEMM (weights
+// expanded to int8 in the prefill workspace), smaller ones on gemm_kernel.
+constexpr int kWideGemmRows = 256;
 
 PfLayout pf_layout(const Derived& r, int rows) {
   PfLayout w;
@@ -96,9 +99,14 @@ PfLayout pf_layout(const Derived& r, int rows) {
   w.proj = off;  off = align_up(off + (size_t)rows * r.IPO * 2);
   w.g = off;     off = align_up(off + (size_t)rows * r.DI * 2);
   w.slots = off; off = align_up(off + (size_t)rows * r.n_slots * 8);
-  w.q = off;     off = align_up(off + (size_t)rows * kq);
+  w.q = off;     off = align_up(off + (size_t)(rows + 15) / 16 * 16 * kq);  // rows padded to 16 (tiled)
   w.xs = off;    off = align_up(off + (size_t)rows * 4);
   w.h = off;     off = align_up(off + (size_t)rows * 16 * 4);
+  w.w8 = off;
+  if (rows >= kWideGemmRows) {  // the larger projection's expanded weights
+    const size_t a = gemm_wide_w8_bytes(r.IPO, r.D), b = gemm_wide_w8_bytes(r.D, r.DI);
+    off = align_up(off + (a > b ? a : b));
+  }
   w.total = off;
   return w;
 }
@@ -696,6 +704,7 @@ static int prefill_chunk(const dfssm_model* model, const int64_t* tokens, int n_
       p.xs_out = (float*)(pw + w.xs);
       p.h_out = (float*)(pw + w.h);
       p.K = in ? r.D : r.DI;
+      p.q_tiled = R >= kWideGemmRows;  // the wide GEMM reads q tiled
       st = launch_prep(p, R, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s);
       if (st != hipSuccess) return hip_status(st);
       GemmArgs a{};
@@ -711,7 +720,8 @@ static int prefill_chunk(const dfssm_model* model, const int64_t* tokens, int n_
         a.out = xr; a.ld_out = r.D;
         a.N = r.D; a.K = r.DI;
       }
-      st = launch_gemm(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s);
+      st = R >= kWideGemmRows ? launch_gemm_wide(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, (int8_t*)(pw + w.w8), s)
+                              : launch_gemm(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s);
       if (st != hipSuccess) return hip_status(st);
       if (!in) break;
       ConvSeqArgs c{conv, proj + r.DI, r.IPO, Lw.conv_w, Lw.conv_b, r.C, tc};

@@ -27,7 +27,15 @@ struct PrepArgs {
   uint16_t* xn_out;          // (M, K) normalized activations, or null
   uint16_t* xs16_out;        // (M) activation scale as fp16 bits, or null
   int K;
+  int q_tiled;               // q_out in the 16-row tiled layout of the wide GEMM (many-row path only)
 };
+// The wide GEMM's operand layout (activations q and expanded weights): 16-row tiles of 64-column
+// k steps, [row / 16][k / 64][(k / 16) % 4][row % 16][k % 16], so that lane l of a wave reading
+// (row tile, k step) takes bytes 16 l .. 16 l + 15: one contiguous 1 KiB per wave-wide load.
+// K is a multiple of 64; the rows are padded to a multiple of 16.
+__host__ __device__ inline size_t wide_tiled_offset(int row, int k, int K) {
+  return (((size_t)(row >> 4) * (K >> 6) + (k >> 6)) * 4 + ((k >> 4) & 3)) * 256 + (row & 15) * 16 + (k & 15);
+}
 
 struct ProjArgs {
   const uint32_t* bits;      // tiled sign bits [N_pad/64][K/128][64][4]
@@ -279,6 +287,11 @@ hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uin
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s);
+// Prefill GEMM for thousands of rows (IN without conv, OUT): q in the wide tiled layout (rows
+// padded to 16); expands the bits to w8 (gemm_wide_w8_bytes of scratch, tiled likewise) and runs
+// a tiled MFMA GEMM with gemm_kernel's epilogue.
+size_t gemm_wide_w8_bytes(int N, int K);
+hipError_t launch_gemm_wide(const GemmArgs& a, int mode, int8_t* w8, hipStream_t s);
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s);
 hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s);
 hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);

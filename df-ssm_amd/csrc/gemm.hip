@@ -347,6 +347,166 @@ static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
   return (a.M > 16 && a.K <= 4096) ? launch_gemm_rt<2, MODE>(a, s) : launch_gemm_rt<1, MODE>(a, s);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Wide GEMM for the prompt prefill (thousands of activation rows). The sign bits are expanded once
+// per projection to int8 +-1 (expand_bits_kernel: W8 row-major (N, K)), then a plain MFMA GEMM:
+// a workgroup of 4 waves owns a 128 x 128 tile (activation rows x output rows), wave w the 64 x 64
+// quarter (rows 64 (w & 1), outputs 64 (w >> 1)) as 4 x 4 tiles of v_mfma_i32_16x16x64_i8, its A
+// (q) and B (W8) operands loaded straight into registers two k steps ahead (three-stage ring; loads
+// complete in issue order). Both operands are stored in 16-row tiles (wide_tiled_offset), so the
+// MFMA lane layout (lane l: row l % 16, 16 bytes of k block l / 16) is one contiguous 1 KiB per
+// wave-wide load; row-major rows K bytes apart put every lane on its own cache line. acc = sum_k q[m][k] W8[n][k] is exact (int32), i.e. gemm_kernel's
+// acc; the epilogue is gemm_kernel's, operation for operation (scales, LoRA term in fp64, proj
+// rows or residual add). Workgroup -> tile: workgroups are dealt to the 8 XCDs in turn, so XCD x
+// takes the row tiles m = x (mod 8) (each activation tile is read by one XCD's L2) and walks the
+// output tiles of one row tile after another.
+// ---------------------------------------------------------------------------------------------
+// W8 = bit k of row n ? +1 : -1 in the wide tiled layout; one thread per (row, 128-column chunk)
+// of the tiled bits.
+__global__ __launch_bounds__(256) void expand_bits_kernel(const uint32_t* __restrict__ bits, int8_t* __restrict__ w8,
+                                                          int N, int K) {
+  const int CH = K / 128;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= N * CH) return;
+  const int n = i / CH, c = i - n * CH;
+  const u32x4 b = ld_nt(bits + (((size_t)(n >> 6) * CH + c) * 64 + (n & 63)) * 4);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {  // 16 columns 128 c + 16 q .. + 15: bits 16 q .. of the chunk
+    const uint32_t h16 = (b[q >> 1] >> (16 * (q & 1))) & 0xffffu;
+    uint32_t o[4];
+#pragma unroll
+    for (int nib = 0; nib < 4; ++nib) {
+      const uint32_t x = (((h16 >> (4 * nib)) & 0xfu) * 0x00204081u) & 0x01010101u;  // 0/1 bytes
+      o[nib] = ~(x * 0xfeu);                                                          // -> -1/+1
+    }
+    *(u32x4*)(w8 + wide_tiled_offset(n, 128 * c + 16 * q, K)) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+constexpr int kWT = 128;  // tile edge (rows and outputs)
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmArgs a, const int8_t* __restrict__ w8, int TN) {
+  __shared__ float hl[kWT][DFSSM_LORA_R];
+  __shared__ float xsl[kWT];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int L = (int)blockIdx.x, xcd = L & 7, j = L >> 3;
+  const int tm = 8 * (j / TN) + xcd, tn = j % TN;
+  const int TM = (a.M + kWT - 1) / kWT;
+  if (tm >= TM) return;  // uniform over the workgroup
+  const int m0 = tm * kWT, n0 = tn * kWT, K = a.K, KS = K / 64;
+  const int lr = lane & 15;
+  // operand bases: 16-row tiles of the tiled layouts, lane l at byte 16 l of a (tile, k step)
+  // (tiles past the last one are clamped to it: their results are discarded)
+  const int lastA = (a.M + 15) / 16 - 1, lastB = (a.N + 15) / 16 - 1;
+  uint32_t ao[4], bo[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int ta = (m0 + 64 * wm + 16 * t) >> 4, tb = (n0 + 64 * wn + 16 * t) >> 4;
+    ao[t] = (uint32_t)((ta < lastA ? ta : lastA) * KS * 1024 + 16 * lane);
+    bo[t] = (uint32_t)((tb < lastB ? tb : lastB) * KS * 1024 + 16 * lane);
+  }
+  v4i acc[4][4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = v4i{0, 0, 0, 0};
+  v4i A[3][4], B[3][4];
+  auto load = [&](int st, int step) {
+    const uint32_t ko = (uint32_t)(1024 * (step < KS ? step : KS - 1));  // the ring's overrun re-reads
+#pragma unroll
+    for (int t = 0; t < 4; ++t) A[st][t] = *(const v4i*)(a.q + ao[t] + ko);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) B[st][t] = *(const v4i*)(w8 + bo[t] + ko);
+  };
+  auto mma = [&](int st) {
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[st][ti], B[st][tj], acc[ti][tj], 0, 0, 0);
+  };
+  load(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  // whole groups of three steps (K / 64 = 8, 16, ... 80: the last group may run past KS; those
+  // steps multiply a re-read of step KS - 1 and are skipped)
+  for (int s = 0; s < KS; s += 3) {
+    load(2, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    load(0, s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < KS) mma(1);
+    load(1, s + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 2 < KS) mma(2);
+  }
+
+  // ---- epilogue (gemm_kernel's): the tile's LoRA intermediates and activation scales in LDS ----
+  for (int i = tid; i < kWT * DFSSM_LORA_R; i += 256) {
+    const int m = m0 + i / DFSSM_LORA_R;
+    (&hl[0][0])[i] = m < a.M ? a.h[(size_t)m * DFSSM_LORA_R + i % DFSSM_LORA_R] : 0.0f;
+  }
+  if (tid < kWT) xsl[tid] = m0 + tid < a.M ? a.xs[m0 + tid] : 0.0f;
+  __syncthreads();
+#pragma unroll  // (a runtime tj would index the accumulators dynamically: scratch memory)
+  for (int tj = 0; tj < 4; ++tj) {
+    const int n = n0 + 64 * wn + 16 * tj + lr;
+    if (n >= a.N) continue;
+    const u32x4 la = *(const u32x4*)(a.lA + (size_t)n * DFSSM_LORA_R);
+    const float as = h2f(a.lAs[n]), ws = h2f(a.wscale[n]);
+    double aqd[DFSSM_LORA_R];
+#pragma unroll
+    for (int rr = 0; rr < DFSSM_LORA_R; ++rr) aqd[rr] = (double)r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * as);
+    uint16_t old[4][4];
+    if (MODE == DFSSM_MODE_OUT) {  // the residual rows, all loaded before any is used
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + 64 * wm + 16 * ti + 4 * (lane >> 4) + e;
+          old[ti][e] = a.out[(size_t)(m < a.M ? m : a.M - 1) * a.ld_out + n];
+        }
+    }
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int mb = 64 * wm + 16 * ti + 4 * (lane >> 4) + e, m = m0 + mb;
+        if (m >= a.M) continue;
+        const int accv = acc[ti][tj][e];
+        const float y = r16(r16(r16((float)accv) * xsl[mb]) * ws);
+        double lo = 0.0;
+#pragma unroll
+        for (int rr = 0; rr < DFSSM_LORA_R; ++rr) lo += (double)hl[mb][rr] * aqd[rr];
+        const float out = r16((float)lo + y);
+        uint16_t* op = a.out + (size_t)m * a.ld_out + n;
+        if (MODE == DFSSM_MODE_IN) *op = f2h(out);
+        else *op = f2h(h2f(old[ti][e]) + out);
+      }
+  }
+}
+
+size_t gemm_wide_w8_bytes(int N, int K) { return (size_t)(N + 15) / 16 * 16 * K; }
+
+hipError_t launch_gemm_wide(const GemmArgs& a, int mode, int8_t* w8, hipStream_t s) {
+  if (a.M < 1 || a.K % 512 || a.K > 5120 || !a.h || !a.xs || !a.lA || !a.lAs || !a.wscale || a.conv_state ||
+      a.acc_out || (mode != DFSSM_MODE_IN && mode != DFSSM_MODE_OUT))
+    return hipErrorInvalidValue;
+  const int CH = a.K / 128;
+  hipLaunchKernelGGL(expand_bits_kernel, dim3((a.N * CH + 255) / 256), dim3(256), 0, s, a.bits, w8, a.N, a.K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int TM = (a.M + kWT - 1) / kWT, TN = (a.N + kWT - 1) / kWT;
+  const dim3 g(8 * ((TM + 7) / 8) * TN);
+  if (mode == DFSSM_MODE_IN) hipLaunchKernelGGL(gemm_wide_kernel<DFSSM_MODE_IN>, g, dim3(256), 0, s, a, w8, TN);
+  else hipLaunchKernelGGL(gemm_wide_kernel<DFSSM_MODE_OUT>, g, dim3(256), 0, s, a, w8, TN);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {
   if (a.M < 1 || a.M > kGemmMaxRows || a.K % 512 || a.K > 5120) return hipErrorInvalidValue;
   switch (mode) {

@@ -167,8 +167,9 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
 // values of a thread's 8 columns (16 ranks) stay in registers across the rows, and each row's
 // RMSNorm, quantizer and 16 LoRA intermediates are computed once (prep_kernel's 16 workgroups per
 // row each recompute the norm). The thread -> column map, the per-thread order of the fp64 sums
-// and the reduction trees are prep_kernel's, so every output is identical. Writes q_out, xs_out,
-// h_out and s_out; the decode-only outputs (planes_out, xn_out, xs16_out) are not supported.
+// and the reduction trees are prep_kernel's, so every output is identical. Writes q_out (row-major
+// or, with q_tiled, in the wide GEMM's tiled layout), xs_out, h_out and s_out; the decode-only
+// outputs (planes_out, xn_out, xs16_out) are not supported.
 constexpr int kPrepRows = 16;
 constexpr int kPrepRowsT = kMaxK / 8;  // threads per workgroup at most
 
@@ -282,7 +283,10 @@ __global__ __launch_bounds__(kPrepRowsT) void prep_rows_kernel(PrepArgs a, int M
       qsum += q;
       qw[e >> 2] |= (uint32_t)(q & 0xff) << (8 * (e & 3));
     }
-    if (a.q_out) *(uint2*)(a.q_out + (size_t)m * a.ld_q + 8 * tid) = uint2{qw[0], qw[1]};
+    if (a.q_out) {
+      int8_t* qp = a.q_tiled ? a.q_out + wide_tiled_offset(m, 8 * tid, K) : a.q_out + (size_t)m * a.ld_q + 8 * tid;
+      *(uint2*)qp = uint2{qw[0], qw[1]};
+    }
     int S = 0;
     if (want_sum) {  // uniform
       const int qs = wave_sum_dpp_i32(qsum);
@@ -603,7 +607,9 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
   if (mode == DFSSM_MODE_OUT && (!a.sumsq_slots || a.n_slots < 1 || a.n_slots > a.K / 8)) return hipErrorInvalidValue;
   if (a.lB && !a.lBs) return hipErrorInvalidValue;
   if (a.K > kMaxK || a.K % 512) return hipErrorInvalidValue;  // K / 8 threads: whole waves
-  if (M > 64 && !a.planes_out && !a.xn_out && !a.xs16_out && (a.h_out || !a.lB)) {  // many rows: one pass each
+  const bool rows_path = M > 64 && !a.planes_out && !a.xn_out && !a.xs16_out && (a.h_out || !a.lB);
+  if (a.q_tiled && !rows_path) return hipErrorInvalidValue;
+  if (rows_path) {  // many rows: one pass each
     const dim3 g((M + kPrepRows - 1) / kPrepRows);
     if (mode == DFSSM_MODE_IN)
       hipLaunchKernelGGL(prep_rows_kernel<DFSSM_MODE_IN>, g, dim3(a.K / 8), 0, s, a, M);

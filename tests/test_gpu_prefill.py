@@ -61,7 +61,7 @@ def tiny_weights():
     return make_weights(config_tiny(n_layer=3), seed=0)
 
 
-@pytest.mark.parametrize("B,T", [(1, 1), (1, 17), (3, 40), (5, 16), (16, 9), (64, 3)])
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 17), (3, 40), (5, 16), (16, 9), (64, 3), (5, 61), (64, 9)])
 def test_prefill_equals_steps_tiny(tiny_weights, B, T):
     print(f"prefill tiny B={B} T={T}", flush=True)
     _prefill_vs_steps(tiny_weights, B, T)
