@@ -13,13 +13,16 @@
 //                    thread -> state-element map and every reduction tree are those of
 //                    ssm_kernel<true>, so state, g and the per-block sum(g^2) slots are bit-for-bit
 //                    what n decode steps produce. The tokens' operands (B | C, x, z, dt) are staged
-//                    in LDS kTT tokens at a time, double-buffered, with softplus dt, exp(dt A) and
-//                    the gate factor z sigma(z) computed once per token (per row) while staging.
+//                    in LDS kTT tokens at a time, double-buffered, with softplus dt, exp(dt A),
+//                    the gate factor z sigma(z), B widened to fp32 and C to fp64 computed once per
+//                    token (per row) while staging.
 //
 // Together with the row-wise kernels this makes the prefill equal, bit for bit, to n calls of the
 // decode step (Mamba-2 recurrence of df_ssm_kernels.cu:53-103 / training/
 // df_ssm_mamba2_distill_dfw.py:346-381, evaluated token by token as the reference's
 // cpu_inference_driver.py:186-204 ingests a prompt).
+#include <type_traits>
+
 #include "common.h"
 #include "dfssm_kernels.h"
 
@@ -66,7 +69,8 @@ constexpr int kPGMax = 4;  // 16-row state blocks per workgroup
 constexpr int kTG = 4;     // tokens whose reductions run together
 
 struct ScanBuf {
-  uint16_t bc[kTT][256];           // B (0..127) | C (128..255) of each token
+  float bf[kTT][128];              // B of each token, widened once here (fp16 values)
+  double cd[kTT][128];             // C of each token, widened to fp64 (fp16 values)
   uint16_t x[kTT][16 * kPGMax];    // x of the workgroup's rows
   float sz[kTT][16 * kPGMax];      // gate factor fp16(z sigma(z)) of the workgroup's rows
   float dt[kTT], abar[kTT];        // softplus dt and exp(dt A) of the head
@@ -117,7 +121,21 @@ __device__ __forceinline__ void scan_stage(ScanBuf& S, const ScanRaw<PG>& r, flo
 #pragma unroll
   for (int k = 0; k < ScanRaw<PG>::KB; ++k) {
     const int i = tid + NT * k;
-    if (i < kTT * 32) *(u32x4*)&S.bc[i / 32][8 * (i % 32)] = r.bc[k];
+    if (i < kTT * 32) {
+      const int t = i / 32, c = i % 32;  // halves 8 c .. 8 c + 7 of B | C
+      const u32x4 v = r.bc[k];
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+      if (c < 16) {
+        *(f32x4*)&S.bf[t][8 * c] = f32x4{f[0], f[1], f[2], f[3]};
+        *(f32x4*)&S.bf[t][8 * c + 4] = f32x4{f[4], f[5], f[6], f[7]};
+      } else {
+        double* d = &S.cd[t][8 * (c - 16)];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d[e] = (double)f[e];
+      }
+    }
   }
   if (tid < kTT * RW) {
     const int t = tid / RW, i = tid % RW;
@@ -171,31 +189,38 @@ __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
     for (int t = 0; t < nt; t += kTG) {
       double acc0[kTG], acc1[kTG];
       float xv0[kTG], xv1[kTG];
+      // FULL: all kTG tokens of the group exist (every group but a prompt's last), no selects
+      auto group = [&](auto full_t) {
+        constexpr bool FULL = decltype(full_t)::value;
 #pragma unroll
-      for (int j = 0; j < kTG; ++j) {
-        const int tt = t + j < nt ? t + j : t;
-        const uint2 b4 = *(const uint2*)&S.bc[tt][n0];
-        const uint2 c4 = *(const uint2*)&S.bc[tt][128 + n0];
-        const float dt = S.dt[tt], abar = S.abar[tt];
-        xv0[j] = h2f(S.x[tt][rl]);
-        xv1[j] = h2f(S.x[tt][rl + 8]);
-        const float X0 = xv0[j] * dt, X1 = xv1[j] * dt;
-        const uint32_t bw[2] = {b4.x, b4.y}, cw[2] = {c4.x, c4.y};
-        const bool valid = t + j < nt;
-        acc0[j] = 0.0;
-        acc1[j] = 0.0;
+        for (int j = 0; j < kTG; ++j) {
+          const int tt = FULL ? t + j : (t + j < nt ? t + j : t);
+          const f32x4 b4 = *(const f32x4*)&S.bf[tt][n0];
+          const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+          const double* cp = &S.cd[tt][n0];
+          const double cq[4] = {cp[0], cp[1], cp[2], cp[3]};
+          const float dt = S.dt[tt], abar = S.abar[tt];
+          xv0[j] = h2f(S.x[tt][rl]);
+          xv1[j] = h2f(S.x[tt][rl + 8]);
+          const float X0 = xv0[j] * dt, X1 = xv1[j] * dt;
+          const bool valid = FULL || t + j < nt;
+          acc0[j] = 0.0;
+          acc1[j] = 0.0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float bn = h2f((uint16_t)(bw[q >> 1] >> (16 * (q & 1))));
-          const float cn = h2f((uint16_t)(cw[q >> 1] >> (16 * (q & 1))));
-          const float n0v = __builtin_fmaf(abar, h0[q], X0 * bn);
-          const float n1v = __builtin_fmaf(abar, h1[q], X1 * bn);
-          h0[q] = valid ? n0v : h0[q];
-          h1[q] = valid ? n1v : h1[q];
-          acc0[j] += (double)cn * (double)h0[q];
-          acc1[j] += (double)cn * (double)h1[q];
+          for (int q = 0; q < 4; ++q) {
+            const float n0v = __builtin_fmaf(abar, h0[q], X0 * bq[q]);
+            const float n1v = __builtin_fmaf(abar, h1[q], X1 * bq[q]);
+            h0[q] = valid ? n0v : h0[q];
+            h1[q] = valid ? n1v : h1[q];
+            // C h is exact in fp64 (11 x 24 significant bits), so the fma rounds exactly as
+            // ssm_kernel's multiply-then-add
+            acc0[j] = __builtin_fma(cq[q], (double)h0[q], acc0[j]);
+            acc1[j] = __builtin_fma(cq[q], (double)h1[q], acc1[j]);
+          }
         }
-      }
+      };
+      if (t + kTG <= nt) group(std::true_type{});
+      else group(std::false_type{});
 #pragma unroll
       for (int j = 0; j < kTG; ++j) {
         acc0[j] = row_sum_f64(acc0[j]);
