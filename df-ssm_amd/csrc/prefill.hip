@@ -150,6 +150,22 @@ __device__ __forceinline__ void scan_stage(ScanBuf& S, const ScanRaw<PG>& r, flo
   }
 }
 
+// v of lane l + 16 in lanes 0..15 and 32..47, and of lane l + 32 in lanes 0..31, by the gfx950
+// lane swaps (v_permlane16_swap between rows 0|1 and 2|3, v_permlane32_swap between the halves;
+// with both operands v, the second result holds the partner row's value in rows 0 and 2).
+__device__ __forceinline__ double lane_plus16(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_permlane16_swap((uint32_t)u, (uint32_t)u, false, false)[1];
+  const uint32_t hi = __builtin_amdgcn_permlane16_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false)[1];
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double lane_plus32(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_permlane32_swap((uint32_t)u, (uint32_t)u, false, false)[1];
+  const uint32_t hi = __builtin_amdgcn_permlane32_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false)[1];
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 template <int PG>
 __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
   __shared__ ScanBuf buf[2];
@@ -229,15 +245,14 @@ __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
       double gsqd[kTG];
 #pragma unroll
       for (int j = 0; j < kTG; ++j) {
-        const double t0a = readlane_f64(acc0[j], 0) + readlane_f64(acc0[j], 16);
-        const double t0b = readlane_f64(acc0[j], 32) + readlane_f64(acc0[j], 48);
-        const double t1a = readlane_f64(acc1[j], 0) + readlane_f64(acc1[j], 16);
-        const double t1b = readlane_f64(acc1[j], 32) + readlane_f64(acc1[j], 48);
+        // the two 16-lane row sums of each state row added as ssm_kernel's readlanes add them:
+        // (lane 0) + (lane 16) in lane 0, (lane 32) + (lane 48) in lane 32
+        const double s0 = acc0[j] + lane_plus16(acc0[j]);
+        const double s1 = acc1[j] + lane_plus16(acc1[j]);
         gsqd[j] = 0.0;
         if ((gt & 31) == 0 && t + j < nt) {
-          const bool hi = lane >= 32;
-          const float y0 = r16((float)(hi ? t0b : t0a) + xv0[j] * Dh);
-          const float y1 = r16((float)(hi ? t1b : t1a) + xv1[j] * Dh);
+          const float y0 = r16((float)s0 + xv0[j] * Dh);
+          const float y1 = r16((float)s1 + xv1[j] * Dh);
           const float o0 = r16(y0 * S.sz[t + j][rl]);
           const float o1 = r16(y1 * S.sz[t + j][rl + 8]);
           gsqd[j] = (double)o0 * (double)o0 + (double)o1 * (double)o1;
@@ -250,7 +265,7 @@ __global__ __launch_bounds__(256 * PG) void ssm_scan_kernel(ScanArgs a) {
       // wave_sum_dpp_f64 adds exact zeros to them and equals (lane 0) + (lane 32)
 #pragma unroll
       for (int j = 0; j < kTG; ++j) {
-        const double s = readlane_f64(gsqd[j], 0) + readlane_f64(gsqd[j], 32);
+        const double s = gsqd[j] + lane_plus32(gsqd[j]);  // (lane 0) + (lane 32) in lane 0
         if (lane == 0 && t + j < nt) S.gpart[t + j][w] = s;
       }
     }
