@@ -41,15 +41,21 @@ struct PrepLds {
   int red_i[kPW];
 };
 
-// Grid (16, M) x K/8 threads (8 columns each; K is a multiple of 512, so whole waves): workgroup
-// (r, m) recomputes the normalization and quantization of row m, writes the q bytes (and for the
+// 16 M workgroups (more when M is not a multiple of 8) x K/8 threads (8 columns each; K is a
+// multiple of 512, so whole waves): workgroup (r, m) recomputes the normalization and quantization of row m, writes the q bytes (and for the
 // bit-plane GEMV the planes) of column slice r (K/16 columns) and the LoRA intermediate h[m][r];
 // workgroup (0, m) also writes sum q (when asked) and the scale. Three LDS reductions: the sum of
 // squares, then the LoRA sum and the maximum together, then (workgroup 0, when asked) sum q.
 template <int MODE>
-__global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a) {
+__global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
   __shared__ PrepLds L;
-  const int rr = blockIdx.x, m = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // workgroup -> (rank rr, row m): workgroups are dealt to the 8 XCDs in turn, and XCD x takes
+  // the rows m = x (mod 8) with all 16 ranks of each, so a row (read by all 16 of its
+  // workgroups) is fetched into one XCD's L2 rather than into all eight
+  const int x8 = (int)blockIdx.x & 7, j8 = (int)blockIdx.x >> 3;
+  const int m = 8 * (j8 / DFSSM_LORA_R) + x8, rr = j8 % DFSSM_LORA_R;
+  if (m >= M) return;  // uniform over the workgroup
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int K = a.K, NT = (int)blockDim.x, nw = NT >> 6;
   const uint16_t* act = a.act + (size_t)m * a.ld_act;
   // Loads first, in the order they are needed (loads complete in issue order, so waiting for one
@@ -618,9 +624,9 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
     return hipGetLastError();
   }
   if (mode == DFSSM_MODE_IN)
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(8 * DFSSM_LORA_R * ((M + 7) / 8)), dim3(a.K / 8), 0, s, a, M);
   else
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(DFSSM_LORA_R, M), dim3(a.K / 8), 0, s, a);
+    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(8 * DFSSM_LORA_R * ((M + 7) / 8)), dim3(a.K / 8), 0, s, a, M);
   return hipGetLastError();
 }
 
