@@ -215,6 +215,10 @@ int dfssm_tile_embedding(const void* src, void* dst, int vocab, int row_bytes, v
   return hip_status(launch_tile_emb((const uint8_t*)src, (uint8_t*)dst, vocab, row_bytes, as_stream(stream)));
 }
 
+// The stand-alone scaffold op runs the bit-plane GEMV (N / 64 workgroups) only with at least this
+// many output rows; with fewer, the matrix-core GEMM (N / 16 workgroups) measured faster.
+constexpr int kScaffoldGemvMinN = 4096;
+
 int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint16_t* xscale,
                         const uint16_t* wscale, int M, int N, int K, int32_t* acc_out,
                         uint16_t* y_out, void* stream) {
@@ -223,7 +227,7 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
   if (M < 1 || M > 64) return DFSSM_E_BATCH;
   if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
   if (!aligned16(tiled_bits) || !aligned16(q)) return DFSSM_E_ALIGN;
-  if (M <= 4) {
+  if (M <= 4 && N >= kScaffoldGemvMinN) {
     ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, nullptr, nullptr, nullptr, N, K};
     return hip_status(launch_scaffold(a, M, as_stream(stream)));
   }
@@ -247,13 +251,14 @@ int dfssm_scaffold_lora_gemm(const uint32_t* tiled_bits, const uint16_t* wscale,
   if (!aligned16(tiled_bits) || !aligned16(q) || !aligned16(xn) || !aligned16(lBq) || !aligned16(lA))
     return DFSSM_E_ALIGN;
   hipStream_t s = as_stream(stream);
+  if (M == 1 && N >= kScaffoldGemvMinN) {  // one launch, the GEMV's workgroups compute the intermediates
+    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, lA, lA_s, nullptr, N, K, xn, lBq, lora_h};
+    return hip_status(launch_scaffold(a, M, s));
+  }
+  // otherwise the intermediates once (lora_h_kernel), then the matrix-core GEMM
   LoraHArgs la{xn, lBq, lora_h, K};
   hipError_t e = launch_lora_h(la, M, s);
   if (e != hipSuccess) return hip_status(e);
-  if (M <= 4) {
-    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, lA, lA_s, lora_h, N, K};
-    return hip_status(launch_scaffold(a, M, s));
-  }
   GemmArgs a{};
   a.bits = tiled_bits; a.wscale = wscale;
   a.q = q; a.ld_q = K; a.M = M;

@@ -92,6 +92,11 @@ struct ScaffoldArgs {
   const uint16_t* lAs;
   const uint16_t* h16;
   int N, K;
+  // M <= 4 with LoRA (one launch): the intermediates are computed in the kernel from xn and the
+  // fp16 LoRA-B table, and written to h_out
+  const uint16_t* xn;        // (M, K) fp16
+  const uint16_t* lBq;       // (16, K) fp16(B_i8 * B_s)
+  uint16_t* h_out;           // (M, 16) fp16
 };
 
 // LoRA intermediates of the stand-alone scaffold op: h[m][r] = fp16(sum_k xn[m][k] * lBq[r][k]).

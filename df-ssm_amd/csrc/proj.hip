@@ -457,52 +457,171 @@ __global__ __launch_bounds__(kNT) void proj_kernel(ProjArgs a) {
   }
 }
 
-// Stand-alone scaffold GEMM for given int8 activations (tests / microbench): acc and y only.
-constexpr int kNTs = 256;  // scaffold_kernel: 4 waves, each a quarter of K
-
-template <int M>
-__global__ __launch_bounds__(kNTs) void scaffold_kernel(ScaffoldArgs a) {
-  __shared__ uint32_t planes[M][kMaxK / 32][8];
-  __shared__ int T[4][M][64];
-  __shared__ int S[M];
-  __shared__ int red_i[4];
+// Stand-alone scaffold op on many output rows (N >= 4096) at M <= 4 (dfssm_scaffold_gemm), and
+// with LoRA at M = 1 in one launch (dfssm_scaffold_lora_gemm): proj_kernel's GEMV for given int8
+// activations. (With fewer output rows, N / 64 workgroups leave most CUs idle and with LoRA at
+// M >= 2 the intermediates cost M x 16 K fp64 products per workgroup: the GEMM path is faster.) One
+// workgroup (1024 threads) owns 64 output rows. The small operands are loaded first (q bytes,
+// the LoRA inputs), then the sign-bit chunks, so that building the bit planes and sum q (every
+// workgroup for itself: M K values, two ballots' worth per thread) and the LoRA intermediates
+// overlaps the bit stream. LoRA: wave r computes h[m][r] = fp16(sum_k xn[m][k] lBq[r][k]), each
+// lane summing its K / 64 columns in fp64, then one wave sum per row; the fp16 x fp16 products
+// are exact in fp32, so this is lora_h_kernel's sum in another order (fp64 sums of exact products:
+// the same value while they stay exact, the assumption the one-launch layer's LoRA split makes
+// too). Workgroup 0 writes the intermediates out.
+template <int M, bool LORA>
+__global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
+  __shared__ ProjLds<M> L;
+  __shared__ __attribute__((aligned(16))) uint16_t xns[LORA ? M : 1][LORA ? kMaxK : 8];
+  __shared__ int Sred[kNW][M];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x;
-  const int K = a.K, KW = K / 32, CH = KW / 4, CPW = CH / 4;
-  const uint4* bits = (const uint4*)a.bits + ((size_t)g * CH + wave * CPW) * 64 + lane;
-  for (int m = 0; m < M; ++m) {
-    int qsum = 0;
-    for (int k0 = (tid & ~63); k0 < K; k0 += kNTs) {
-      const int k = k0 + lane;
-      const int q = a.q[(size_t)m * K + k];
-      qsum += q;
-      const uint32_t qb = (uint32_t)q & 0xffu;
+  const int K = a.K, CH = K / 128, NB = K / 64;
+  // ---- small operands first: q bytes of this wave's 64-value blocks, the xn rows (to LDS) and
+  // this wave's LoRA-B row (rank = wave) ----
+  // (unconditional loads from clamped indices: a load in a branch makes the compiler wait for
+  // every outstanding load where the paths join)
+  constexpr int kQB = (kMaxK / 64 + kNW - 1) / kNW;  // 64-value blocks per wave and row
+  int8_t qv[M][kQB];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const uint64_t mask = __ballot((qb >> b) & 1u);
-        if (lane == b) planes[m][k0 / 32][b] = (uint32_t)mask;
-        if (lane == 8 + b) planes[m][k0 / 32 + 1][b] = (uint32_t)(mask >> 32);
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) {
+      const int b = wave + kNW * j;
+      qv[m][j] = a.q[(size_t)m * K + 64 * (b < NB ? b : NB - 1) + lane];
+    }
+  constexpr int kLB = kMaxK / 512;  // 512-column blocks
+  constexpr int kXI = (kMaxK / 8 + kNT - 1) / kNT;  // xn vectors per thread and row
+  u32x4 bq[kLB], xv8[LORA ? M : 1][kXI];
+  if (LORA) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int i = 0; i < kXI; ++i) {
+        const int c = tid + kNT * i;  // 8-column vector of row m (stored to LDS below)
+        xv8[m][i] = *(const u32x4*)(a.xn + (size_t)m * K + 8 * (c < K / 8 ? c : K / 8 - 1));
+      }
+#pragma unroll
+    for (int v = 0; v < kLB; ++v)
+      bq[v] = *(const u32x4*)(a.lBq + (size_t)wave * K + 512 * (v < K / 512 ? v : K / 512 - 1) + 8 * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the small loads stay ahead of the bit stream
+  // ---- the sign-bit chunks and the epilogue row data ----
+  const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + lane;
+  u32x4 wb[kMaxCPW];
+#pragma unroll
+  for (int j = 0; j < kMaxCPW; ++j) {  // chunks past CH re-read the last one (not used)
+    const int c = wave + kNW * j;
+    wb[j] = ld_nt(bits + (size_t)(c < CH ? c : CH - 1) * 64);
+  }
+  const int n = g * 64 + lane;
+  const bool erow = tid < M * 64 && n < a.N;
+  const int em = tid >> 6;
+  const int nc = n < a.N ? n : a.N - 1, mc = em < M ? em : M - 1;
+  // the scales are optional when y is not written: a valid stand-in address then (the sign bits
+  // hold N K / 8 >= 2 N bytes, q M K >= 2 M bytes)
+  const uint16_t* wsp = a.wscale ? a.wscale : (const uint16_t*)a.bits;
+  const uint16_t* xsp = a.xscale ? a.xscale : (const uint16_t*)a.q;
+  const uint16_t ws_raw = wsp[nc], xs_raw = xsp[mc];
+  u32x4 la = {0u, 0u, 0u, 0u};
+  uint16_t as_raw = 0;
+  if (LORA) {
+    la = *(const u32x4*)(a.lA + (size_t)nc * DFSSM_LORA_R);
+    as_raw = a.lAs[nc];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (LORA) {  // the xn rows to LDS (waits for the small loads only: they were issued first);
+               // threads past the row rewrite its last vector with the same data
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int i = 0; i < kXI; ++i) {
+        const int c = tid + kNT * i;
+        *(u32x4*)&xns[m][8 * (c < K / 8 ? c : K / 8 - 1)] = xv8[m][i];
+      }
+  }
+  // ---- bit planes and sum q ----
+  int qsum[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    qsum[m] = 0;
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) {
+      const int b = wave + kNW * j;
+      if (b < NB) {  // wave-uniform
+        const int q = qv[m][j];
+        qsum[m] += q;
+        uint32_t pw[16];
+        planes64(q, pw);
+        planes_store(&L.planes[m][2 * b][0], pw);
       }
     }
-    const int s = block_sum_i32<kNTs>(qsum, red_i);
-    if (tid == 0) S[m] = s;
   }
-  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int s = wave_sum_dpp_i32(qsum[m]);
+    if (lane == 0) Sred[wave][m] = s;
+  }
+  // ---- LoRA intermediates (wave r = rank r) ----
+  if (LORA) {
+    lds_barrier();  // xn in LDS (stored above)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      double acc = 0.0;  // this lane's columns 512 v + 8 lane .. + 7, then one wave sum
+#pragma unroll
+      for (int v = 0; v < kLB; ++v) {
+        if (v < K / 512) {  // uniform
+          const u32x4 xv = *(const u32x4*)&xns[m][512 * v + 8 * lane];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = h2f((uint16_t)(xv[e >> 1] >> (16 * (e & 1))));
+            const float b = h2f((uint16_t)(bq[v][e >> 1] >> (16 * (e & 1))));
+            acc += (double)(x * b);
+          }
+        }
+      }
+      const double t = wave_sum_dpp_f64(acc);
+      if (lane == 0) {
+        const uint16_t hb = f2h((float)t);
+        L.hl[m][wave] = h2f(hb);
+        if (g == 0) a.h_out[(size_t)m * DFSSM_LORA_R + wave] = hb;
+      }
+    }
+  }
+  lds_barrier();  // planes, sum q partials, intermediates
+  if (tid < M) {
+    int S = 0;
+    for (int w = 0; w < kNW; ++w) S += Sred[w][tid];
+    L.S[tid] = S;
+  }
+  // ---- GEMV (proj_kernel's) ----
   uint32_t cnt[M][8];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int b = 0; b < 8; ++b) cnt[m][b] = 0;
-  for (int c = 0; c < CPW; ++c) {
-    const u32x4 w4 = ld_nt(bits + (size_t)c * 64);
-    const int word0 = (wave * CPW + c) * 4;
-    const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < kMaxCPW; ++j) {
+    const int c = wave + kNW * j;
+    if (c < CH) {
 #pragma unroll
-      for (int m = 0; m < M; ++m)
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = wb[j][i];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) cnt[m][b] += __builtin_popcount(ww[i] & planes[m][word0 + i][b]);
+        for (int m = 0; m < M; ++m) {
+          const u32x4 p0 = *(const u32x4*)&L.planes[m][c * 4 + i][0];
+          const u32x4 p1 = *(const u32x4*)&L.planes[m][c * 4 + i][4];
+          cnt[m][0] += __builtin_popcount(w & p0[0]);
+          cnt[m][1] += __builtin_popcount(w & p0[1]);
+          cnt[m][2] += __builtin_popcount(w & p0[2]);
+          cnt[m][3] += __builtin_popcount(w & p0[3]);
+          cnt[m][4] += __builtin_popcount(w & p1[0]);
+          cnt[m][5] += __builtin_popcount(w & p1[1]);
+          cnt[m][6] += __builtin_popcount(w & p1[2]);
+          cnt[m][7] += __builtin_popcount(w & p1[3]);
+        }
+      }
+    }
   }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -510,31 +629,31 @@ __global__ __launch_bounds__(kNTs) void scaffold_kernel(ScaffoldArgs a) {
 #pragma unroll
     for (int b = 0; b < 7; ++b) t += (int)(cnt[m][b] << b);
     t -= (int)(cnt[m][7] << 7);
-    T[wave][m][lane] = t;
+    L.T[wave][m][lane] = t;
   }
-  __syncthreads();
-  if (tid < M * 64) {
-    const int m = tid >> 6;
-    const int n = g * 64 + lane;
-    if (n < a.N) {
-      const int acc = 2 * (T[0][m][lane] + T[1][m][lane] + T[2][m][lane] + T[3][m][lane]) - S[m];
-      if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = acc;
-      if (a.y_out) {
-        const float y = r16(r16(r16((float)acc) * h2f(a.xscale[m])) * h2f(a.wscale[n]));
-        float out = y;
-        if (a.lA) {  // LoRA term: sum_r h[m][r] * fp16(A_i8[n][r] * A_s[n]) (exact products, fp64)
-          const u32x4 la = *(const u32x4*)(a.lA + (size_t)n * DFSSM_LORA_R);
-          const float as = h2f(a.lAs[n]);
-          double lo = 0.0;
+  lds_barrier();
+  // ---- epilogue: thread (m = tid / 64, row n) ----
+  if (erow) {
+    const int m = em;
+    int T = 0;
 #pragma unroll
-          for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
-            const float aq = r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * as);
-            lo += (double)h2f(a.h16[(size_t)m * DFSSM_LORA_R + rr]) * (double)aq;
-          }
-          out = r16((float)lo + y);
+    for (int w = 0; w < kNW; ++w) T += L.T[w][m][lane];
+    const int acc = 2 * T - L.S[m];
+    if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = acc;
+    if (a.y_out) {
+      const float y = r16(r16(r16((float)acc) * h2f(xs_raw)) * h2f(ws_raw));
+      float out = y;
+      if (LORA) {
+        const float as = h2f(as_raw);
+        double lo = 0.0;
+#pragma unroll
+        for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
+          const float aq = r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * as);
+          lo += (double)L.hl[m][rr] * (double)aq;
         }
-        a.y_out[(size_t)m * a.N + n] = f2h(out);
+        out = r16((float)lo + y);
       }
+      a.y_out[(size_t)m * a.N + n] = f2h(out);
     }
   }
 }
@@ -632,12 +751,18 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
 
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s) {
   const int groups = (a.N + 63) / 64;
+  if (a.K > kMaxK || a.K % 512 || M < 1 || M > 4) return hipErrorInvalidValue;
+  if (a.xn) {  // LoRA with the intermediates computed in the same launch (M = 1)
+    if (M != 1 || !a.lBq || !a.h_out || !a.lA || !a.lAs || !a.y_out) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((scaffold_fused_kernel<1, true>), dim3(groups), dim3(kNT), 0, s, a);
+    return hipGetLastError();
+  }
+  if (a.lA) return hipErrorInvalidValue;  // LoRA without xn: the GEMM path
   switch (M) {
-    case 1: hipLaunchKernelGGL(scaffold_kernel<1>, dim3(groups), dim3(kNTs), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(scaffold_kernel<2>, dim3(groups), dim3(kNTs), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(scaffold_kernel<3>, dim3(groups), dim3(kNTs), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(scaffold_kernel<4>, dim3(groups), dim3(kNTs), 0, s, a); break;
-    default: return hipErrorInvalidValue;
+    case 1: hipLaunchKernelGGL((scaffold_fused_kernel<1, false>), dim3(groups), dim3(kNT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((scaffold_fused_kernel<2, false>), dim3(groups), dim3(kNT), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((scaffold_fused_kernel<3, false>), dim3(groups), dim3(kNT), 0, s, a); break;
+    default: hipLaunchKernelGGL((scaffold_fused_kernel<4, false>), dim3(groups), dim3(kNT), 0, s, a); break;
   }
   return hipGetLastError();
 }

@@ -38,7 +38,7 @@ def _np16(t):
 
 # ------------------------------------------------------------------------------ config 1
 @pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096)])
-@pytest.mark.parametrize("M", [1, 4, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 32])
 def test_scaffold_lora_op_bit_exact(N, K, M):
     """packed bits with fp16 row scales ~U(0.01, 0.05), int8 activations
     ~N(0, 40) clipped with fp16 per-token scales, rank-16 int8 LoRA A/B; xn is the fp16 vector
