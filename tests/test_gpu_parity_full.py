@@ -120,6 +120,27 @@ def test_2p7b_dims_full_vocab_batch64():
     assert gpu.error_flag() == 0
 
 
+@pytest.mark.parametrize("B", [1, 5])
+def test_largest_vocab_head(B):
+    """The largest supported vocabulary (65536 = 1024 table groups: the most per-workgroup argmax
+    pairs the heads' last workgroup reduces) at B = 1 (head_i8_kernel) and B = 5 (head_i8b_kernel):
+    tokens and final logits identical to the oracle."""
+    c = DFSSMConfig(n_layer=1, d_model=512, d_inner=1024, d_state=128, nheads=16, headdim=64, ngroups=1,
+                    vocab_size=65536, kw=4)
+    w = make_weights(c, seed=11)
+    print(f"V=65536 head, B={B}", flush=True)
+    prompts = make_prompts(B, c.vocab_size, 3)
+    orc = O.OracleModel(w, B)
+    ref, _ = orc.generate(prompts, 3)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    got = gpu.generate(n_tokens=3, prompt=torch.from_numpy(prompts), return_tokens=True, verbose=False)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    lg = _np16(gpu.forward(torch.from_numpy(ref[:, -1]).to(DEV))).astype(np.float32)
+    lo, _ = orc.step(ref[:, -1])
+    assert np.abs(lg - lo.astype(np.float32)).max() == 0.0
+    assert gpu.error_flag() == 0
+
+
 def test_2p7b_layers_prefill_300_chunked():
     """A 300-token prompt through config 4's layer shapes at batch 4, prefilled in chunks of 128
     tokens (two chunk boundaries), against 300 decode steps: state, conv state, next-step input,

@@ -1,8 +1,8 @@
 """Sampling head (dfssm_sample) on the GPU against the oracle's definition (or_sample).
 
 The draw is deterministic for a seed, so the GPU must reproduce the oracle's tokens, occurrence
-counts and step counters exactly: per kernel call on random logits (vocabularies 1000 and
-50288, every parameter combination, several steps) and end to end (sampled generation of a tiny
+counts and step counters exactly: per kernel call on random logits (vocabularies from 7 to the
+largest, 65536, every parameter combination, several steps) and end to end (sampled generation of a tiny
 model against the oracle's decode step followed by or_sample). top_p = 0 must give the greedy
 tokens.
 """
@@ -30,7 +30,9 @@ def _model(V, B):
     return DFSSMModel.from_weights(make_weights(c, seed=3), device=DEV, batch_size=B)
 
 
-@pytest.mark.parametrize("V,B", [(1000, 1), (1000, 5), (50288, 3)])
+# V = 7: one slice workgroup; 513: two ragged slices; 65536: the largest vocabulary (64 slices of
+# 1024 tokens); B = 32: a decode batch
+@pytest.mark.parametrize("V,B", [(7, 2), (513, 3), (1000, 1), (1000, 5), (50288, 3), (50288, 32), (65536, 2)])
 def test_sample_kernel_vs_oracle(V, B):
     print(f"sampler V={V} B={B}", flush=True)
     m = _model(V, B)
