@@ -69,7 +69,7 @@ def algorithmic_bytes(cfg, B):
     return weights, state, per_phase
 
 
-LAYER_KERNELS = {"auto": 0, "fused": 1, "five": 2, "item": 3, "multi": 4}  # dfssm_set_layer_kernel codes
+LAYER_KERNELS = {"auto": 0, "fused": 1, "five": 2, "item": 3, "multi": 4, "xcd": 5}  # dfssm_set_layer_kernel codes
 LAYER_KERNEL = "auto"
 
 

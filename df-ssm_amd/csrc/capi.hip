@@ -34,7 +34,8 @@ Derived derive(const dfssm_dims* d) {
 
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
-      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, total;
+      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, launches_x, proj_x, g_x, h_x,
+      bc_x, dt_x, flag_x, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -77,6 +78,14 @@ WsLayout ws_layout(const dfssm_dims* d) {
   // multi-layer launch of the phase-organised layer: x handed from layer to layer
   w.x_t = off;      off = align_up(off + (size_t)2 * kXRep * kXStride * 4);
   w.ltab = off;     off = align_up(off + (size_t)r.L * sizeof(FusedArgs));  // its per-layer arguments
+  // XCD-partitioned layer: its launch counts and exchange words (per-XCD copies 4 KiB apart)
+  w.launches_x = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
+  w.proj_x = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
+  w.g_x = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
+  w.h_x = off;      off = align_up(off + (size_t)kXcd * kHStride * 4);
+  w.bc_x = off;     off = align_up(off + (size_t)kXcd * kBcStride * 4);
+  w.dt_x = off;     off = align_up(off + (size_t)kXcd * kDtStride * 8);
+  w.flag_x = off;   off = align_up(off + 256);
   w.total = off;
   return w;
 }
@@ -120,7 +129,13 @@ int g_layer_kernel = DFSSM_LAYER_AUTO;
 // item-organised layer 917 us).
 constexpr bool kAutoItem = false;
 constexpr bool kAutoMulti = false;
+constexpr bool kAutoXcd = false;
 
+// Whether the current setting runs the XCD-partitioned one-launch layer for these dimensions.
+bool use_xcd_layer(int B, int D, int DI, int H, int P, int N) {
+  const bool want = g_layer_kernel == DFSSM_LAYER_XCD || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoXcd);
+  return want && xcd_layer_supported(B, D, DI, H, P, N);
+}
 // Whether the current setting runs the item-organised one-launch layer for these dimensions.
 bool use_item_layer(int B, int D, int DI, int H, int P) {
   const bool want = g_layer_kernel == DFSSM_LAYER_ITEM || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoItem);
@@ -177,9 +192,15 @@ int dfssm_one_launch_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
   return fused_plan(cus, blocks_per_cu, blocks_per_cu, r.B, r.IPO, r.D, r.DI, r.H, r.P, nullptr);
 }
 
+int dfssm_xcd_layer_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
+  if (!d || dfssm_check_dims(d) != DFSSM_OK) return 0;
+  const Derived r = derive(d);
+  return xcd_plan(cus, blocks_per_cu, r.B, r.D, r.DI, r.H, r.P, r.N);
+}
+
 int dfssm_set_layer_kernel(int which) {
   if (which != DFSSM_LAYER_AUTO && which != DFSSM_LAYER_FUSED && which != DFSSM_LAYER_FIVE &&
-      which != DFSSM_LAYER_ITEM && which != DFSSM_LAYER_MULTI)
+      which != DFSSM_LAYER_ITEM && which != DFSSM_LAYER_MULTI && which != DFSSM_LAYER_XCD)
     return DFSSM_E_RANGE;
   const int prev = g_layer_kernel;
   g_layer_kernel = which;
@@ -413,6 +434,18 @@ static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const d
                        void* workspace, void* stream) {
   const Derived r = derive(&model->dims);
   FusedArgs a = fused_args(model, layer, x, state, workspace);
+  if (use_xcd_layer(r.B, r.D, r.DI, r.H, r.P, r.N)) {
+    const WsLayout w = ws_layout(&model->dims);
+    char* ws = (char*)workspace;
+    a.launches = (uint32_t*)(ws + w.launches_x);
+    a.projT = (uint32_t*)(ws + w.proj_x);
+    a.gT = (uint32_t*)(ws + w.g_x);
+    a.hT = (uint32_t*)(ws + w.h_x);
+    a.bcT = (uint32_t*)(ws + w.bc_x);
+    a.dtT = (uint64_t*)(ws + w.dt_x);
+    a.xflag = (uint32_t*)(ws + w.flag_x);
+    return hip_status(launch_xcd_layer(a, r.B, as_stream(stream)));
+  }
   if (use_item_layer(r.B, r.D, r.DI, r.H, r.P)) {
     const WsLayout w = ws_layout(&model->dims);
     a.launches = (uint32_t*)((char*)workspace + w.launches1);
@@ -581,7 +614,7 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
   const Derived r = derive(&model->dims);
   const bool one_launch = g_layer_kernel != DFSSM_LAYER_FIVE &&
                           (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P) ||
-                           use_item_layer(r.B, r.D, r.DI, r.H, r.P));
+                           use_item_layer(r.B, r.D, r.DI, r.H, r.P) || use_xcd_layer(r.B, r.D, r.DI, r.H, r.P, r.N));
   if (one_launch) return fused_layer(model, layer, x, state, workspace, stream);
   for (int phase = 0; phase < DFSSM_LAYER_PHASES; ++phase) {
     const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);

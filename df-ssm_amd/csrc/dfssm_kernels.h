@@ -251,6 +251,7 @@ struct FusedArgs {
   int layer, n_layer;
   uint32_t* xT;              // multi-layer launch: 2 x kXRep copies (stride kXStride words) of (M, D)
                              // tagged x words, layer l's output in buffer l % 2
+  uint32_t* xflag;           // XCD-partitioned layer: a tagged word XCD 0 sets once all of g is in
   int D, DI, N, H, P, IPO, C;
 };
 
@@ -268,6 +269,16 @@ constexpr int kXRep = 8;
 constexpr int kHStride = 1024;   // words between copies of hT (>= 2 * 4 * 16)
 constexpr int kBcStride = 1088;  // words between copies of bcT (>= 4 * 256)
 constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
+// The XCD-partitioned one-launch layer (batch <= 4): 8 XCDs x 32 workgroups (one per CU; workgroups
+// go to the XCDs round robin); XCD x owns the SSM heads x H/8 .. (x + 1) H/8 - 1, computes their in_proj
+// rows, the B | C rows and the dt rows itself and exchanges them, and its LoRA intermediates,
+// through its own L2 (XCD-scope words: hT, bcT in copy x, dtT at x kDtStride, projT); only g
+// crosses XCDs. 0 = not usable on this device / shape.
+constexpr int kXcd = 8, kXcdWg = 32, kXcdGrid = kXcd * kXcdWg;
+constexpr int kDtStride = 2 * 4 * 320 + 64;  // u64 words between the XCDs' dt words (>= 2 M H)
+int xcd_plan(int cus, int per_cu, int M, int D, int DI, int H, int P, int N);
+bool xcd_layer_supported(int M, int D, int DI, int H, int P, int N);
+hipError_t launch_xcd_layer(const FusedArgs& a, int M, hipStream_t s);
 constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
 
 // The item-organised one-launch layer (layer1.hip): grid = one workgroup per SSM item (head,

@@ -55,6 +55,7 @@ constexpr int kFMaxCPW = (kFMaxK / 128 + kFW - 1) / kFW;
 template <int RG>
 constexpr int kCR = (2 * (kFMaxK / 128) + kFT / RG - 1) / (kFT / RG);
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kSpinMax = 1u << 18;
 constexpr int kMaxItems = kFW / 2;  // SSM items per workgroup (two polling waves each)
 // at batch M: at most 2 M items per workgroup (the plan checks it), so that the per-item
@@ -65,8 +66,6 @@ constexpr int kItemsOf = 2 * M < kMaxItems ? 2 * M : kMaxItems;
 // waits for that layer's input (true), or only after (false: measured the same per step at batch
 // 1, with less memory traffic while the previous layer's phase C runs).
 constexpr bool kPrefetchNextLayer = false;
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Thread and workgroup index, opaque to the optimizer: addresses derived from them are computed
 // where they are used instead of being hoisted to the kernel start and kept live (in registers)
@@ -89,7 +88,8 @@ __device__ __forceinline__ int bix() {
 #ifdef DFSSM_TIMELINE
 constexpr int kTlSlots = 64, kTlWg = 256, kTlStamps = 16;
 __device__ unsigned long long dfssm_timeline[kTlSlots][kTlWg][kTlStamps];
-#define TL_DECL __shared__ unsigned long long tl_s[kTlStamps]
+__shared__ unsigned long long tl_s[kTlStamps];
+#define TL_DECL
 #define TL(k)                                                                   \
   do {                                                                          \
     if (tix() == 0) tl_s[k] = __builtin_amdgcn_s_memrealtime();                 \
@@ -113,6 +113,34 @@ template <class T>
 __device__ __forceinline__ void st_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// XCD-scope exchange (between workgroups of one XCD, which share its L2): a plain store goes to
+// the L2 (the per-CU L1 is write-through), and a non-temporal load neither allocates in nor hits
+// the per-CU L1, so it reads the L2. Measured two-workgroup round trip 0.5 us, against 0.9 us on
+// one XCD and 1.2 us across XCDs for device-scope (sc1) accesses, which go past the L2. Valid only
+// for words that no CU reads with a plain load in the same launch (a plain load would allocate the
+// line in that CU's L1).
+template <class T>
+__device__ __forceinline__ T ld_xcd(const T* p) {
+  asm volatile("" ::: "memory");  // a fresh load at every call (polls)
+  return __builtin_nontemporal_load(p);
+}
+template <class T>
+__device__ __forceinline__ void st_xcd(T* p, T v) {
+  // a relaxed atomic store of wavefront scope is a plain global store (no cache-policy bits; the
+  // workgroup scope would add sc0), and unlike a plain C++ store it is neither merged nor dropped
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+// Exchange of the one-launch layers: device scope (XL false) or XCD scope (XL true).
+template <bool XL, class T>
+__device__ __forceinline__ T ld_x(const T* p) {
+  if constexpr (XL) return ld_xcd(p);
+  else return ld_dev(p);
+}
+template <bool XL, class T>
+__device__ __forceinline__ void st_x(T* p, T v) {
+  if constexpr (XL) st_xcd(p, v);
+  else st_dev(p, v);
+}
 
 // Words of one SSM item, polled by two waves and shared through LDS.
 struct ItemLds {
@@ -127,6 +155,7 @@ struct FusedLds {
   int T[M][64][kFW + 1];  // per-wave GEMV partials of each row (padded against bank conflicts)
   uint16_t xn[kFMaxK];
   double rd[M][kFW];   // per-wave partial sums (squares; LoRA rank)
+  double rq[M][4][kFW];  // per-wave LoRA sums of up to 4 ranks (XCD-partitioned layer)
   float rf[M][kFW];    // per-wave partial amax
   int ri[M][kFW];      // per-wave partial sum q
   float hl[M][DFSSM_LORA_R];
@@ -153,23 +182,72 @@ struct ConvPend {
   uint16_t v0, v1, v2;
 };
 
-// Activations of columns 8 tid .. 8 tid + 7 (IN only) and their norm weights.
+// Columns of the activation values that thread t < K / 8 holds in the norm and the prologue (K is a
+// multiple of 512, checked with the model dims). Contiguous map (IL false): columns 8 t .. 8 t + 7.
+// Interleaved map (IL true, used where the values are polled): wave w covers columns 512 w ..
+// 512 w + 511 as 256 adjacent pairs, lane l the pairs l, l + 64, l + 128, l + 192, so that each
+// wave-wide poll of one pair is one contiguous 512 bytes of tagged words: a poll round of a
+// workgroup then touches each cache line of the polled words once (with the contiguous map, four
+// times). Threads >= K / 8 map as thread 0 (their values are never used).
+template <bool IL>
+struct PairMap {
+  int base;  // pair j at column base + 128 j (IL) or base + 2 j
+  __device__ __forceinline__ int col(int j) const { return base + (IL ? 128 : 2) * j; }
+};
+template <bool IL>
+__device__ __forceinline__ PairMap<IL> pair_map(int K) {
+  const int t = tix() < K / 8 ? tix() : 0;
+  return PairMap<IL>{IL ? 512 * (t >> 6) + 2 * (t & 63) : 8 * t};
+}
+
+// Activations (IN only) and their norm weights, 4 pairs at pair_map's columns.
 template <int M>
 struct PIn {
   u32x4 av[M];
-  f32x4 w0, w1;
+  f32x4 w0, w1;  // weights of values 0..3 and 4..7 (pairs 0, 1 and 2, 3)
 };
 
-template <int M, bool OUT>
+template <int M, bool OUT, bool IL>
 __device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K, const float* norm_w) {
-  // unconditional loads from a clamped column (threads >= K / 8 re-read column 0; their values
-  // are never used): a load inside a branch makes the compiler wait for all loads at the join
-  const int t = tix() < K / 8 ? tix() : 0;
+  // unconditional loads from a clamped column: a load inside a branch makes the compiler wait for
+  // all loads at the join
+  const PairMap<IL> pm = pair_map<IL>(K);
+  if (IL) {
 #pragma unroll
-  for (int m = 0; m < M; ++m)
-    pi.av[m] = OUT ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(act + (size_t)m * K + 8 * t);
-  pi.w0 = *(const f32x4*)(norm_w + 8 * t);
-  pi.w1 = *(const f32x4*)(norm_w + 8 * t + 4);
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pi.av[m][j] = OUT ? 0u : *(const uint32_t*)(act + (size_t)m * K + pm.col(j));
+    f32x2 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = *(const f32x2*)(norm_w + pm.col(j));
+    pi.w0 = f32x4{w[0][0], w[0][1], w[1][0], w[1][1]};
+    pi.w1 = f32x4{w[2][0], w[2][1], w[3][0], w[3][1]};
+  } else {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      pi.av[m] = OUT ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(act + (size_t)m * K + pm.base);
+    pi.w0 = *(const f32x4*)(norm_w + pm.base);
+    pi.w1 = *(const f32x4*)(norm_w + pm.base + 4);
+  }
+}
+
+// The 4 pairs of this thread at pair_map's columns of an fp16 row in LDS or memory.
+template <bool IL>
+__device__ __forceinline__ u32x4 load_pairs(const uint16_t* row, const PairMap<IL>& pm) {
+  if (!IL) return *(const u32x4*)(row + pm.base);
+  u32x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = *(const uint32_t*)(row + pm.col(j));
+  return v;
+}
+template <bool IL>
+__device__ __forceinline__ void store_pairs(uint16_t* row, const PairMap<IL>& pm, const uint32_t (&o)[4]) {
+  if (!IL) {
+    *(u32x4*)(row + pm.base) = u32x4{o[0], o[1], o[2], o[3]};
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *(uint32_t*)(row + pm.col(j)) = o[j];
 }
 
 __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t* bits, int grp, int K) {
@@ -240,15 +318,16 @@ __device__ __forceinline__ void poll_timeout(bool& ok, int* err) {
   ok = false;
   atomicOr(err, 4);
 }
+template <bool XL = false>
 __device__ __forceinline__ uint32_t poll1(const uint32_t* p, uint32_t tag, bool& ok, int* err) {
-  uint32_t v = ld_dev(p);
+  uint32_t v = ld_x<XL>(p);
   for (uint32_t it = 0; ok && (v >> 16) != tag; ++it) {
     if (it == kSpinMax) {
       poll_timeout(ok, err);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
-    v = ld_dev(p);
+    v = ld_x<XL>(p);
   }
   return v & 0xffffu;
 }
@@ -257,13 +336,13 @@ __device__ __forceinline__ bool tag_ok2(uint64_t v, uint32_t tag) {
 }
 __device__ __forceinline__ uint32_t pack2(uint64_t v) { return ((uint32_t)v & 0xffffu) | ((uint32_t)(v >> 32) << 16); }
 
-// N pairs of adjacent tagged words at p + 2 j (8-byte aligned), all loads in flight together;
+// N pairs of adjacent tagged words at p + 2 S j (8-byte aligned), all loads in flight together;
 // out[j] = the pair's two fp16 values packed low | high.
-template <int N>
+template <int N, int S, bool XL = false>
 __device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t (&out)[N], bool& ok, int* err) {
   uint64_t v[N];
 #pragma unroll
-  for (int j = 0; j < N; ++j) v[j] = ld_dev((const uint64_t*)p + j);
+  for (int j = 0; j < N; ++j) v[j] = ld_x<XL>((const uint64_t*)p + S * j);
   for (uint32_t it = 0; ok; ++it) {
     bool good = true;
 #pragma unroll
@@ -276,7 +355,7 @@ __device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t 
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      if (!tag_ok2(v[j], tag)) v[j] = ld_dev((const uint64_t*)p + j);
+      if (!tag_ok2(v[j], tag)) v[j] = ld_x<XL>((const uint64_t*)p + S * j);
   }
 #pragma unroll
   for (int j = 0; j < N; ++j) out[j] = pack2(v[j]);
@@ -285,7 +364,7 @@ __device__ __forceinline__ void pollv(const uint32_t* p, uint32_t tag, uint32_t 
 // RMSNorm of the M activation rows (K columns) into L.xn, one row at a time, with `body(m, mx)`
 // run after each row's normalized values are in LDS (mx = this thread's max |xn|). IN: x loaded
 // ahead (pi.av); OUT: the gated g of this launch, polled from its tagged words (gT).
-template <int M, bool OUT, class Body>
+template <int M, bool OUT, bool IL, class Body>
 __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K,
                                           uint32_t tag, int* err, Body body) {
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
@@ -298,7 +377,8 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
     if (has_v) {
       if (OUT) {
         uint32_t w4[4];
-        pollv<4>(gT + (size_t)m * K + 8 * tid, tag, w4, ok, err);
+        const PairMap<IL> pm = pair_map<IL>(K);
+        pollv<4, IL ? 64 : 1>(gT + (size_t)m * K + pm.base, tag, w4, ok, err);
         av = u32x4{w4[0], w4[1], w4[2], w4[3]};
       } else {
         av = pi.av[m];
@@ -312,6 +392,7 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
     const double wsum = wave_sum_dpp_f64(part);
     if (lane == 0) L.rd[m][wave] = wsum;
     lds_barrier();  // also: every wave is done with the previous row's xn
+    if (OUT && m == 0) TL(14);
     double ss = 0.0;
 #pragma unroll
     for (int w = 0; w < kFW; ++w) ss += L.rd[m][w];
@@ -327,7 +408,7 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
         mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
         o[e >> 1] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
       }
-      *(u32x4*)&L.xn[8 * tid] = u32x4{o[0], o[1], o[2], o[3]};
+      store_pairs<IL>(L.xn, pair_map<IL>(K), o);
     }
     body(m, mx);
   }
@@ -350,14 +431,15 @@ __device__ __forceinline__ void planes_store64(uint32_t* dst, int q, int lane) {
 // Projection prologue (GEMV workgroups): per row the amax, the quantization scale, and each
 // wave's bit planes of its own GEMV chunks (no barrier before the GEMV) with their sum q.
 // CW: the wave's chunks are CW consecutive ones per round of CW * 16 (those its GEMV reads).
-template <int M, bool OUT, int CW = 1>
+template <int M, bool OUT, bool IL, int CW = 1>
 __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, int K, uint32_t tag, int* err) {
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const int CH = K / 128;
-  norm_rows<M, OUT>(L, pi, gT, K, tag, err, [&](int m, float mx) {
+  norm_rows<M, OUT, IL>(L, pi, gT, K, tag, err, [&](int m, float mx) {
     const float wmax = wave_max_dpp_f32(mx);
     if (lane == 0) L.rf[m][wave] = wmax;
     lds_barrier();  // publishes xn and the partial maxima
+    if (OUT && m == 0) TL(15);
     float amax = L.rf[m][0];
 #pragma unroll
     for (int w = 1; w < kFW; ++w) amax = fmaxf(amax, L.rf[m][w]);
@@ -383,18 +465,18 @@ __device__ void prologue(FusedLds<M>& L, const PIn<M>& pi, const uint32_t* gT, i
 // fp16(sum_k xn_k * Bq[r][k]), fp16 x fp16 products exact in fp32, summed in fp64, stored as a
 // tagged word hout[m * 16 + r] with `tag`. OUT (or a polled x): the activations are polled from
 // gT until they carry `ptag`.
-template <int M, bool OUT>
+template <int M, bool OUT, bool IL>
 __device__ void lora_rank(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT, int K, const float* norm_w,
                           const uint16_t* lBq, int r, uint32_t* hout, uint32_t tag, int* err, uint32_t ptag) {
   const int tid = tix(), lane = tid & 63, wave = tid >> 6;
   const bool has_v = tid < K / 8;
   PIn<M> pi;
-  load_pin<M, OUT>(pi, x, K, norm_w);
-  const u32x4 b8 = has_v ? *(const u32x4*)(lBq + (size_t)r * K + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
-  norm_rows<M, OUT>(L, pi, gT, K, ptag, err, [&](int m, float) {
+  load_pin<M, OUT, IL>(pi, x, K, norm_w);
+  const u32x4 b8 = load_pairs<IL>(lBq + (size_t)r * K, pair_map<IL>(K));
+  norm_rows<M, OUT, IL>(L, pi, gT, K, ptag, err, [&](int m, float) {
     double hacc = 0.0;
     if (has_v) {
-      const u32x4 xv8 = *(const u32x4*)&L.xn[8 * tid];  // this thread's own columns
+      const u32x4 xv8 = load_pairs<IL>(L.xn, pair_map<IL>(K));  // this thread's own columns
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float xv = h2f((uint16_t)(xv8[e >> 1] >> (16 * (e & 1))));
@@ -503,16 +585,18 @@ __device__ __forceinline__ void gemv_partials_rg(FusedLds<M>& L, const u32x2 (&w
 
 // LoRA intermediates of this phase (threads < 16 M): the first load is issued before the GEMV
 // (lora_issue), the poll completes after it (lora_finish) into L.hl; the caller then passes a
-// barrier.
+// barrier. (A second load issued halfway through the GEMV measured no earlier: a device-scope store
+// takes ~1 us to become visible, and the producers store the words shortly before the GEMV starts.)
+template <bool XL = false>
 __device__ __forceinline__ uint32_t lora_issue(const uint32_t* hsrc, int M) {
-  return tix() < M * DFSSM_LORA_R ? ld_dev(hsrc + tix()) : 0u;
+  return tix() < M * DFSSM_LORA_R ? ld_x<XL>(hsrc + tix()) : 0u;
 }
-template <int M>
+template <int M, bool XL = false>
 __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc, uint32_t v, uint32_t tag, int* err) {
   const int tid = tix();
   if (tid < M * DFSSM_LORA_R) {
     bool ok = true;
-    if ((v >> 16) != tag) v = poll1(hsrc + tid, tag, ok, err);
+    if ((v >> 16) != tag) v = poll1<XL>(hsrc + tid, tag, ok, err);
     L.hl[tid / DFSSM_LORA_R][tid % DFSSM_LORA_R] = h2f((uint16_t)v);
   }
 }
@@ -523,9 +607,10 @@ __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc
 // finalizes sequence m. IN: z rows store the gate z sigma(z), x/B/C rows conv + SiLU, dt rows
 // softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x (also kept in
 // *xkeep and, for a next layer of the same launch, published to every copy at xpub).
-template <int M, bool IN, int RG = 64>
+// XL (XCD-partitioned layer): the words go to this XCD's copies with XCD-scope stores.
+template <int M, bool IN, int RG = 64, bool XL = false>
 __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag,
-                             uint32_t* xpub = nullptr, uint32_t* xkeep = nullptr) {
+                             uint32_t* xpub = nullptr, uint32_t* xkeep = nullptr, int xcd = 0) {
   ConvPend cp{nullptr, 0, 0, 0};
   const int tid = tix(), s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
@@ -567,18 +652,22 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
     } else {  // dt row of head dtr
       const float dt = dev_log1pf(dev_expf(out + er.bias));
       const float abar = dev_expf(dt * -dev_expf(er.alog));
-      uint64_t* w = a.dtT + ((size_t)m * a.H + dtr) * 2;
-      st_dev(w, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, dt));
-      st_dev(w + 1, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, abar));
+      uint64_t* w = a.dtT + (XL ? (size_t)xcd * kDtStride : 0) + ((size_t)m * a.H + dtr) * 2;
+      st_x<XL>(w, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, dt));
+      st_x<XL>(w + 1, ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, abar));
       return cp;
     }
     const uint32_t word = tagged(tag, f2h(out));
     const int bc = ch - a.DI;  // B | C channel index, or < 0
     if (bc >= 0) {
+      if (XL) {
+        st_xcd(a.bcT + xcd * kBcStride + m * 2 * a.N + bc, word);
+      } else {
 #pragma unroll
-      for (int c = 0; c < kXRep; ++c) st_dev(a.bcT + c * kBcStride + m * 2 * a.N + bc, word);
+        for (int c = 0; c < kXRep; ++c) st_dev(a.bcT + c * kBcStride + m * 2 * a.N + bc, word);
+      }
     } else {
-      st_dev(a.projT + (size_t)m * a.IPO + n, word);
+      st_x<XL>(a.projT + (size_t)m * a.IPO + n, word);
     }
   } else {
     const uint16_t xv = f2h(h2f((uint16_t)er.xres) + out);
@@ -617,18 +706,19 @@ __device__ __forceinline__ float* state_row(const FusedArgs& a, const Item& t) {
 }
 
 // Poll the words of item k (waves 2k and 2k + 1) into L.item[k]. Wave 2k: B and C (lane l:
-// words 4l .. 4l + 3 of the 256); wave 2k + 1: lanes 0..15 x, 16..31 the gate of the 16 rows,
+// pairs l and 64 + l of the 128); wave 2k + 1: lanes 0..15 x, 16..31 the gate of the 16 rows,
 // lanes 32 and 33 dt and exp(dt A).
-template <int M>
-__device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, uint32_t tag) {
+// XL: from this XCD's copies (xcd), with XCD-scope loads.
+template <int M, bool XL = false>
+__device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item& t, uint32_t tag, int xcd = 0) {
   const int lane = tix() & 63, wave = tix() >> 6;
   const uint32_t* pr = a.projT + (size_t)t.m * a.IPO;
   bool ok = true;
   if (wave == 2 * k) {
-    uint32_t w[2];
-    pollv<2>(a.bcT + (bix() % kXRep) * kBcStride + t.m * 2 * a.N + 4 * lane, tag, w, ok, a.err);
-    L.item[k].bc[2 * lane] = w[0];
-    L.item[k].bc[2 * lane + 1] = w[1];
+    uint32_t w[2];  // pairs lane (B) and 64 + lane (C): each wave-wide load one contiguous 512 bytes
+    pollv<2, 64, XL>(a.bcT + (XL ? xcd : bix() % kXRep) * kBcStride + t.m * 2 * a.N + 2 * lane, tag, w, ok, a.err);
+    L.item[k].bc[lane] = w[0];
+    L.item[k].bc[DFSSM_WAVE + lane] = w[1];
   } else if (wave == 2 * k + 1 && lane < 34) {
     // lanes 0..31 poll 32-bit words (tag in the high half), lanes 32 and 33 64-bit words (tag in
     // the high word), all in one loop so that neither set waits for the other's round trips
@@ -636,18 +726,18 @@ __device__ void poll_item(FusedLds<M>& L, const FusedArgs& a, int k, const Item&
     const bool w32 = lane < 32;
     // every lane loads both kinds (from valid addresses): no divergent loads inside the loop
     const uint32_t* p32 = (lane & 31) < 16 ? pr + a.DI + r0 + (lane & 15) : pr + r0 + (lane & 15);
-    const uint64_t* p64 = a.dtT + ((size_t)t.m * a.H + t.head) * 2 + (lane & 1);
+    const uint64_t* p64 = a.dtT + (XL ? (size_t)xcd * kDtStride : 0) + ((size_t)t.m * a.H + t.head) * 2 + (lane & 1);
     auto ready = [&](uint32_t x, uint64_t y) { return w32 ? (x >> 16) == tag : (uint32_t)(y >> 32) == tag; };
-    uint32_t va = ld_dev(p32);
-    uint64_t vb = ld_dev(p64);
+    uint32_t va = ld_x<XL>(p32);
+    uint64_t vb = ld_x<XL>(p64);
     for (uint32_t it = 0; ok && !ready(va, vb); ++it) {
       if (it == kSpinMax) {
         poll_timeout(ok, a.err);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
-      va = ld_dev(p32);
-      vb = ld_dev(p64);
+      va = ld_x<XL>(p32);
+      vb = ld_x<XL>(p64);
     }
     const uint64_t r = w32 ? (uint64_t)va : vb;
     if (lane < 16) L.item[k].x[lane] = (uint16_t)r;
@@ -672,7 +762,7 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
   hv.x = __builtin_fmaf(I.abar, h0.x, X * h2f((uint16_t)bp));
   hv.y = __builtin_fmaf(I.abar, h0.y, X * h2f((uint16_t)(bp >> 16)));
   double acc = (double)h2f((uint16_t)cp) * (double)hv.x + (double)h2f((uint16_t)(cp >> 16)) * (double)hv.y;
-  __builtin_nontemporal_store(hv, (f32x2*)state_row(a, t));
+  st_dev((uint64_t*)state_row(a, t), __builtin_bit_cast(uint64_t, hv));
   acc = wave_sum_dpp_f64(acc);
   if (lane == 0) {
     const float y = r16((float)acc + xv * Dh);
@@ -787,12 +877,13 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
   EpiRow ea = {};
   PIn<M> pa;
   if (wg < gA) {  // x first: the prologue needs it before the weights
-    load_pin<M, false>(pa, a.x, a.D, a.ln_w);
+    load_pin<M, false, MULTI>(pa, a.x, a.D, a.ln_w);
     load_bits(wa, a.in_bits, wg, a.D);
     ea = load_epi<M, true>(a, wg);
   }
   // state row of this workgroup's first SSM item (the other items' rows load before phase B's polls)
-  // (unconditional, from a clamped item: see load_pin)
+  // (unconditional, from a clamped item: see load_pin). Issuing these and the weights only once x
+  // is in measured slower (the prologue waits as long for x, and then for the weights).
   const f32x2 h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg < items ? wg : items - 1)));
   if constexpr (MULTI && kPrefetchNextLayer) {
     if (poll_x) {
@@ -803,8 +894,8 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
 
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
   if (wg < gA) {
-    if (poll_x) prologue<M, true>(L, pa, x_src, a.D, tag_of_layer(l - 1), a.err);
-    else prologue<M, false>(L, pa, nullptr, a.D, 0u, a.err);  // x loaded ahead, no polls
+    if (poll_x) prologue<M, true, MULTI>(L, pa, x_src, a.D, tag_of_layer(l - 1), a.err);
+    else prologue<M, false, MULTI>(L, pa, nullptr, a.D, 0u, a.err);  // x loaded ahead, no polls
     TL(1);
     for (int grp = wg; grp < gA; grp += G) {
       if (grp != wg) {
@@ -824,10 +915,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
     }
   } else if (wg < gA + DFSSM_LORA_R) {
     if (poll_x)
-      lora_rank<M, true>(L, nullptr, x_src, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err,
+      lora_rank<M, true, MULTI>(L, nullptr, x_src, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err,
                          tag_of_layer(l - 1));
     else
-      lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err, 0u);
+      lora_rank<M, false, MULTI>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err, 0u);
     TL(4);
   }
   // ---- phase B: SSM + gate ----
@@ -867,10 +958,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
   if (wg < gC) {
     lds_barrier();  // LDS reuse after phase A
     PIn<M> pc;
-    load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
+    load_pin<M, true, true>(pc, nullptr, a.DI, a.norm_w);
     const uint32_t tag = tag_now();
     TL(8);
-    prologue<M, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);  // the chunks of the wave's GEMV
+    prologue<M, true, true, RC == 16 ? 2 : 1>(L, pc, a.gT, a.DI, tag, a.err);  // the chunks of the wave's GEMV
     TL(9);
     for (int grp = wg; grp < gC; grp += G) {
       if (grp != wg) {
@@ -891,7 +982,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
     }
   } else if (wg < gC + DFSSM_LORA_R) {
     lds_barrier();
-    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err, tag_now());
+    lora_rank<M, true, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err, tag_now());
     TL(12);
   }
   lds_barrier();  // LDS reuse by the next layer; every wave has read the launch count
@@ -903,6 +994,238 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a0, const Fu
   }
   if (tix() == 0) st_dev(a0.launches + bix(), epoch_raw + 1u);
 }
+
+// ---------------------------------------------------------------------------------------------
+// XCD-partitioned one-launch layer (batch <= 4). Grid: 8 XCDs x 32 workgroups, one per CU;
+// workgroup w runs on XCD x (its XCC_ID register; w % 8 up to a rotation that varies by dispatch)
+// with local index i = w / 8. XCD x owns the SSM heads x H/8 .. (x + 1) H/8 - 1 and every word its
+// items need is produced on x itself and exchanged through x's L2 (XCD-scope stores and
+// non-temporal loads, ~2x faster than device scope); only g crosses XCDs (device scope).
+//   A  i < 2 gz: the z and x row groups of x's heads (gz = H/8 P / 64 groups each); then the
+//      gbc = 4 B | C groups and the dt groups holding x's heads (computed on every XCD), then
+//      4..16 LoRA-rank workgroups (16 / their number ranks each). The B | C conv state is updated
+//      by XCD 0 only, in phase C, once all of g is in: every item's g needs its XCD's B | C rows,
+//      so by then every XCD's B | C workgroups have read the old state.
+//   B  local item j (sequence, head, 16-row block of x's heads) on workgroup j % 32.
+//   C  i < gc = D / 256: out_proj rows 32 (x gc + i) .. + 31 (g polled device-scope); the last 4
+//      workgroups of the XCD: the out_proj LoRA intermediates, 4 ranks each.
+constexpr int kXRankC = 4;  // out_proj LoRA-rank workgroups per XCD (4 ranks each)
+
+__device__ __forceinline__ int xcc_id() {
+  return (int)(__builtin_amdgcn_s_getreg(20 | ((4 - 1) << 11)) & 0xfu);  // HW_REG_XCC_ID bits 3:0
+}
+
+// Local SSM item j of XCD x: (sequence, head, 16-row block) over x's heads.
+__device__ __forceinline__ Item xcd_item(const FusedArgs& a, int xcd, int j) {
+  const int hx = a.H / kXcd, PB = a.P / 16, per = hx * PB;
+  const int m = j / per, rem = j - m * per;
+  return Item{m, xcd * hx + rem / PB, rem % PB};
+}
+
+// LoRA intermediates of ranks r0 .. r0 + nr - 1 (nr <= 4) for every row, as lora_rank, stored once
+// (to this XCD's words) with XCD scope.
+template <int M, bool OUT, bool IL>
+__device__ void lora_ranks(FusedLds<M>& L, const uint16_t* x, const uint32_t* gT, int K, const float* norm_w,
+                           const uint16_t* lBq, int r0, int nr, uint32_t* hout, uint32_t tag, int* err,
+                           uint32_t ptag) {
+  const int tid = tix(), lane = tid & 63, wave = tid >> 6;
+  const bool has_v = tid < K / 8;
+  PIn<M> pi;
+  load_pin<M, OUT, IL>(pi, x, K, norm_w);
+  u32x4 b8[4];  // ranks past nr re-read rank r0 (unused)
+#pragma unroll
+  for (int q = 0; q < 4; ++q) b8[q] = load_pairs<IL>(lBq + (size_t)(r0 + (q < nr ? q : 0)) * K, pair_map<IL>(K));
+  norm_rows<M, OUT, IL>(L, pi, gT, K, ptag, err, [&](int m, float) {
+    double hacc[4] = {0.0, 0.0, 0.0, 0.0};
+    if (has_v) {
+      const u32x4 xv8 = load_pairs<IL>(L.xn, pair_map<IL>(K));  // this thread's own columns
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = h2f((uint16_t)(xv8[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hacc[q] += (double)(xv * h2f((uint16_t)(b8[q][e >> 1] >> (16 * (e & 1)))));
+      }
+    }
+    double hw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hw[q] = q < nr ? wave_sum_dpp_f64(hacc[q]) : 0.0;
+    lds_barrier();  // the sum-of-squares partials of this row have been read by every wave
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) L.rq[m][q][wave] = hw[q];
+    }
+    lds_barrier();
+    if (tid < nr) {
+      double t = 0.0;
+#pragma unroll
+      for (int w = 0; w < kFW; ++w) t += L.rq[m][tid][w];
+      st_xcd(hout + m * DFSSM_LORA_R + r0 + tid, tagged(tag, f2h((float)t)));
+    }
+  });
+}
+
+template <int M>
+__global__ __launch_bounds__(kFT) void layer_xcd_kernel(FusedArgs a) {
+  __shared__ FusedLds<M> L;
+  TL_DECL;
+  const uint32_t epoch_raw = ld_dev(a.launches + bix());
+  auto tag_now = [&]() {  // derived where used (see layer_fused_kernel)
+    uint32_t v = epoch_raw;
+    asm volatile("" : "+v"(v));
+    return (v * (uint32_t)a.n_layer + (uint32_t)a.layer + 1u) & 0xffffu;
+  };
+  // XCD from the hardware: workgroups go to the XCDs round robin, but the first one's XCD varies
+  // from dispatch to dispatch (under graph replay workgroup 0 ran on XCD 7), so workgroup w runs on
+  // XCD (w + c) % 8 for some c; (XCC_ID, w / 8) is then one (XCD, local index) pair per workgroup.
+  // (Another placement would leave a role without a workgroup: its consumers' waits time out.)
+  const int wg = bix(), xcd = xcc_id(), li = wg / kXcd;
+#ifdef DFSSM_TIMELINE
+  if (tix() < kTlStamps) tl_s[tix()] = 0ull;
+  lds_barrier();
+#endif
+  TL(0);
+  const int hx = a.H / kXcd, PB = a.P / 16;
+  const int gz = hx * a.P / 64, gbc = 2 * a.N / 64;
+  const int dt0 = xcd * hx / 64, gdt = ((xcd + 1) * hx - 1) / 64 - dt0 + 1;  // dt groups of x's heads
+  const int nga = 2 * gz + gbc + gdt;
+  const int nra = nga + 16 <= kXcdWg ? 16 : (nga + 8 <= kXcdWg ? 8 : 4), rpa = DFSSM_LORA_R / nra;
+  const int gc = a.D / (kXcd * 32);
+  int grpA = -1;
+  if (li < gz) grpA = xcd * gz + li;
+  else if (li < 2 * gz) grpA = a.DI / 64 + xcd * gz + (li - gz);
+  else if (li < 2 * gz + gbc) grpA = 2 * a.DI / 64 + (li - 2 * gz);
+  else if (li < nga) grpA = (2 * a.DI + 2 * a.N) / 64 + dt0 + (li - 2 * gz - gbc);
+  const bool bcA = li >= 2 * gz && li < 2 * gz + gbc;
+  uint32_t* hA = a.hT + xcd * kHStride;  // this XCD's LoRA words: in_proj (M, 16), then out_proj
+  uint32_t* hC = hA + M * DFSSM_LORA_R;
+  const int nloc = M * hx * PB;
+  const int nk = li < nloc ? (nloc - 1 - li) / kXcdWg + 1 : 0;  // <= kItemsOf<M> (the plan checks it)
+
+  // ---- loads that do not depend on the activations ----
+  u32x4 wa[kFMaxCPW];
+  EpiRow ea = {};
+  PIn<M> pa;
+  if (grpA >= 0) {  // x first: the prologue needs it before the weights
+    load_pin<M, false, false>(pa, a.x, a.D, a.ln_w);
+    load_bits(wa, a.in_bits, grpA, a.D);
+    ea = load_epi<M, true>(a, grpA);
+  }
+  const f32x2 h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, xcd_item(a, xcd, li < nloc ? li : 0)));
+
+  // ---- phase A: in_proj row groups, LoRA ranks ----
+  ConvPend cpA{nullptr, 0, 0, 0};  // XCD 0: this thread's B | C conv-state update, stored in phase C
+  if (grpA >= 0) {
+    prologue<M, false, false>(L, pa, nullptr, a.D, 0u, a.err);
+    TL(1);
+    const uint32_t hv = lora_issue<true>(hA, M);
+    gemv_partials<M>(L, wa, a.D);
+    TL(2);
+    const uint32_t tag = tag_now();
+    lora_finish<M, true>(L, hA, hv, tag, a.err);
+    lds_barrier();
+    TL(3);
+    const ConvPend cp = epilogue<M, true, 64, true>(L, a, ea, grpA, tag, nullptr, nullptr, xcd);
+    if (!bcA) store_conv(cp);
+    else if (xcd == 0) cpA = cp;
+    TL(4);
+    lds_barrier();
+  } else if (li < nga + nra) {
+    lora_ranks<M, false, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, (li - nga) * rpa, rpa, hA, tag_now(), a.err,
+                                0u);
+    TL(4);
+  }
+  // ---- phase B: SSM + gate of this XCD's items ----
+  const int grpC = li < gc ? xcd * gc + li : -1;
+  u32x2 wcr[kCR<32>];
+  EpiRow ec = {};
+  if (grpC >= 0) {  // phase-C weights, loaded while phase B runs
+    load_bits_rg<32>(wcr, a.out_bits, grpC, a.DI);
+    ec = load_epi<M, false, 32>(a, grpC);
+  }
+  if (nk > 0) {
+    f32x2 hk[kItemsOf<M>];
+    float dk[kItemsOf<M>];
+    hk[0] = h0;
+#pragma unroll
+    for (int k = 0; k < kItemsOf<M>; ++k) {
+      if (k < nk) {
+        const Item t = xcd_item(a, xcd, li + k * kXcdWg);
+        if (k > 0) hk[k] = __builtin_nontemporal_load((const f32x2*)state_row(a, t));
+        dk[k] = a.Dp[t.head];
+      }
+    }
+    const uint32_t tag = tag_now();
+    TL(5);
+    for (int k = 0; k < nk; ++k) poll_item<M, true>(L, a, k, xcd_item(a, xcd, li + k * kXcdWg), tag, xcd);
+    lds_barrier();
+    TL(6);
+#pragma unroll
+    for (int k = 0; k < kItemsOf<M>; ++k)
+      if (k < nk) ssm_item<M>(L, a, k, xcd_item(a, xcd, li + k * kXcdWg), hk[k], dk[k], tag);
+  }
+  TL(7);
+  // ---- phase C: out_proj + residual, LoRA ranks ----
+  if (grpC >= 0) {
+    lds_barrier();  // LDS reuse after phases A and B
+    PIn<M> pc;
+    load_pin<M, true, true>(pc, nullptr, a.DI, a.norm_w);
+    const uint32_t tag = tag_now();
+    TL(8);
+    prologue<M, true, true, 1>(L, pc, a.gT, a.DI, tag, a.err);
+    TL(9);
+    if (xcd == 0 && li == 0 && tix() == 0) st_xcd(a.xflag, tagged(tag, 0));  // every g word is in
+    const uint32_t hv = lora_issue<true>(hC, M);
+    gemv_partials_rg<M, 32>(L, wcr, a.DI);
+    TL(10);
+    lora_finish<M, true>(L, hC, hv, tag, a.err);
+    lds_barrier();
+    TL(11);
+    (void)epilogue<M, false, 32, true>(L, a, ec, grpC, tag);
+    TL(12);
+    lds_barrier();
+  } else if (li >= kXcdWg - kXRankC) {
+    lds_barrier();
+    lora_ranks<M, true, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, (li - (kXcdWg - kXRankC)) * 4, 4, hC,
+                              tag_now(), a.err, tag_now());
+    TL(12);
+  } else if (cpA.p) {  // XCD 0's B | C workgroups (idle in phase C: the plan checks it)
+    bool ok = true;
+    (void)poll1<true>(a.xflag, tag_now(), ok, a.err);
+    store_conv(cpA);
+  }
+  lds_barrier();
+  TL(13);
+#ifdef DFSSM_TIMELINE
+  if (tix() == 0) tl_s[15] = 1000ull + xcc_id();  // profiling builds: the XCD this workgroup ran on
+  lds_barrier();
+  TL_FLUSH(epoch_raw * (uint32_t)a.n_layer + (uint32_t)a.layer);
+#endif
+  if (tix() == 0) st_dev(a.launches + bix(), epoch_raw + 1u);
+}
+
+// Grid of the XCD-partitioned layer, or 0: the device must have exactly 8 x 32 CUs with the
+// instantiation resident once per CU; per XCD the phase-A row groups plus at least 4 LoRA-rank
+// workgroups fit in 32, the out_proj groups (D / 256 of 32 rows) come before the B | C workgroups
+// and those before the last 4 (the phase-C rank workgroups), so that the B | C workgroups are idle
+// in phase C; a workgroup polls at most 2 M (and kMaxItems) items.
+int xcd_plan(int cus, int per_cu, int M, int D, int DI, int H, int P, int N) {
+  if (cus != kXcdGrid || per_cu < 1 || M < 1 || M > 4 || N != 128) return 0;
+  if (D > kFMaxK || DI > kFMaxK || H % kXcd || P % 16 || D % (kXcd * 32)) return 0;
+  const int hx = H / kXcd;
+  if ((hx * P) % 64) return 0;
+  const int gz = hx * P / 64, gbc = 2 * N / 64;
+  int gdt = 1;
+  for (int x = 0; x < kXcd; ++x) {
+    const int g = ((x + 1) * hx - 1) / 64 - x * hx / 64 + 1;
+    gdt = g > gdt ? g : gdt;
+  }
+  const int nga = 2 * gz + gbc + gdt, gc = D / (kXcd * 32);
+  if (nga + 4 > kXcdWg || gc > 2 * gz || 2 * gz + gbc > kXcdWg - kXRankC) return 0;
+  const int per_wg = (M * hx * (P / 16) + kXcdWg - 1) / kXcdWg;
+  if (per_wg > (2 * M < kMaxItems ? 2 * M : kMaxItems)) return 0;
+  return kXcdGrid;
+}
+
 
 // The one-launch layer waits between its workgroups, so all G of them must be resident at once:
 // G = one workgroup per CU (at most kFusedMaxGrid), which holds only if the launched
@@ -938,11 +1261,21 @@ static int occupancy_of() {
   return per_cu;
 }
 
+template <int M>
+static int xcd_occupancy() {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&layer_xcd_kernel<M>), kFT,
+                                                   0) != hipSuccess)
+    return 0;
+  return per_cu;
+}
+
 // Device facts for the plan, queried once per device: CU count and, per batch M = 1..4, the
 // occupancy of both row-group instantiations, single-layer [0] and multi-layer [1].
 struct FusedDev {
   int cus = -1;
   int per_cu[5][2][2] = {};
+  int xcd_per_cu[5] = {};  // layer_xcd_kernel<M>
 };
 
 static const FusedDev* fused_dev() {
@@ -958,6 +1291,8 @@ static const FusedDev* fused_dev() {
   d.per_cu[MM][0][1] = occupancy_of<MM, 32, true>(); d.per_cu[MM][1][1] = occupancy_of<MM, 64, true>();
     DFSSM_OCC(1) DFSSM_OCC(2) DFSSM_OCC(3) DFSSM_OCC(4)
 #undef DFSSM_OCC
+    d.xcd_per_cu[1] = xcd_occupancy<1>(); d.xcd_per_cu[2] = xcd_occupancy<2>();
+    d.xcd_per_cu[3] = xcd_occupancy<3>(); d.xcd_per_cu[4] = xcd_occupancy<4>();
     d.cus = cus;
   }
   return &d;
@@ -971,6 +1306,27 @@ static int fused_grid(int M, int IPO, int D, int DI, int H, int P, int* rc, bool
 
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P, bool multi) {
   return fused_grid(M, IPO, D, DI, H, P, nullptr, multi) > 0;
+}
+
+static int xcd_grid(int M, int D, int DI, int H, int P, int N) {
+  const FusedDev* d = fused_dev();
+  if (!d || M < 1 || M > 4) return 0;
+  return xcd_plan(d->cus, d->xcd_per_cu[M], M, D, DI, H, P, N);
+}
+
+bool xcd_layer_supported(int M, int D, int DI, int H, int P, int N) { return xcd_grid(M, D, DI, H, P, N) > 0; }
+
+hipError_t launch_xcd_layer(const FusedArgs& a, int M, hipStream_t s) {
+  const int G = xcd_grid(M, a.D, a.DI, a.H, a.P, a.N);
+  if (G < 1 || a.xflag == nullptr) return hipErrorNotSupported;
+  switch (M) {
+    case 1: hipLaunchKernelGGL(layer_xcd_kernel<1>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(layer_xcd_kernel<2>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(layer_xcd_kernel<3>, dim3(G), dim3(kFT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(layer_xcd_kernel<4>, dim3(G), dim3(kFT), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // out[r][k] = fp16(B[r][k] * Bs[r]), the load-time LoRA-B dequantization.

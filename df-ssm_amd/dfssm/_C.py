@@ -54,6 +54,7 @@ _SIGS = {
     "dfssm_error_string": (ctypes.c_char_p, [c_int]),
     "dfssm_check_dims": (c_int, [ctypes.POINTER(Dims)]),
     "dfssm_one_launch_plan": (c_int, [ctypes.POINTER(Dims), c_int, c_int]),
+    "dfssm_xcd_layer_plan": (c_int, [ctypes.POINTER(Dims), c_int, c_int]),
     "dfssm_set_layer_kernel": (c_int, [c_int]),
     "dfssm_tiled_bits_bytes": (c_size_t, [c_int, c_int]),
     "dfssm_tiled_emb_bytes": (c_size_t, [c_int, c_int]),

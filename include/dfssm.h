@@ -88,6 +88,11 @@ int dfssm_check_dims(const dfssm_dims* dims);
  * rule can be checked without a GPU. No counterpart in the reference (its layers are separate
  * kernel launches, df_ssm_inference.py:161-207). */
 int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
+/* Grid of the XCD-partitioned one-launch layer (DFSSM_LAYER_XCD) for these dims on a device with
+ * `cus` CUs where `blocks_per_cu` of its workgroups fit per CU, or 0 when that layer cannot run
+ * (it needs exactly 8 XCDs x 32 CUs, batch <= 4 and a shape whose per-XCD roles fit 32 workgroups).
+ * Exposed so that the rule can be checked without a GPU. No counterpart in the reference. */
+int dfssm_xcd_layer_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
 
 /* Layer kernel selection for dfssm_layer_step / dfssm_decode_step (process-wide; returns the
  * previous setting, or DFSSM_E_RANGE). At batch <= 4: DFSSM_LAYER_FUSED runs the
@@ -96,15 +101,18 @@ int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
  * power of two <= 256) where the shape allows it, else as DFSSM_LAYER_FUSED;
  * DFSSM_LAYER_MULTI lets dfssm_decode_step run all layers of a step in one launch of the
  * phase-organised layer (when every per-layer weight pointer is equally spaced from layer to
- * layer, as one allocation per field gives), else as DFSSM_LAYER_FUSED; DFSSM_LAYER_FIVE always
- * runs five kernels per layer; DFSSM_LAYER_AUTO (default) is the fastest on the benchmark
- * shape (DFSSM_LAYER_FUSED). All give bit-identical results; the setting exists to compare them.
- * No counterpart in the reference. */
+ * layer, as one allocation per field gives), else as DFSSM_LAYER_FUSED; DFSSM_LAYER_XCD runs the
+ * XCD-partitioned one-launch layer (8 XCDs x 32 workgroups, each XCD owning 1/8 of the SSM heads
+ * and exchanging its words through its own L2; needs exactly 256 CUs) where the device and the
+ * shape allow it, else as DFSSM_LAYER_FUSED; DFSSM_LAYER_FIVE always runs five kernels per layer;
+ * DFSSM_LAYER_AUTO (default) is the fastest on the benchmark shape (DFSSM_LAYER_FUSED). All give
+ * bit-identical results; the setting exists to compare them. No counterpart in the reference. */
 #define DFSSM_LAYER_AUTO 0
 #define DFSSM_LAYER_FUSED 1
 #define DFSSM_LAYER_FIVE 2
 #define DFSSM_LAYER_ITEM 3
 #define DFSSM_LAYER_MULTI 4
+#define DFSSM_LAYER_XCD 5
 int dfssm_set_layer_kernel(int which);
 /* 1 when dfssm_decode_step runs all layers of a step in one launch with the current setting on
  * the current device (batch <= 4, a shape the phase-organised layer takes, per-layer weights

@@ -32,12 +32,29 @@ def test_one_launch_plan(kw, cus, per_cu, grid):
     assert _C.lib().dfssm_one_launch_plan(_dims(**kw), cus, per_cu) == grid
 
 
+@pytest.mark.parametrize("kw,cus,per_cu,grid", [
+    ({}, 256, 1, 256),                 # 1.3B shape on MI355X: 8 XCDs x 32 CUs
+    ({"batch": 4}, 256, 1, 256),
+    ({}, 256, 0, 0),                   # the instantiation does not fit a CU
+    ({}, 304, 1, 0),                   # not 8 x 32 CUs
+    ({"batch": 5}, 256, 1, 0),         # batch >= 5: five kernels
+    ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 256, 1, 256),   # 2.7B: 26 phase-A groups per XCD
+    ({"d_model": 512, "d_inner": 1024, "nheads": 16}, 256, 1, 256),    # the tests' tiny model
+    ({"d_model": 4096, "d_inner": 4096}, 256, 1, 256),                 # 16 out_proj groups per XCD
+    ({"d_model": 512, "d_inner": 1024, "nheads": 32}, 256, 1, 256),    # 4 heads x 32 rows per XCD: 2 row groups
+    ({"d_model": 5120, "d_inner": 5120, "nheads": 80}, 256, 1, 256),   # 20 out_proj groups = 2 x 10 z groups
+    ({"d_model": 4096, "d_inner": 2048, "nheads": 32}, 256, 1, 0),     # 16 out_proj groups > 2 x 4 z groups
+])
+def test_xcd_layer_plan(kw, cus, per_cu, grid):
+    assert _C.lib().dfssm_xcd_layer_plan(_dims(**kw), cus, per_cu) == grid
+
+
 def test_describe_error_flag():
     assert dfi.describe_error_flag(0) == ""
     assert "token id out of range" in dfi.describe_error_flag(dfi.ERR_TOKEN_RANGE)
     assert "timed out" in dfi.describe_error_flag(dfi.ERR_WAIT_TIMEOUT)
-    both = dfi.describe_error_flag(dfi.ERR_TOKEN_RANGE | dfi.ERR_WAIT_TIMEOUT | 8)
-    assert "out of range" in both and "timed out" in both and "0x8" in both
+    both = dfi.describe_error_flag(dfi.ERR_TOKEN_RANGE | dfi.ERR_WAIT_TIMEOUT | 16)
+    assert "out of range" in both and "timed out" in both and "0x10" in both
 
 
 def _hostless_model(B=2):

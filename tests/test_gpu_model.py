@@ -110,15 +110,25 @@ def test_1p3b_greedy(w13, B, T, n):
     assert gpu.error_flag() == 0
 
 
-@pytest.mark.parametrize("kernel", [3, 1])   # DFSSM_LAYER_ITEM, DFSSM_LAYER_FUSED
+def _require_xcd_layer(gpu, kernel):
+    """The XCD-partitioned layer (kernel 5) must really run for these dims on this device."""
+    from dfssm import _C
+    if kernel == 5:
+        props = torch.cuda.get_device_properties(0)
+        assert _C.lib().dfssm_xcd_layer_plan(gpu.dims, props.multi_processor_count, 1) == 256
+
+
+@pytest.mark.parametrize("kernel", [3, 1, 5])   # DFSSM_LAYER_ITEM, DFSSM_LAYER_FUSED, DFSSM_LAYER_XCD
 @pytest.mark.parametrize("B", [1, 3])
 def test_one_launch_layer_equals_five_kernels(tiny_weights, B, kernel):
-    """dfssm_layer_step (one launch at batch <= 4: the item-organised layer, or the
-    phase-organised one) against dfssm_layer_phase 0..4 (the five-kernel form) on the same
-    inputs: x, SSM state and conv state identical bit for bit."""
+    """dfssm_layer_step (one launch at batch <= 4: the item-organised layer, the phase-organised
+    one or the XCD-partitioned one) against dfssm_layer_phase 0..4 (the five-kernel form) on the
+    same inputs: x, SSM state and conv state identical bit for bit."""
     from dfssm import _C
     w = tiny_weights
+    print(f"one-launch kernel {kernel} B={B}", flush=True)
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    _require_xcd_layer(gpu, kernel)
     gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, 5)))  # non-trivial state
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
@@ -165,6 +175,22 @@ def _decode_run(w, B, kernel, steps, prompt_len=5):
 
 
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
+def test_xcd_layer_decode_equals_five_kernels(tiny_weights, B):
+    """dfssm_decode_step with the XCD-partitioned layer (DFSSM_LAYER_XCD) against the five-kernel
+    form, 6 greedy steps: logits, tokens, x and both states identical bit for bit."""
+    print(f"xcd decode B={B}", flush=True)
+    one_x, out_x, x_x, h_x, c_x = _decode_run(tiny_weights, B, 5, 6)
+    one_5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
+    assert one_x == 0 and one_5 == 0
+    for (lx, nx), (l5, n5) in zip(out_x, out_5):
+        assert torch.equal(lx.view(torch.int16), l5.view(torch.int16))
+        assert torch.equal(nx, n5)
+    assert torch.equal(x_x.view(torch.int16), x_5.view(torch.int16))
+    assert torch.equal(h_x, h_5)
+    assert torch.equal(c_x.view(torch.int16), c_5.view(torch.int16))
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 4])
 def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
     """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
     from layer to layer as tagged words) against the five-kernel form, 6 steps: logits, tokens,
@@ -182,7 +208,7 @@ def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
     assert torch.equal(c_m.view(torch.int16), c_5.view(torch.int16))
 
 
-@pytest.mark.parametrize("kernel", [3, 1])
+@pytest.mark.parametrize("kernel", [3, 1, 5])
 @pytest.mark.parametrize("B", [1, 4])
 def test_one_launch_layer_wide_model(B, kernel):
     """d_model 4096 (128 out_proj groups of 32 rows, the widest grid use): the one-launch layer
@@ -192,8 +218,9 @@ def test_one_launch_layer_wide_model(B, kernel):
     c = DFSSMConfig(n_layer=1, d_model=4096, d_inner=4096, d_state=128, nheads=64, headdim=64, ngroups=1,
                     vocab_size=1000, kw=4)
     w = make_weights(c, seed=5)
-    print(f"wide one-launch B={B}", flush=True)
+    print(f"wide one-launch kernel {kernel} B={B}", flush=True)
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    _require_xcd_layer(gpu, kernel)
     gpu.ingest(torch.from_numpy(make_prompts(B, c.vocab_size, 3)))
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
