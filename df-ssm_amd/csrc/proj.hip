@@ -37,23 +37,27 @@ constexpr int kPW = kPT / 64;
 struct PrepLds {
   uint16_t xn[kMaxK];
   double red_d[kPW];
+  double red_h[2][kPW];  // per-wave LoRA sums of the workgroup's ranks
   float red_f[kPW];
   int red_i[kPW];
 };
 
-// 16 M workgroups (more when M is not a multiple of 8) x K/8 threads (8 columns each; K is a
-// multiple of 512, so whole waves): workgroup (r, m) recomputes the normalization and quantization of row m, writes the q bytes (and for the
-// bit-plane GEMV the planes) of column slice r (K/16 columns) and the LoRA intermediate h[m][r];
-// workgroup (0, m) also writes sum q (when asked) and the scale. Three LDS reductions: the sum of
-// squares, then the LoRA sum and the maximum together, then (workgroup 0, when asked) sum q.
-template <int MODE>
+// 16 M / R workgroups (more when M is not a multiple of 8) x K/8 threads (8 columns each; K is a
+// multiple of 512, so whole waves): workgroup (r, m) recomputes the normalization and quantization
+// of row m, writes the q bytes (and for the bit-plane GEMV the planes) of column slice r (R K/16
+// columns) and the LoRA intermediates h[m][R r .. R r + R - 1]; workgroup (0, m) also writes sum q
+// (when asked) and the scale. R = 1, or 2 when 16 workgroups per row would not all be resident at
+// once. Three LDS reductions: the sum of squares, then the LoRA sums and the maximum together,
+// then (workgroup 0, when asked) sum q.
+template <int MODE, int R>
 __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
   __shared__ PrepLds L;
-  // workgroup -> (rank rr, row m): workgroups are dealt to the 8 XCDs in turn, and XCD x takes
-  // the rows m = x (mod 8) with all 16 ranks of each, so a row (read by all 16 of its
+  constexpr int NR = DFSSM_LORA_R / R;  // workgroups per row
+  // workgroup -> (rank group, row m): workgroups are dealt to the 8 XCDs in turn, and XCD x takes
+  // the rows m = x (mod 8) with all rank groups of each, so a row (read by all of its
   // workgroups) is fetched into one XCD's L2 rather than into all eight
   const int x8 = (int)blockIdx.x & 7, j8 = (int)blockIdx.x >> 3;
-  const int m = 8 * (j8 / DFSSM_LORA_R) + x8, rr = j8 % DFSSM_LORA_R;
+  const int m = 8 * (j8 / NR) + x8, rg = j8 % NR, rr = R * rg;
   if (m >= M) return;  // uniform over the workgroup
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int K = a.K, NT = (int)blockDim.x, nw = NT >> 6;
@@ -67,8 +71,13 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
   const u32x4 av = *(const u32x4*)(act + 8 * tid);
   const f32x4 w0 = *(const f32x4*)(a.norm_w + 8 * tid);
   const f32x4 w1 = *(const f32x4*)(a.norm_w + 8 * tid + 4);
-  const uint2 b8 = *(const uint2*)((a.lB ? a.lB + (size_t)rr * K : (const int8_t*)act) + 8 * tid);
-  const uint16_t bs_raw = *(a.lB ? a.lBs + rr : act);
+  uint2 b8[R];
+  uint16_t bs_raw[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    b8[q] = *(const uint2*)((a.lB ? a.lB + (size_t)(rr + q) * K : (const int8_t*)act) + 8 * tid);
+    bs_raw[q] = *(a.lB ? a.lBs + rr + q : act);
+  }
   double part = 0.0;
   if (MODE == DFSSM_MODE_IN) {
 #pragma unroll
@@ -90,40 +99,52 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
   const float var = (float)ss * (1.0f / (float)K);
   const float r = 1.0f / sqrt_rn(var + 1e-5f);
   const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-  const float bs = a.lB ? h2f(bs_raw) : 0.0f;
   float mx = 0.0f;
-  double hacc = 0.0;
+  double hacc[R];
   uint32_t o[4];
   {
-    const uint32_t bw[2] = {b8.x, b8.y};
+#pragma unroll
+    for (int q = 0; q < R; ++q) hacc[q] = 0.0;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
       const float x0 = r16((h2f((uint16_t)(av[e >> 1])) * r) * wv[e]);
       const float x1 = r16((h2f((uint16_t)(av[e >> 1] >> 16)) * r) * wv[e + 1]);
       mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
       o[e >> 1] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
-      // LoRA intermediate of rank r over this thread's 8 columns (fp16 x fp16 is exact in fp32)
-      const float b0 = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
-      const float b1 = r16((float)(int8_t)(bw[(e + 1) >> 2] >> (8 * ((e + 1) & 3))) * bs);
-      hacc += (double)(x0 * b0);
-      hacc += (double)(x1 * b1);
+      // LoRA intermediates of ranks rr .. rr + R - 1 over this thread's 8 columns (fp16 x fp16 is
+      // exact in fp32)
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const float bs = a.lB ? h2f(bs_raw[q]) : 0.0f;
+        const uint32_t bw[2] = {b8[q].x, b8[q].y};
+        const float b0 = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
+        const float b1 = r16((float)(int8_t)(bw[(e + 1) >> 2] >> (8 * ((e + 1) & 3))) * bs);
+        hacc[q] += (double)(x0 * b0);
+        hacc[q] += (double)(x1 * b1);
+      }
     }
     *(u32x4*)&L.xn[8 * tid] = u32x4{o[0], o[1], o[2], o[3]};
   }
-  {  // LoRA sum and maximum in one exchange (the first barrier: every wave has read the squares)
-    const double hw = wave_sum_dpp_f64(hacc);
+  {  // LoRA sums and maximum in one exchange (the first barrier: every wave has read the squares)
+    double hw[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) hw[q] = wave_sum_dpp_f64(hacc[q]);
     const float mw = wave_max_dpp_f32(mx);
     lds_barrier();
     if (lane == 0) {
-      L.red_d[w] = hw;
+#pragma unroll
+      for (int q = 0; q < R; ++q) L.red_h[q][w] = hw[q];
       L.red_f[w] = mw;
     }
   }
   lds_barrier();  // also publishes xn
-  double ht = 0.0;
+  double ht[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) ht[q] = 0.0;
   float amax = L.red_f[0];
   for (int i = 0; i < nw; ++i) {
-    ht += L.red_d[i];
+#pragma unroll
+    for (int q = 0; q < R; ++q) ht[q] += L.red_h[q][i];
     amax = fmaxf(amax, L.red_f[i]);
   }
   const float xs = quant_scale(amax);
@@ -132,7 +153,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
   // of the 64-column wave blocks that start in slice rr (slices narrower than 64 columns, K < 1024,
   // leave every other workgroup nothing to write). Global stores come last: a wave with a store
   // outstanding waits for its acknowledgement wherever a later load must be complete.
-  const int lo = rr * (K / 16), hi = lo + K / 16;
+  const int lo = rr * (K / 16), hi = lo + R * (K / 16);
   const bool want_sum = a.s_out != nullptr;
   int qsum = 0;
   for (int k0 = 64 * w; k0 < K; k0 += NT) {
@@ -150,7 +171,10 @@ __global__ __launch_bounds__(kPT) void prep_kernel(PrepArgs a, int M) {
     }
   }
   if (a.xn_out && rr == 0) *(u32x4*)(a.xn_out + (size_t)m * K + 8 * tid) = u32x4{o[0], o[1], o[2], o[3]};
-  if (a.lB && tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + rr] = r16((float)ht);
+  if (a.lB && tid == 0) {
+#pragma unroll
+    for (int q = 0; q < R; ++q) a.h_out[(size_t)m * DFSSM_LORA_R + rr + q] = r16((float)ht[q]);
+  }
   if (rr == 0) {
     int S = 0;
     if (want_sum) {
@@ -742,10 +766,26 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
       hipLaunchKernelGGL(prep_rows_kernel<DFSSM_MODE_OUT>, g, dim3(a.K / 8), 0, s, a, M);
     return hipGetLastError();
   }
-  if (mode == DFSSM_MODE_IN)
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_IN>, dim3(8 * DFSSM_LORA_R * ((M + 7) / 8)), dim3(a.K / 8), 0, s, a, M);
-  else
-    hipLaunchKernelGGL(prep_kernel<DFSSM_MODE_OUT>, dim3(8 * DFSSM_LORA_R * ((M + 7) / 8)), dim3(a.K / 8), 0, s, a, M);
+  // 16 workgroups of K / 8 threads per row while they are all resident at once (at most 32 waves
+  // per CU: 1024 workgroups of 640 threads at batch 64 and K = 5120 would take 1.3 rounds of the
+  // CUs), else 2 ranks per workgroup
+  int cus = 256;
+  {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess)
+      cus = 256;
+  }
+  const long long waves = 16LL * ((M + 7) / 8 * 8) * (a.K / 512);
+  const bool two = waves > 32LL * cus;
+  const dim3 g(8 * (two ? DFSSM_LORA_R / 2 : DFSSM_LORA_R) * ((M + 7) / 8));
+  if (mode == DFSSM_MODE_IN) {
+    if (two) hipLaunchKernelGGL((prep_kernel<DFSSM_MODE_IN, 2>), g, dim3(a.K / 8), 0, s, a, M);
+    else hipLaunchKernelGGL((prep_kernel<DFSSM_MODE_IN, 1>), g, dim3(a.K / 8), 0, s, a, M);
+  } else {
+    if (two) hipLaunchKernelGGL((prep_kernel<DFSSM_MODE_OUT, 2>), g, dim3(a.K / 8), 0, s, a, M);
+    else hipLaunchKernelGGL((prep_kernel<DFSSM_MODE_OUT, 1>), g, dim3(a.K / 8), 0, s, a, M);
+  }
   return hipGetLastError();
 }
 
