@@ -474,6 +474,33 @@ def timeline(B, path, graphs=4):
     return out
 
 
+def decode_only(B, path, shape, graphs):
+    """Only the decode step: a seeded 8-token prompt ingested, then `graphs` replays of the 8-step
+    decode graph (HIP events around them), nothing else -- the run to trace with rocprofv3 for the
+    kernels' durations inside the decode step (the per-kernel timing graphs of time_kernels run one
+    kernel back to back, which can rank variants differently)."""
+    import torch
+    from dfssm.synth import make_prompts
+    m, _ = build_model(B, path, shape=shape)
+    m.ingest(torch.from_numpy(make_prompts(B, m.cfg.vocab_size, 8)))
+    g, _ = m._gen_graph(STEPS_PER_GRAPH)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(graphs):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    if m.error_flag():
+        raise RuntimeError(f"decode reported error flag {m.error_flag():#x}")
+    us = e0.elapsed_time(e1) * 1e3 / (graphs * STEPS_PER_GRAPH)
+    log(f"decode only, {shape} batch {B}: {us:.1f} us/step, {B * 1e6 / us:.0f} tok/s ({graphs} graphs of "
+        f"{STEPS_PER_GRAPH} steps)")
+    return {"shape": shape, "batch": B, "us_per_step": round(us, 1), "tok_s": round(B * 1e6 / us, 1)}
+
+
 def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
     """Decode throughput and per-kernel timing at batch B (one model instance)."""
     import torch
@@ -629,6 +656,9 @@ def main():
                          "from the profiling build libdfssm_hip_timeline.so")
     ap.add_argument("--layer-kernel", choices=sorted(LAYER_KERNELS), default="auto",
                     help="layer kernel at batch <= 4 (dfssm_set_layer_kernel; auto: the library's default)")
+    ap.add_argument("--decode-only", type=int, default=0,
+                    help="only replay the decode graph this many times at --batch (and --shape), for kernel traces")
+    ap.add_argument("--shape", choices=("1p3b", "2p7b"), default="1p3b", help="model shape of --decode-only")
     a = ap.parse_args()
     global LAYER_KERNEL
     LAYER_KERNEL = a.layer_kernel
@@ -640,6 +670,10 @@ def main():
         return
     if a.timeline:
         print(json.dumps(timeline(a.timeline, a.model_path)), flush=True)
+        return
+    if a.decode_only:
+        path = a.model_path if a.shape == "1p3b" else a.model_path_2p7b
+        print(json.dumps(decode_only(a.batch, path, a.shape, a.decode_only)), flush=True)
         return
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
