@@ -35,7 +35,7 @@ Derived derive(const dfssm_dims* d) {
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
       proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, launches_x, proj_x, g_x, h_x,
-      bc_x, dt_x, flag_x, total;
+      bc_x, dt_x, flag_x, g_s, launches_s, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -86,6 +86,9 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.bc_x = off;     off = align_up(off + (size_t)kXcd * kBcStride * 4);
   w.dt_x = off;     off = align_up(off + (size_t)kXcd * kDtStride * 8);
   w.flag_x = off;   off = align_up(off + 256);
+  // batch >= 5: the SSM + gated-norm prologue launch's tagged g words and launch counts
+  w.g_s = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
+  w.launches_s = off; off = align_up(off + (size_t)(r.DI / 16 + 16) * r.B * 4);  // 16 LoRA ranks
   w.total = off;
   return w;
 }
@@ -607,6 +610,33 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
   return hip_status(launch_proj(a, r.B, DFSSM_MODE_OUT, s));
 }
 
+// Phases 2 and 3 of dfssm_layer_phase in one launch (batch >= 5): the SSM step + gate, with the
+// gated-norm prologue of out_proj computed by workgroups of the same launch.
+static int ssm_prep_layer(const dfssm_model* model, int layer, const dfssm_state* state, void* workspace,
+                          void* stream) {
+  const Derived r = derive(&model->dims);
+  const dfssm_layer& Lw = model->layers[layer];
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  uint16_t* proj = (uint16_t*)(ws + w.proj);
+  SsmPrepArgs a{};
+  a.s.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
+  a.s.xbc = proj + r.DI; a.s.ld_xbc = r.IPO;
+  a.s.dt = proj + r.DI + r.C; a.s.ld_dt = r.IPO;
+  a.s.z = proj; a.s.ld_z = r.IPO;
+  a.s.dt_bias = Lw.dt_bias; a.s.A_log = Lw.A_log; a.s.D = Lw.D;
+  a.s.H = r.H; a.s.P = r.P; a.s.N = r.N;
+  a.gT = (uint32_t*)(ws + w.g_s);
+  a.launches = (uint32_t*)(ws + w.launches_s);
+  a.err = (int*)(ws + w.err);
+  a.norm_w = Lw.norm_w;
+  a.lB = Lw.out_lB; a.lBs = Lw.out_lB_s;
+  a.q_out = (int8_t*)(ws + w.q); a.ld_q = r.D > r.DI ? r.D : r.DI;
+  a.xs_out = (float*)(ws + w.xs);
+  a.h_out = (float*)(ws + w.h);
+  return hip_status(launch_ssm_prep(a, r.B, as_stream(stream)));
+}
+
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream) {
   int rc = check_layer_args(model, layer, x, state, workspace);
@@ -616,6 +646,16 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
                           (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P) ||
                            use_item_layer(r.B, r.D, r.DI, r.H, r.P) || use_xcd_layer(r.B, r.D, r.DI, r.H, r.P, r.N));
   if (one_launch) return fused_layer(model, layer, x, state, workspace, stream);
+  if (r.B > 4 && g_layer_kernel != DFSSM_LAYER_FIVE && ssm_prep_supported(r.B, r.DI, r.P)) {
+    // four launches: prologue + in_proj, SSM with the out_proj prologue, out_proj
+    for (int phase : {0, 1}) {
+      rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
+      if (rc) return rc;
+    }
+    rc = ssm_prep_layer(model, layer, state, workspace, stream);
+    if (rc) return rc;
+    return dfssm_layer_phase(model, layer, 4, x, state, workspace, stream);
+  }
   for (int phase = 0; phase < DFSSM_LAYER_PHASES; ++phase) {
     const int rc = dfssm_layer_phase(model, layer, phase, x, state, workspace, stream);
     if (rc) return rc;

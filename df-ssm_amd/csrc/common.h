@@ -15,6 +15,16 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 ld_nt(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
 __device__ __forceinline__ f32x4 ld_nt_f4(const float* p) { return __builtin_nontemporal_load((const f32x4*)p); }
 __device__ __forceinline__ void st_nt_f4(float* p, f32x4 v) { __builtin_nontemporal_store(v, (f32x4*)p); }
+// Device-scope (agent) coherent 32/64-bit accesses: they go past the L2 of the issuing XCD, so a
+// word stored by a workgroup on one XCD is seen by a load on another without any cache flush.
+template <class T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(f16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }  // RNE

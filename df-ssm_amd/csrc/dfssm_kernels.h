@@ -126,6 +126,26 @@ struct SsmArgs {
   int H, P, N;
 };
 
+// Decode at batch >= 5: the SSM step + gate (SsmArgs, whose y_out and sumsq_slots are unused) and
+// the gated-norm prologue of out_proj (prep_kernel<OUT>'s outputs) in one launch. The gated g
+// travels between the launch's workgroups as tagged words (tag << 16) | fp16 in gT.
+struct SsmPrepArgs {
+  SsmArgs s;
+  uint32_t* gT;              // (M, H P) tagged words, rewritten by every launch
+  uint32_t* launches;        // ((H P / 16 + 16) M) per-workgroup launch counts, zeroed at init
+  int* err;                  // bit 2: a wait timed out
+  const float* norm_w;       // (H P) fp32 gated-RMSNorm weight
+  const int8_t* lB;          // (16, H P) LoRA B, int8 (null: no LoRA intermediate)
+  const uint16_t* lBs;       // (16) fp16
+  int8_t* q_out;             // (M, ld_q) int8 activations
+  int ld_q;
+  float* xs_out;             // (M) activation scale (an fp16 value)
+  float* h_out;              // (M, 16) LoRA intermediate (fp16 values)
+};
+// Whether launch_ssm_prep takes these dimensions (K = H P <= 5120, a multiple of 512; P % 16 == 0).
+bool ssm_prep_supported(int M, int K, int P);
+hipError_t launch_ssm_prep(const SsmPrepArgs& a, int M, hipStream_t s);
+
 struct ConvArgs {
   uint16_t* state;           // (M, C, 3) fp16
   uint16_t* x;               // (M, ld) fp16, in place

@@ -105,14 +105,6 @@ __shared__ unsigned long long tl_s[kTlStamps];
 #define TL_FLUSH(slot) do {} while (0)
 #endif
 
-template <class T>
-__device__ __forceinline__ T ld_dev(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ void st_dev(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // XCD-scope exchange (between workgroups of one XCD, which share its L2): a plain store goes to
 // the L2 (the per-CU L1 is write-through), and a non-temporal load neither allocates in nor hits
 // the per-CU L1, so it reads the L2. Measured two-workgroup round trip 0.5 us, against 0.9 us on

@@ -190,6 +190,23 @@ def test_xcd_layer_decode_equals_five_kernels(tiny_weights, B):
     assert torch.equal(c_x.view(torch.int16), c_5.view(torch.int16))
 
 
+@pytest.mark.parametrize("B", [5, 16, 64])
+def test_batched_ssm_prologue_launch_equals_five_kernels(tiny_weights, B):
+    """Batch >= 5: dfssm_decode_step with the default setting (the SSM step and the out_proj
+    prologue in one launch, g handed over as tagged words) against DFSSM_LAYER_FIVE (separate SSM
+    and prologue kernels), 6 greedy steps: logits, tokens, x and both states identical bit for bit."""
+    print(f"ssm+prologue decode B={B}", flush=True)
+    one_a, out_a, x_a, h_a, c_a = _decode_run(tiny_weights, B, 0, 6)
+    one_5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
+    assert one_a == 0 and one_5 == 0
+    for (la, na), (l5, n5) in zip(out_a, out_5):
+        assert torch.equal(la.view(torch.int16), l5.view(torch.int16))
+        assert torch.equal(na, n5)
+    assert torch.equal(x_a.view(torch.int16), x_5.view(torch.int16))
+    assert torch.equal(h_a, h_5)
+    assert torch.equal(c_a.view(torch.int16), c_5.view(torch.int16))
+
+
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
 def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
     """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
