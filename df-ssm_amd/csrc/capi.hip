@@ -35,7 +35,7 @@ Derived derive(const dfssm_dims* d) {
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
       proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, launches_x, proj_x, g_x, h_x,
-      bc_x, dt_x, flag_x, g_s, launches_s, total;
+      bc_x, dt_x, flag_x, g_s, launches_s, x_s, launches_o, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -89,6 +89,9 @@ WsLayout ws_layout(const dfssm_dims* d) {
   // batch >= 5: the SSM + gated-norm prologue launch's tagged g words and launch counts
   w.g_s = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
   w.launches_s = off; off = align_up(off + (size_t)(r.DI / 16 + 16) * r.B * 4);  // 16 LoRA ranks
+  // batch >= 5: the out_proj launch with the next layer's prologue, its tagged x words and counts
+  w.x_s = off;      off = align_up(off + (size_t)r.B * r.D * 4);
+  w.launches_o = off; off = align_up(off + (size_t)kGemmProMaxWg * 4);
   w.total = off;
   return w;
 }
@@ -520,6 +523,32 @@ int dfssm_decode_one_launch(const dfssm_model* model) {
   return all_layers_one_launch(model, st) ? 1 : 0;
 }
 
+// Arguments of the matrix-core in_proj (in) or out_proj GEMM of `layer` (batch >= 5).
+static GemmArgs batched_gemm_args(const dfssm_model* model, int layer, bool in, uint16_t* x, const dfssm_state* state,
+                                  void* workspace) {
+  const Derived r = derive(&model->dims);
+  const dfssm_layer& Lw = model->layers[layer];
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  GemmArgs a{};
+  a.q = (const int8_t*)(ws + w.q); a.ld_q = r.D > r.DI ? r.D : r.DI; a.M = r.B;
+  a.xs = (const float*)(ws + w.xs);
+  a.h = (const float*)(ws + w.h);
+  if (in) {
+    a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
+    a.out = (uint16_t*)(ws + w.proj); a.ld_out = r.IPO;
+    a.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
+    a.conv_w = Lw.conv_w; a.conv_b = Lw.conv_b;
+    a.conv_lo = r.DI; a.conv_c = r.C;
+    a.N = r.IPO; a.K = r.D;
+  } else {
+    a.bits = Lw.out_bits; a.wscale = Lw.out_scale; a.lA = Lw.out_lA; a.lAs = Lw.out_lA_s;
+    a.out = x; a.ld_out = r.D;
+    a.N = r.D; a.K = r.DI;
+  }
+  return a;
+}
+
 int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
                       const dfssm_state* state, void* workspace, void* stream) {
   int rc = check_layer_args(model, layer, x, state, workspace);
@@ -570,22 +599,7 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
   }
   const bool in = phase == 1;
   if (r.B > 4) {  // int8 matrix-core path
-    GemmArgs a{};
-    a.q = (const int8_t*)(ws + w.q); a.ld_q = kq; a.M = r.B;
-    a.xs = (const float*)(ws + w.xs);
-    a.h = (const float*)(ws + w.h);
-    if (in) {
-      a.bits = Lw.in_bits; a.wscale = Lw.in_scale; a.lA = Lw.in_lA; a.lAs = Lw.in_lA_s;
-      a.out = proj; a.ld_out = r.IPO;
-      a.conv_state = state->conv + (size_t)layer * r.B * r.C * 3;
-      a.conv_w = Lw.conv_w; a.conv_b = Lw.conv_b;
-      a.conv_lo = r.DI; a.conv_c = r.C;
-      a.N = r.IPO; a.K = r.D;
-    } else {
-      a.bits = Lw.out_bits; a.wscale = Lw.out_scale; a.lA = Lw.out_lA; a.lAs = Lw.out_lA_s;
-      a.out = x; a.ld_out = r.D;
-      a.N = r.D; a.K = r.DI;
-    }
+    const GemmArgs a = batched_gemm_args(model, layer, in, x, state, workspace);
     return hip_status(launch_gemm(a, in ? DFSSM_MODE_IN : DFSSM_MODE_OUT, s));
   }
   ProjArgs a{};
@@ -697,6 +711,50 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   return DFSSM_OK;
 }
 
+// The layers of a decode step, launch by launch. Batch >= 5 (unless DFSSM_LAYER_FIVE): per layer
+// the in_proj GEMM, the SSM launch with out_proj's prologue, and the out_proj launch with the
+// next layer's in_proj prologue (the first layer's runs on its own), three launches instead of
+// five; other batches layer by layer as dfssm_layer_step.
+static int decode_layers(const dfssm_model* model, uint16_t* x, const dfssm_state* state, void* workspace,
+                         void* stream) {
+  const Derived r = derive(&model->dims);
+  int rc = DFSSM_OK;
+  if (r.B <= 4 || g_layer_kernel == DFSSM_LAYER_FIVE || !ssm_prep_supported(r.B, r.DI, r.P)) {
+    for (int l = 0; l < r.L && !rc; ++l) rc = dfssm_layer_step(model, l, x, state, workspace, stream);
+    return rc;
+  }
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  bool prepped = false;  // the q, scale and LoRA intermediates of this layer's in_proj are written
+  for (int l = 0; l < r.L; ++l) {
+    if (!prepped && (rc = dfssm_layer_phase(model, l, 0, x, state, workspace, stream))) return rc;
+    if ((rc = dfssm_layer_phase(model, l, 1, x, state, workspace, stream))) return rc;
+    if ((rc = ssm_prep_layer(model, l, state, workspace, stream))) return rc;
+    prepped = false;
+    if (l + 1 < r.L) {
+      const dfssm_layer& Ln = model->layers[l + 1];
+      GemmPro p{};
+      p.xT = (uint32_t*)(ws + w.x_s);
+      p.launches = (uint32_t*)(ws + w.launches_o);
+      p.err = (int*)(ws + w.err);
+      p.norm_w = Ln.ln_w;
+      p.lB = Ln.in_lB; p.lBs = Ln.in_lB_s;
+      p.q_out = (int8_t*)(ws + w.q); p.ld_q = r.D > r.DI ? r.D : r.DI;
+      p.xs_out = (float*)(ws + w.xs);
+      p.h_out = (float*)(ws + w.h);
+      const hipError_t e =
+          launch_gemm_out_pro(batched_gemm_args(model, l, false, x, state, workspace), p, as_stream(stream));
+      if (e == hipSuccess) {
+        prepped = true;
+        continue;
+      }
+      if (e != hipErrorNotSupported) return hip_status(e);
+    }
+    if ((rc = dfssm_layer_phase(model, l, 4, x, state, workspace, stream))) return rc;
+  }
+  return DFSSM_OK;
+}
+
 int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
                       const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
                       int fuse_next_embed, void* stream) {
@@ -709,10 +767,8 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
   }
   rc = fused_all_layers(model, x, state, workspace, stream);
   if (rc == DFSSM_E_DIMS) {
-    for (int l = 0; l < model->dims.n_layer; ++l) {
-      rc = dfssm_layer_step(model, l, x, state, workspace, stream);
-      if (rc) return rc;
-    }
+    rc = decode_layers(model, x, state, workspace, stream);
+    if (rc) return rc;
   } else if (rc) {
     return rc;
   }

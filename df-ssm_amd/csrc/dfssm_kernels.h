@@ -79,7 +79,29 @@ struct GemmArgs {
   int conv_lo, conv_c;
   int N, K;
 };
-constexpr int kGemmMaxRows = 32768;  // activation rows of one gemm_kernel launch (prefill)
+constexpr int kGemmMaxRows = 32768;
+// Decode at batch >= 5: the next layer's in_proj prologue (prep_kernel<IN>'s outputs) computed
+// by M extra workgroups of the out_proj launch, after every GEMM workgroup, from the new x rows
+// handed over as tagged words (tag << 16) | fp16.
+struct GemmPro {
+  uint32_t* xT;              // (M, N) tagged words of the new x, rewritten by every launch
+  uint32_t* launches;        // per-workgroup launch counts (kGemmProMaxWg), zeroed at init
+  int* err;                  // bit 2: a wait timed out
+  const float* norm_w;       // (N) fp32 RMSNorm weight of the next layer
+  const int8_t* lB;          // (16, N) its LoRA B, int8 (null: no LoRA intermediate)
+  const uint16_t* lBs;       // (16) fp16
+  int8_t* q_out;             // (M, ld_q) int8 activations
+  int ld_q;
+  float* xs_out;             // (M) activation scale (an fp16 value)
+  float* h_out;              // (M, 16) LoRA intermediate (fp16 values)
+  int gy;                    // set by the launch: grid rows of GEMM workgroups (prologues follow)
+};
+constexpr int kGemmProMaxWg = 4096;  // workgroups of one out_proj launch with the prologue
+// out_proj (MODE_OUT) with the next layer's prologue; hipErrorNotSupported (nothing launched) for
+// a shape it does not take (M > 64, N not a multiple of 512 or above 5120, a grid beyond
+// kGemmProMaxWg), so the caller runs the two kernels instead
+hipError_t launch_gemm_out_pro(const GemmArgs& a, const GemmPro& p, hipStream_t s);
+  // activation rows of one gemm_kernel launch (prefill)
 
 struct ScaffoldArgs {
   const uint32_t* bits;      // tiled sign bits

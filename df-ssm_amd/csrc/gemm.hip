@@ -40,8 +40,130 @@ __host__ __device__ constexpr size_t gemm_lora_bytes(int MI, int RT) {
   return (size_t)((16 / RT) / MI < 4 ? (16 / RT) / MI : 4) * RT * MI * 4 * 64 * 8;
 }
 
-template <int MI, int RT, int MODE>
-__global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
+// ---- the next layer's in_proj prologue in the out_proj launch (PRO; decode, batch >= 5) ----
+// Four workgroups (16 waves) per sequence m, placed after every GEMM workgroup; workgroup k polls
+// the row of the new x (D = N columns) from the tagged words the GEMM epilogues publish, computes
+// RMSNorm (fp64 sum of squares), the maximum and the scale, writes the q bytes of columns
+// k D / 4 .. (k + 1) D / 4 - 1, and computes the LoRA intermediates of ranks 4 k .. 4 k + 3: wave w
+// sums rank 4 k + w / 4 over column quarter w % 4 (lane l: 8-column blocks 64 i + l of the quarter)
+// from the normalized row in LDS -- prep_kernel<IN>'s outputs; every sum is a sum of exact
+// products in fp64. (One workgroup per sequence, all 16 ranks, took 3.8 us more per layer: these
+// workgroups inherit the GEMM's LDS, one per CU, so a row's 16 dot products ran on one CU.)
+// Waiting: every GEMM workgroup comes before them in dispatch order and never waits, so every
+// wait ends; every wait is also bounded (bit 2 of err on a timeout).
+constexpr int kProPW = 4;   // prologue workgroups per sequence
+constexpr int kProPJ = 3;   // column pairs per thread at most (N / 2 <= 2560 over 1024 threads)
+constexpr int kProBI = 3;   // 8-column blocks per lane of a quarter at most (N / 32 <= 160 over 64 lanes)
+constexpr int kProPF = 4;   // 16-byte prefetch vectors per thread of the next layer's prologue weights
+__device__ __forceinline__ bool pro_tag_ok(uint64_t v, uint32_t tag) {
+  return ((uint32_t)v >> 16) == tag && ((uint32_t)(v >> 32) >> 16) == tag;
+}
+__device__ __forceinline__ void gemm_in_prologue(const GemmPro& p, int D, int m, int k, uint32_t tag, uint32_t* xn2) {
+  __shared__ double pr_d[16];
+  __shared__ float pr_f[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int np = D / 2, nbq = D / 32;  // column pairs; 8-column blocks per quarter
+  const int rr = kProPW * k + (w >> 2), c0 = (w & 3) * (D / 4);
+  // norm weights of this thread's pairs u = tid + 1024 j and the LoRA-B bytes of rank rr over the
+  // wave's quarter first, then x
+  float2 wv[kProPJ];
+#pragma unroll
+  for (int j = 0; j < kProPJ; ++j) {
+    const int u = tid + 1024 * j;
+    wv[j] = u < np ? *(const float2*)(p.norm_w + 2 * u) : make_float2(0.0f, 0.0f);
+  }
+  const int8_t* lb = p.lB ? p.lB + (size_t)rr * D + c0 : nullptr;
+  uint2 bq[kProBI];
+#pragma unroll
+  for (int i = 0; i < kProBI; ++i) {
+    const int b = 64 * i + lane;
+    bq[i] = (lb && b < nbq) ? *(const uint2*)(lb + 8 * b) : uint2{0u, 0u};
+  }
+  const float bs = p.lB ? h2f(p.lBs[rr]) : 0.0f;
+  const uint64_t* xp = (const uint64_t*)(p.xT + (size_t)m * D) + tid;
+  uint64_t xv[kProPJ];
+#pragma nounroll
+  for (uint32_t it = 0;; ++it) {
+#pragma unroll
+    for (int j = 0; j < kProPJ; ++j) xv[j] = tid + 1024 * j < np ? ld_dev(xp + 1024 * j) : 0ull;
+    bool good = true;
+#pragma unroll
+    for (int j = 0; j < kProPJ; ++j) good = good && (tid + 1024 * j >= np || pro_tag_ok(xv[j], tag));
+    if (good) break;
+    if (it == (1u << 18)) {
+      atomicOr(p.err, 4);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  double part = 0.0;
+#pragma unroll
+  for (int j = 0; j < kProPJ; ++j) {
+    if (tid + 1024 * j >= np) break;
+    const double x0 = (double)h2f((uint16_t)xv[j]), x1 = (double)h2f((uint16_t)(xv[j] >> 32));
+    part += x0 * x0;
+    part += x1 * x1;
+  }
+  {  // sum of squares (fp64: the sums are exact)
+    const double pw = wave_sum_dpp_f64(part);
+    if (lane == 0) pr_d[w] = pw;
+  }
+  lds_barrier();
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss += pr_d[i];
+  const float r = 1.0f / sqrt_rn((float)ss * (1.0f / (float)D) + 1e-5f);
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kProPJ; ++j) {
+    const int u = tid + 1024 * j;
+    if (u >= np) break;
+    const float x0 = r16((h2f((uint16_t)xv[j]) * r) * wv[j].x);
+    const float x1 = r16((h2f((uint16_t)(xv[j] >> 32)) * r) * wv[j].y);
+    mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
+    xn2[u] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+  }
+  {
+    const float mw = wave_max_dpp_f32(mx);
+    if (lane == 0) pr_f[w] = mw;
+  }
+  lds_barrier();  // publishes xn and the maxima (every wave has read the squares before it)
+  float amax = pr_f[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) amax = fmaxf(amax, pr_f[i]);
+  const float xs = quant_scale(amax);
+  const float rinv = quant_rcp(xs);
+  // rank rr over this wave's quarter (fp16 x fp16 is exact in fp32)
+  double hacc = 0.0;
+#pragma unroll
+  for (int i = 0; i < kProBI; ++i) {
+    const int b = 64 * i + lane;
+    if (b >= nbq) break;
+    const u32x4 x8 = *(const u32x4*)&xn2[(c0 >> 1) + 4 * b];
+    const uint32_t bw[2] = {bq[i].x, bq[i].y};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = h2f((uint16_t)(x8[e >> 1] >> (16 * (e & 1))));
+      const float bv = r16((float)(int8_t)(bw[e >> 2] >> (8 * (e & 3))) * bs);
+      hacc += (double)(x * bv);
+    }
+  }
+  {  // per-wave partials into pr_d (its sums of squares were read before the last barrier)
+    const double hw = wave_sum_dpp_f64(hacc);
+    if (lane == 0) pr_d[w] = hw;
+  }
+  const uint16_t* xn = (const uint16_t*)xn2;
+  for (int c = k * (D / 4) + tid; c < (k + 1) * (D / 4); c += kGT)
+    p.q_out[(size_t)m * p.ld_q + c] = (int8_t)quant_i8(h2f(xn[c]), rinv);
+  lds_barrier();  // publishes the partials
+  if (tid < kProPW && p.lB)
+    p.h_out[(size_t)m * DFSSM_LORA_R + kProPW * k + tid] =
+        r16((float)((pr_d[4 * tid] + pr_d[4 * tid + 1]) + (pr_d[4 * tid + 2] + pr_d[4 * tid + 3])));
+  if (tid == 0 && k == 0) p.xs_out[m] = xs;
+}
+
+template <int MI, int RT, int MODE, bool PRO>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   constexpr int MP = MI * 16;  // activation rows per block
   constexpr int KQ = 16 / RT;  // k slots
   constexpr int kKMax = MI == 2 ? 4096 : 5120;  // the host picks MI = 2 only for K <= 4096
@@ -53,7 +175,23 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   __shared__ float hl[MP][DFSSM_LORA_R];
   __shared__ float xsl[MP];
   __shared__ uint32_t zero_s;  // read back as 0 in every row block (see below)
+  __shared__ uint32_t tag_s;  // PRO: this launch's tag
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // PRO: launch count of this workgroup (read at the start, advanced once its tag is known)
+  uint32_t* cnt = nullptr;
+  uint32_t epoch = 0;
+  if constexpr (PRO) {
+    cnt = p.launches + (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+    if ((int)blockIdx.y >= p.gy) {  // prologue workgroups
+      const int pi = ((int)blockIdx.y - p.gy) * (int)gridDim.x + (int)blockIdx.x;
+      const uint32_t ep = ld_dev(cnt);
+      if (pi < kProPW * a.M) gemm_in_prologue(p, a.N, pi / kProPW, pi % kProPW, (ep + 1u) & 0xffffu, (uint32_t*)qs);
+      lds_barrier();  // every wave has used its tag before the count is advanced
+      if (tid == 0) st_dev(cnt, ep + 1u);
+      return;
+    }
+    if (tid == 0) epoch = ld_dev(cnt);
+  }
   const int rt = wave % RT, kq = wave / RT, j = lane >> 4;
   const int g = blockIdx.x;
   const int K = a.K, CH = K / 128;
@@ -149,6 +287,26 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
   // partial LoRA terms [slot][rt][ib][e][lane] (fp64), after the int32 partials in the dynamic LDS
   double* lod = (double*)(qs + gemm_part_bytes(MI, RT));
   if (tid == 0) zero_s = 0u;
+  if (PRO && tid == 0) {  // read by every thread after the loop's barriers
+    tag_s = (epoch + 1u) & 0xffffu;
+    st_dev(cnt, epoch + 1u);
+  }
+  // PRO: the next layer's prologue weights (norm weights and LoRA-B table, 20 N bytes, the first
+  // 64 KiB of them) into every XCD's L2 -- workgroups 0..7 are dealt one to each XCD -- so the
+  // prologue workgroups, which start only as GEMM workgroups end, do not wait on HBM for them;
+  // the values are consumed (a register dependency) only after the last row block
+  u32x4 pf[kProPF];
+  const bool pf_on = PRO && (int)(blockIdx.y * gridDim.x + blockIdx.x) < 8;
+  if (pf_on) {
+    const int nw4 = a.N / 4;  // 16-byte vectors of the norm weights; the table's follow
+#pragma unroll
+    for (int i = 0; i < kProPF; ++i) {
+      const int v = tid + kGT * i;
+      pf[i] = v < nw4 ? *(const u32x4*)(p.norm_w + 4 * v)
+                      : (v < nw4 + a.N && p.lB ? *(const u32x4*)(p.lB + 16 * (size_t)(v - nw4)) : u32x4{0u, 0u, 0u, 0u});
+    }
+    asm volatile("" ::: "memory");  // issued here, not sunk to their use
+  }
 #pragma nounroll
   for (int m0 = m_begin; m0 < m_end; m0 += MP) {
     const int MB = m_end - m0 < MP ? m_end - m0 : MP;  // rows in this block
@@ -337,11 +495,28 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
           }
           *op = f2h(out);
         } else {
-          *op = f2h(h2f(*op) + out);
+          const uint16_t xv = f2h(h2f(*op) + out);
+          *op = xv;
+          if (PRO) st_dev(p.xT + (size_t)m * a.N + n, (tag_s << 16) | xv);
         }
       }
     }
   }
+  if (pf_on) {
+#pragma unroll
+    for (int i = 0; i < kProPF; ++i) asm volatile("" ::"v"(pf[i][0]));
+  }
+}
+
+// The kernels: the GEMM alone, and out_proj with the next layer's prologue (separate entry points,
+// so that the GEMM alone keeps its own argument block and LDS)
+template <int MI, int RT, int MODE>
+__global__ __launch_bounds__(kGT) void gemm_kernel(GemmArgs a) {
+  gemm_body<MI, RT, MODE, false>(a, GemmPro{});
+}
+template <int MI, int RT>
+__global__ __launch_bounds__(kGT) void gemm_pro_kernel(GemmArgs a, GemmPro p) {
+  gemm_body<MI, RT, DFSSM_MODE_OUT, true>(a, p);
 }
 
 static size_t gemm_lds_bytes(int MI, int RT, int K) {
@@ -350,12 +525,9 @@ static size_t gemm_lds_bytes(int MI, int RT, int K) {
   return tile > part ? tile : part;
 }
 
-template <int MI, int RT, int MODE>
-static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
+template <int MI, int RT, int MODE, bool PRO>
+static hipError_t launch_gemm_mi(const GemmArgs& a, const GemmPro* pro, hipStream_t s) {
   const size_t shm = gemm_lds_bytes(MI, RT, a.K);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, RT, MODE>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-  if (e != hipSuccess) return e;
   // one workgroup per CU (registers and LDS). Decode batches: with 16 output rows per workgroup
   // (N <= 4096: 128..256 workgroups) one row block per workgroup, the blocks in a second grid
   // dimension (a further round of workgroups starts as CUs free up, where a workgroup walking its
@@ -367,25 +539,58 @@ static hipError_t launch_gemm_mi(const GemmArgs& a, hipStream_t s) {
   const int nblk = (a.M + MI * 16 - 1) / (MI * 16);
   int gy = a.M > 64 ? (512 + gx / 2) / gx : (RT == 1 ? nblk : 1);
   gy = gy < 1 ? 1 : (gy > nblk ? nblk : gy);
-  hipLaunchKernelGGL((gemm_kernel<MI, RT, MODE>), dim3(gx, gy), dim3(kGT), shm, s, a);
+  // PRO: every GEMM grid row must hold rows (each workgroup advances its launch count once), the
+  // prologue's normalized row lives in the dynamic LDS, the counts in kGemmProMaxWg words; a
+  // shape outside these is refused before anything is set or launched
+  const int gyp = gy + (kProPW * a.M + gx - 1) / gx;
+  if (PRO && ((gy - 1) * ((nblk + gy - 1) / gy) >= nblk || shm < (size_t)2 * a.N ||
+              (long long)gx * gyp > kGemmProMaxWg))
+    return hipErrorNotSupported;
+  if (PRO) {
+    // The prologue workgroups inherit the GEMM's registers and LDS (one workgroup per CU), so
+    // they run on CUs the GEMM's last round leaves free, or after it. A GEMM of whole rounds
+    // leaves none: then the prologue's tail costs what its own launch does (batch 32, 256
+    // workgroups: 2322 -> 2338 us per decode step), against 6783 -> 6738 us at the 2.7B shape and
+    // batch 64 (640 workgroups). Refused for whole rounds.
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess)
+      return hipErrorNotSupported;
+    if (cus > 0 && (gx * gy) % cus == 0) return hipErrorNotSupported;
+  }
+  if constexpr (PRO) {
+    static_assert(MODE == DFSSM_MODE_OUT, "the prologue follows out_proj");
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_pro_kernel<MI, RT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    GemmPro p = *pro;
+    p.gy = gy;
+    hipLaunchKernelGGL((gemm_pro_kernel<MI, RT>), dim3(gx, gyp), dim3(kGT), shm, s, a, p);
+  } else {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<MI, RT, MODE>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemm_kernel<MI, RT, MODE>), dim3(gx, gy), dim3(kGT), shm, s, a);
+  }
   return hipGetLastError();
 }
 
-template <int MI, int MODE>
-static hipError_t launch_gemm_rt(const GemmArgs& a, hipStream_t s) {
+template <int MI, int MODE, bool PRO>
+static hipError_t launch_gemm_rt(const GemmArgs& a, const GemmPro* pro, hipStream_t s) {
   // the fewest output rows per workgroup (16, 32 or 64) that keep the grid within one workgroup
   // per CU (256): a workgroup fills its CU, so a grid beyond 256 runs a second round
-  if (a.N <= 256 * 16) return launch_gemm_mi<MI, 1, MODE>(a, s);
-  if (a.N <= 256 * 32) return launch_gemm_mi<MI, 2, MODE>(a, s);
-  return launch_gemm_mi<MI, 4, MODE>(a, s);
+  if (a.N <= 256 * 16) return launch_gemm_mi<MI, 1, MODE, PRO>(a, pro, s);
+  if (a.N <= 256 * 32) return launch_gemm_mi<MI, 2, MODE, PRO>(a, pro, s);
+  return launch_gemm_mi<MI, 4, MODE, PRO>(a, pro, s);
 }
 
-template <int MODE>
-static hipError_t launch_gemm_mode(const GemmArgs& a, hipStream_t s) {
+template <int MODE, bool PRO>
+static hipError_t launch_gemm_mode(const GemmArgs& a, const GemmPro* pro, hipStream_t s) {
   // one launch for all rows, in blocks whose q tile (rows x (K + 16) bytes) fits the 160 KiB of
   // LDS: 32 rows up to K = 4096, 16 above; 16 also for N <= 4096 (one row block per workgroup,
   // see launch_gemm_mi: more, smaller blocks spread over more CUs)
-  return (a.M > 16 && a.K <= 4096 && a.N > 4096) ? launch_gemm_rt<2, MODE>(a, s) : launch_gemm_rt<1, MODE>(a, s);
+  return (a.M > 16 && a.K <= 4096 && a.N > 4096) ? launch_gemm_rt<2, MODE, PRO>(a, pro, s)
+                                                  : launch_gemm_rt<1, MODE, PRO>(a, pro, s);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -551,11 +756,20 @@ hipError_t launch_gemm_wide(const GemmArgs& a, int mode, int8_t* w8, hipStream_t
 hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s) {
   if (a.M < 1 || a.M > kGemmMaxRows || a.K % 512 || a.K > 5120) return hipErrorInvalidValue;
   switch (mode) {
-    case DFSSM_MODE_IN: return launch_gemm_mode<DFSSM_MODE_IN>(a, s);
-    case DFSSM_MODE_OUT: return launch_gemm_mode<DFSSM_MODE_OUT>(a, s);
-    case DFSSM_MODE_SCAFFOLD: return launch_gemm_mode<DFSSM_MODE_SCAFFOLD>(a, s);
+    case DFSSM_MODE_IN: return launch_gemm_mode<DFSSM_MODE_IN, false>(a, nullptr, s);
+    case DFSSM_MODE_OUT: return launch_gemm_mode<DFSSM_MODE_OUT, false>(a, nullptr, s);
+    case DFSSM_MODE_SCAFFOLD: return launch_gemm_mode<DFSSM_MODE_SCAFFOLD, false>(a, nullptr, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_gemm_out_pro(const GemmArgs& a, const GemmPro& p, hipStream_t s) {
+  if (a.M < 1 || a.M > 64 || a.K % 512 || a.K > 5120 || a.N % 512 || a.N > 5120) return hipErrorNotSupported;
+  if (!a.out || !a.lA || !a.lAs) return hipErrorInvalidValue;
+  if (!p.xT || !p.launches || !p.err || !p.norm_w || !p.q_out || !p.xs_out || !p.h_out || p.ld_q < a.N ||
+      (p.lB && !p.lBs))
+    return hipErrorInvalidValue;
+  return launch_gemm_mode<DFSSM_MODE_OUT, true>(a, &p, s);
 }
 
 }  // namespace dfssm
