@@ -31,7 +31,6 @@ sys.path.insert(0, os.path.join(REPO, "df-ssm_amd"))
 sys.path.insert(0, REPO)
 
 PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
-PHASE_NAMES = ("prep_in", "in_proj+conv", "ssm+gate", "prep_out", "out_proj+residual")
 STEPS_PER_GRAPH = 8
 
 
@@ -65,6 +64,13 @@ def algorithmic_bytes(cfg, B):
         # one-launch layer (batch <= 4): the layer's weights, its SSM/conv state read and written,
         # x read and written
         4: layer_bytes(cfg) + B * (H * P * N * 4 + C * 3 * 2) * 2 + B * D * 4,
+        # SSM + out_proj prologue in one launch (batch >= 5): the SSM's bytes without g out and the
+        # partials, the prologue's without g in (g passes between the launch's workgroups): norm_w,
+        # LoRA B + scales in; q, scale, h out
+        5: B * H * P * N * 4 * 2 + B * (DI + 2 * N + H + DI) * 2 + 12 * H + 4 * DI + 16 * DI + 32 + B * (DI + 68),
+        # out_proj + the next layer's in_proj prologue (batch >= 5): gemv_out's bytes, the next ln_w,
+        # LoRA B + scales in; q, scale, h out (x passes between the launch's workgroups)
+        6: D * DI // 8 + 2 * D + 16 * D + 2 * D + B * (DI + 8 + 64) + B * D * 4 + 4 * D + 16 * D + 32 + B * (D + 68),
     }
     return weights, state, per_phase
 
@@ -234,6 +240,10 @@ def time_kernels(m, reps=10):
     one = torch.zeros(1, device="cuda:0")
     empty = graph_time(lambda: [one.mul_(1.0) for _ in range(L)], L)
     out = {"empty": (empty, 0)}
+    def phase(p, li):
+        return lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state, m.workspace.data_ptr(),
+                                     _C.stream())
+
     if m.batch_size <= 4:
         # the decode path runs each layer as one launch at this batch
         def layer():
@@ -241,17 +251,25 @@ def time_kernels(m, reps=10):
                 _C.check(lib.dfssm_layer_step(m._model, li, m.x.data_ptr(), m._state,
                                               m.workspace.data_ptr(), _C.stream()))
         out["layer (one launch)"] = (graph_time(layer, L), L)
-        phases = ("in_proj+conv",)   # the stand-alone scaffold GEMV kernel, timed as a microbenchmark
+        # the stand-alone scaffold GEMV kernel, timed as a microbenchmark
+        plan = [("in_proj+conv", 1, L, 0)]
     else:
-        phases = PHASE_NAMES
-    for p, name in enumerate(PHASE_NAMES):
-        if name not in phases:
-            continue
-        def body(p=p):
-            for li in range(L):
-                _C.check(lib.dfssm_layer_phase(m._model, li, p, m.x.data_ptr(), m._state,
-                                               m.workspace.data_ptr(), _C.stream()))
-        out[name] = (graph_time(body, L), L if m.batch_size > 4 else 0)
+        # the launches of the decode step at this batch (dfssm_decode_step): in_proj, the SSM with
+        # out_proj's prologue and out_proj with the next layer's prologue where the shape takes
+        # them (probed once, eagerly), the prologue of layer 0 and out_proj of the last layer
+        ssm_fused = phase(_C.PHASE_SSM_PROLOGUE, 0) == 0
+        out_fused = L > 1 and phase(_C.PHASE_OUT_PROLOGUE, 0) == 0
+        torch.cuda.synchronize()
+        plan = [("prep_in", 0, L, 1 if out_fused else L), ("in_proj+conv", 1, L, L)]
+        plan += [("ssm+prologue", _C.PHASE_SSM_PROLOGUE, L, L)] if ssm_fused else \
+            [("ssm+gate", 2, L, L), ("prep_out", 3, L, L)]
+        plan += [("out_proj+prologue", _C.PHASE_OUT_PROLOGUE, L - 1, L - 1), ("out_proj+residual", 4, L, 1)] \
+            if out_fused else [("out_proj+residual", 4, L, L)]
+    for name, p, nl, per_step in plan:
+        def body(p=p, nl=nl):
+            for li in range(nl):
+                _C.check(phase(p, li))
+        out[name] = (graph_time(body, nl), per_step)
 
     def head():
         for _ in range(L):
@@ -538,7 +556,7 @@ def measure(B, path, steps, warmup, shape="1p3b", prompt_len=32):
     log(f"density-field state batch {B}: {df_us:.1f} us per boundary, {state_df['gbs']:.0f} GB/s")
     kt = time_kernels(m)
     phase_of = {"prep_in": 0, "in_proj+conv": 1, "ssm+gate": 1.5, "prep_out": 2, "out_proj+residual": 2.5,
-                "head+argmax": 3, "layer (one launch)": 4}
+                "head+argmax": 3, "layer (one launch)": 4, "ssm+prologue": 5, "out_proj+prologue": 6}
     kernels = {}
     for name, (us, n) in kt.items():
         if name == "empty":

@@ -549,12 +549,70 @@ static GemmArgs batched_gemm_args(const dfssm_model* model, int layer, bool in, 
   return a;
 }
 
+// Phases 2 and 3 of dfssm_layer_phase in one launch (batch >= 5): the SSM step + gate, with the
+// gated-norm prologue of out_proj computed by workgroups of the same launch.
+static int ssm_prep_layer(const dfssm_model* model, int layer, const dfssm_state* state, void* workspace,
+                          void* stream) {
+  const Derived r = derive(&model->dims);
+  const dfssm_layer& Lw = model->layers[layer];
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  uint16_t* proj = (uint16_t*)(ws + w.proj);
+  SsmPrepArgs a{};
+  a.s.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
+  a.s.xbc = proj + r.DI; a.s.ld_xbc = r.IPO;
+  a.s.dt = proj + r.DI + r.C; a.s.ld_dt = r.IPO;
+  a.s.z = proj; a.s.ld_z = r.IPO;
+  a.s.dt_bias = Lw.dt_bias; a.s.A_log = Lw.A_log; a.s.D = Lw.D;
+  a.s.H = r.H; a.s.P = r.P; a.s.N = r.N;
+  a.gT = (uint32_t*)(ws + w.g_s);
+  a.launches = (uint32_t*)(ws + w.launches_s);
+  a.err = (int*)(ws + w.err);
+  a.norm_w = Lw.norm_w;
+  a.lB = Lw.out_lB; a.lBs = Lw.out_lB_s;
+  a.q_out = (int8_t*)(ws + w.q); a.ld_q = r.D > r.DI ? r.D : r.DI;
+  a.xs_out = (float*)(ws + w.xs);
+  a.h_out = (float*)(ws + w.h);
+  return hip_status(launch_ssm_prep(a, r.B, as_stream(stream)));
+}
+
+// Phase 4 of `layer` and phase 0 of layer + 1 in one launch (batch >= 5): out_proj with the next
+// layer's in_proj prologue computed by workgroups of the same launch. DFSSM_E_DIMS (nothing
+// launched) where the out_proj grid does not take them.
+static int out_prep_layer(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
+                          void* workspace, void* stream) {
+  const Derived r = derive(&model->dims);
+  const WsLayout w = ws_layout(&model->dims);
+  char* ws = (char*)workspace;
+  const dfssm_layer& Ln = model->layers[layer + 1];
+  GemmPro p{};
+  p.xT = (uint32_t*)(ws + w.x_s);
+  p.launches = (uint32_t*)(ws + w.launches_o);
+  p.err = (int*)(ws + w.err);
+  p.norm_w = Ln.ln_w;
+  p.lB = Ln.in_lB; p.lBs = Ln.in_lB_s;
+  p.q_out = (int8_t*)(ws + w.q); p.ld_q = r.D > r.DI ? r.D : r.DI;
+  p.xs_out = (float*)(ws + w.xs);
+  p.h_out = (float*)(ws + w.h);
+  const hipError_t e = launch_gemm_out_pro(batched_gemm_args(model, layer, false, x, state, workspace), p,
+                                           as_stream(stream));
+  return e == hipErrorNotSupported ? DFSSM_E_DIMS : hip_status(e);
+}
+
 int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
                       const dfssm_state* state, void* workspace, void* stream) {
   int rc = check_layer_args(model, layer, x, state, workspace);
   if (rc) return rc;
-  if (phase < 0 || phase >= DFSSM_LAYER_PHASES) return DFSSM_E_RANGE;
+  if (phase < 0 || phase > DFSSM_PHASE_OUT_PROLOGUE) return DFSSM_E_RANGE;
   const Derived r = derive(&model->dims);
+  if (phase == DFSSM_PHASE_SSM_PROLOGUE) {
+    if (r.B <= 4 || !ssm_prep_supported(r.B, r.DI, r.P)) return DFSSM_E_DIMS;
+    return ssm_prep_layer(model, layer, state, workspace, stream);
+  }
+  if (phase == DFSSM_PHASE_OUT_PROLOGUE) {
+    if (r.B <= 4 || layer + 1 >= r.L) return DFSSM_E_DIMS;
+    return out_prep_layer(model, layer, x, state, workspace, stream);
+  }
   const dfssm_layer& Lw = model->layers[layer];
   const WsLayout w = ws_layout(&model->dims);
   char* ws = (char*)workspace;
@@ -624,33 +682,6 @@ int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* 
   return hip_status(launch_proj(a, r.B, DFSSM_MODE_OUT, s));
 }
 
-// Phases 2 and 3 of dfssm_layer_phase in one launch (batch >= 5): the SSM step + gate, with the
-// gated-norm prologue of out_proj computed by workgroups of the same launch.
-static int ssm_prep_layer(const dfssm_model* model, int layer, const dfssm_state* state, void* workspace,
-                          void* stream) {
-  const Derived r = derive(&model->dims);
-  const dfssm_layer& Lw = model->layers[layer];
-  const WsLayout w = ws_layout(&model->dims);
-  char* ws = (char*)workspace;
-  uint16_t* proj = (uint16_t*)(ws + w.proj);
-  SsmPrepArgs a{};
-  a.s.h = state->h + (size_t)layer * r.B * r.H * r.P * r.N;
-  a.s.xbc = proj + r.DI; a.s.ld_xbc = r.IPO;
-  a.s.dt = proj + r.DI + r.C; a.s.ld_dt = r.IPO;
-  a.s.z = proj; a.s.ld_z = r.IPO;
-  a.s.dt_bias = Lw.dt_bias; a.s.A_log = Lw.A_log; a.s.D = Lw.D;
-  a.s.H = r.H; a.s.P = r.P; a.s.N = r.N;
-  a.gT = (uint32_t*)(ws + w.g_s);
-  a.launches = (uint32_t*)(ws + w.launches_s);
-  a.err = (int*)(ws + w.err);
-  a.norm_w = Lw.norm_w;
-  a.lB = Lw.out_lB; a.lBs = Lw.out_lB_s;
-  a.q_out = (int8_t*)(ws + w.q); a.ld_q = r.D > r.DI ? r.D : r.DI;
-  a.xs_out = (float*)(ws + w.xs);
-  a.h_out = (float*)(ws + w.h);
-  return hip_status(launch_ssm_prep(a, r.B, as_stream(stream)));
-}
-
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream) {
   int rc = check_layer_args(model, layer, x, state, workspace);
@@ -713,8 +744,9 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
 
 // The layers of a decode step, launch by launch. Batch >= 5 (unless DFSSM_LAYER_FIVE): per layer
 // the in_proj GEMM, the SSM launch with out_proj's prologue, and the out_proj launch with the
-// next layer's in_proj prologue (the first layer's runs on its own), three launches instead of
-// five; other batches layer by layer as dfssm_layer_step.
+// next layer's in_proj prologue where the shape takes it (else out_proj, and the next layer's
+// prologue on its own), three launches instead of five; other batches layer by layer as
+// dfssm_layer_step.
 static int decode_layers(const dfssm_model* model, uint16_t* x, const dfssm_state* state, void* workspace,
                          void* stream) {
   const Derived r = derive(&model->dims);
@@ -723,34 +755,15 @@ static int decode_layers(const dfssm_model* model, uint16_t* x, const dfssm_stat
     for (int l = 0; l < r.L && !rc; ++l) rc = dfssm_layer_step(model, l, x, state, workspace, stream);
     return rc;
   }
-  const WsLayout w = ws_layout(&model->dims);
-  char* ws = (char*)workspace;
   bool prepped = false;  // the q, scale and LoRA intermediates of this layer's in_proj are written
   for (int l = 0; l < r.L; ++l) {
     if (!prepped && (rc = dfssm_layer_phase(model, l, 0, x, state, workspace, stream))) return rc;
     if ((rc = dfssm_layer_phase(model, l, 1, x, state, workspace, stream))) return rc;
-    if ((rc = ssm_prep_layer(model, l, state, workspace, stream))) return rc;
-    prepped = false;
-    if (l + 1 < r.L) {
-      const dfssm_layer& Ln = model->layers[l + 1];
-      GemmPro p{};
-      p.xT = (uint32_t*)(ws + w.x_s);
-      p.launches = (uint32_t*)(ws + w.launches_o);
-      p.err = (int*)(ws + w.err);
-      p.norm_w = Ln.ln_w;
-      p.lB = Ln.in_lB; p.lBs = Ln.in_lB_s;
-      p.q_out = (int8_t*)(ws + w.q); p.ld_q = r.D > r.DI ? r.D : r.DI;
-      p.xs_out = (float*)(ws + w.xs);
-      p.h_out = (float*)(ws + w.h);
-      const hipError_t e =
-          launch_gemm_out_pro(batched_gemm_args(model, l, false, x, state, workspace), p, as_stream(stream));
-      if (e == hipSuccess) {
-        prepped = true;
-        continue;
-      }
-      if (e != hipErrorNotSupported) return hip_status(e);
-    }
-    if ((rc = dfssm_layer_phase(model, l, 4, x, state, workspace, stream))) return rc;
+    if ((rc = dfssm_layer_phase(model, l, DFSSM_PHASE_SSM_PROLOGUE, x, state, workspace, stream))) return rc;
+    rc = dfssm_layer_phase(model, l, DFSSM_PHASE_OUT_PROLOGUE, x, state, workspace, stream);
+    prepped = rc == DFSSM_OK;
+    if (rc == DFSSM_E_DIMS && (rc = dfssm_layer_phase(model, l, 4, x, state, workspace, stream))) return rc;
+    if (rc) return rc;
   }
   return DFSSM_OK;
 }

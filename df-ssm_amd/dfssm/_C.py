@@ -106,6 +106,12 @@ def exported_symbols():
     return list(_SIGS)
 
 
+# return codes and layer phases of include/dfssm.h used from Python
+DFSSM_E_DIMS = -2
+PHASE_SSM_PROLOGUE = 5   # DFSSM_PHASE_SSM_PROLOGUE
+PHASE_OUT_PROLOGUE = 6   # DFSSM_PHASE_OUT_PROLOGUE
+
+
 def check(rc: int, what: str = "") -> None:
     if rc != 0:
         msg = lib().dfssm_error_string(rc).decode()

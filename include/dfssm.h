@@ -193,7 +193,9 @@ int* dfssm_workspace_error_flag(const dfssm_dims* dims, void* workspace);
 
 /* One residual block on x (batch, D) fp16, in place: RMSNorm, in_proj scaffold + LoRA, conv,
  * SSM, gate, gated RMSNorm, out_proj scaffold + LoRA, residual. Replaces one iteration of
- * _run_layers, df_ssm_inference.py:161-207. 5 kernel launches. */
+ * _run_layers, df_ssm_inference.py:161-207. One launch at batch <= 4 (see
+ * dfssm_set_layer_kernel); at batch >= 5 four (phases 0, 1, DFSSM_PHASE_SSM_PROLOGUE, 4);
+ * with DFSSM_LAYER_FIVE the five phases below. */
 int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                      void* workspace, void* stream);
 
@@ -203,6 +205,14 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
  * intermediate (:196-199,204), 4 = out_proj scaffold + LoRA + residual (:200-207). Running the
  * phases in order equals dfssm_layer_step; exposed for per-kernel timing. */
 #define DFSSM_LAYER_PHASES 5
+/* Two more values of `phase`, the fused launches of the decode step at batch >= 5 (no counterpart
+ * in the reference; exposed for per-launch timing): DFSSM_PHASE_SSM_PROLOGUE = phases 2 and 3 in
+ * one launch; DFSSM_PHASE_OUT_PROLOGUE = phase 4 of `layer` and phase 0 of layer + 1 in one
+ * launch (layer + 1 < n_layer). Both return DFSSM_E_DIMS, launching nothing, for a batch or shape
+ * they do not take (batch <= 4; the second also where the out_proj grid fills whole rounds of the
+ * CUs, which dfssm_decode_step then runs as two launches). */
+#define DFSSM_PHASE_SSM_PROLOGUE 5
+#define DFSSM_PHASE_OUT_PROLOGUE 6
 int dfssm_layer_phase(const dfssm_model* model, int layer, int phase, uint16_t* x,
                       const dfssm_state* state, void* workspace, void* stream);
 
@@ -215,7 +225,8 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
 /* One whole decode step: if tokens != NULL, x = embedding(tokens) first; then every layer,
  * then the head. With fuse_next_embed != 0, x receives the embedding of the greedy tokens, so
  * the following step can pass tokens = NULL. Replaces forward() + argmax,
- * df_ssm_inference.py:219-224,236. */
+ * df_ssm_inference.py:219-224,236. At batch >= 5 a layer is three launches (in_proj,
+ * DFSSM_PHASE_SSM_PROLOGUE, DFSSM_PHASE_OUT_PROLOGUE) where the shape takes them. */
 int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
                       const dfssm_state* state, void* workspace, uint16_t* logits, int64_t* next,
                       int fuse_next_embed, void* stream);

@@ -207,6 +207,51 @@ def test_batched_ssm_prologue_launch_equals_five_kernels(tiny_weights, B):
     assert torch.equal(c_a.view(torch.int16), c_5.view(torch.int16))
 
 
+@pytest.mark.parametrize("B", [5, 32])
+def test_fused_phases_equal_five_phases(tiny_weights, B):
+    """dfssm_layer_phase with the fused launches (phases 0 and 1, DFSSM_PHASE_SSM_PROLOGUE = 5,
+    DFSSM_PHASE_OUT_PROLOGUE = 6 writing the next layer's prologue, 4 for the last layer) against
+    phases 0..4 of every layer on the same inputs: x, SSM state and conv state identical bit for
+    bit (each layer's in_proj reads the prologue the fused launch wrote)."""
+    from dfssm import _C
+    w = tiny_weights
+    print(f"fused phases B={B}", flush=True)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, 5)))
+    lib = _C.lib()
+    L = w.cfg.n_layer
+
+    def ph(li, p):
+        return lib.dfssm_layer_phase(gpu._model, li, p, gpu.x.data_ptr(), gpu._state, gpu.workspace.data_ptr(),
+                                     _C.stream())
+
+    x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    for li in range(L):
+        for p in range(5):
+            _C.check(ph(li, p))
+    torch.cuda.synchronize()
+    x5, h5, c5 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    gpu.x.copy_(x0); gpu.h_state.copy_(h0); gpu.conv_state.copy_(c0)
+    assert ph(L - 1, _C.PHASE_OUT_PROLOGUE) == _C.DFSSM_E_DIMS  # no next layer
+    prepped = False
+    for li in range(L):
+        if not prepped:
+            _C.check(ph(li, 0))
+        _C.check(ph(li, 1))
+        _C.check(ph(li, _C.PHASE_SSM_PROLOGUE))
+        rc = ph(li, _C.PHASE_OUT_PROLOGUE) if li + 1 < L else _C.DFSSM_E_DIMS
+        prepped = rc == 0
+        if rc == _C.DFSSM_E_DIMS:
+            _C.check(ph(li, 4))
+        else:
+            _C.check(rc)
+    torch.cuda.synchronize()
+    assert gpu.error_flag() == 0
+    assert torch.equal(gpu.x.view(torch.int16), x5.view(torch.int16))
+    assert torch.equal(gpu.h_state, h5)
+    assert torch.equal(gpu.conv_state.view(torch.int16), c5.view(torch.int16))
+
+
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
 def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
     """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
