@@ -198,7 +198,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   const int QS = K + 16;  // padded LDS row stride
   // rows of this workgroup: blocks [blockIdx.y * bpw, +bpw) of the activation rows (one range
   // in decode; the prompt prefill spreads its thousands of rows over gridDim.y ranges)
-  const int nblk = (a.M + MP - 1) / MP, bpw = (nblk + (int)gridDim.y - 1) / (int)gridDim.y;
+  // (PRO: the grid rows past p.gy hold the prologue workgroups, not row ranges)
+  const int grows = PRO ? p.gy : (int)gridDim.y;
+  const int nblk = (a.M + MP - 1) / MP, bpw = (nblk + grows - 1) / grows;
   const int m_begin = (int)blockIdx.y * bpw * MP;
   if (m_begin >= a.M) return;
   const int m_end = m_begin + bpw * MP < a.M ? m_begin + bpw * MP : a.M;
@@ -539,6 +541,13 @@ static hipError_t launch_gemm_mi(const GemmArgs& a, const GemmPro* pro, hipStrea
   const int nblk = (a.M + MI * 16 - 1) / (MI * 16);
   int gy = a.M > 64 ? (512 + gx / 2) / gx : (RT == 1 ? nblk : 1);
   gy = gy < 1 ? 1 : (gy > nblk ? nblk : gy);
+  int cus = 0;
+  if (PRO) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess)
+      return hipErrorNotSupported;
+  }
   // PRO: every GEMM grid row must hold rows (each workgroup advances its launch count once), the
   // prologue's normalized row lives in the dynamic LDS, the counts in kGemmProMaxWg words; a
   // shape outside these is refused before anything is set or launched
@@ -546,18 +555,14 @@ static hipError_t launch_gemm_mi(const GemmArgs& a, const GemmPro* pro, hipStrea
   if (PRO && ((gy - 1) * ((nblk + gy - 1) / gy) >= nblk || shm < (size_t)2 * a.N ||
               (long long)gx * gyp > kGemmProMaxWg))
     return hipErrorNotSupported;
-  if (PRO) {
-    // The prologue workgroups inherit the GEMM's registers and LDS (one workgroup per CU), so
-    // they run on CUs the GEMM's last round leaves free, or after it. A GEMM of whole rounds
-    // leaves none: then the prologue's tail costs what its own launch does (batch 32, 256
-    // workgroups: 2322 -> 2338 us per decode step), against 6783 -> 6738 us at the 2.7B shape and
-    // batch 64 (640 workgroups). Refused for whole rounds.
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                 hipSuccess)
-      return hipErrorNotSupported;
-    if (cus > 0 && (gx * gy) % cus == 0) return hipErrorNotSupported;
-  }
+  // The prologue workgroups inherit the GEMM's registers and LDS (one workgroup per CU), so they
+  // run on CUs the GEMM's last round leaves free, or after it. A GEMM of whole rounds leaves none:
+  // then the prologue's tail cost what its own launch does (batch 32, 256 workgroups: 2322 ->
+  // 2338 us per decode step), against 6783 -> 6738 us at the 2.7B shape and batch 64 (640
+  // workgroups). Refused for whole rounds. (One GEMM grid row instead, each workgroup walking the
+  // row blocks so that the prologue runs beside the GEMM on the free half of the CUs, was slower
+  // still: 2322 -> 2514 us.)
+  if (PRO && cus > 0 && (gx * gy) % cus == 0) return hipErrorNotSupported;
   if constexpr (PRO) {
     static_assert(MODE == DFSSM_MODE_OUT, "the prologue follows out_proj");
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_pro_kernel<MI, RT>),

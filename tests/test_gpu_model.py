@@ -252,6 +252,26 @@ def test_fused_phases_equal_five_phases(tiny_weights, B):
     assert torch.equal(gpu.conv_state.view(torch.int16), c5.view(torch.int16))
 
 
+def test_fused_phases_wide_model_batch64():
+    """d_model 4608 at batch 64: out_proj at 32 output rows per workgroup has one GEMM grid row
+    walking two 32-row blocks, followed by the prologue workgroups' rows (the GEMM workgroups must
+    take their row ranges from the GEMM rows alone). The decode step against DFSSM_LAYER_FIVE:
+    logits, tokens, x and both states identical bit for bit."""
+    from dfssm.format import DFSSMConfig
+    c = DFSSMConfig(n_layer=2, d_model=4608, d_inner=1024, d_state=128, nheads=16, headdim=64, ngroups=1,
+                    vocab_size=4096, kw=4)
+    w = make_weights(c, seed=11)
+    print("wide model d_model 4608 B=64 decode", flush=True)
+    one_a, out_a, x_a, h_a, c_a = _decode_run(w, 64, 0, 3)
+    one_5, out_5, x_5, h_5, c_5 = _decode_run(w, 64, 2, 3)
+    for (la, na), (l5, n5) in zip(out_a, out_5):
+        assert torch.equal(la.view(torch.int16), l5.view(torch.int16))
+        assert torch.equal(na, n5)
+    assert torch.equal(x_a.view(torch.int16), x_5.view(torch.int16))
+    assert torch.equal(h_a, h_5)
+    assert torch.equal(c_a.view(torch.int16), c_5.view(torch.int16))
+
+
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
 def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
     """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
