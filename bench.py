@@ -695,7 +695,8 @@ def main():
         return
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU; multi-GPU decode (data-parallel batch sharding) "
-              "is described in DESIGN.md and not measured", file=sys.stderr)
+              "(every GPU decoding its own shard of the sequences, no collective in the step) is not measured here",
+              file=sys.stderr)
         sys.exit(2)
 
     main_res, w, prompts = measure(a.batch, a.model_path, a.steps, a.warmup)
