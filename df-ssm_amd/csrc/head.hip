@@ -510,9 +510,9 @@ hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int D, hipSt
 // through to the coherent level, the last workgroup (arrival ticket) reduces them and writes the
 // next tokens and their embedding.
 // ---------------------------------------------------------------------------------------------
-// 16-byte k chunks per digit-plane row: D / 16 rounded up to whole groups of three 64-wide k steps
-// (the three-stage ring runs without a tail; the padding is zero)
-__host__ __device__ inline int digit_chunks(int D) { return (D / 64 + 2) / 3 * 3 * 4; }
+// 16-byte k chunks per digit-plane row: D / 16 rounded up to whole groups of four 64-wide k steps
+// (the rings run four steps per iteration without a tail; the padding is zero)
+__host__ __device__ inline int digit_chunks(int D) { return (D / 64 + 3) / 4 * 4 * 4; }
 size_t head_digit_bytes(int M, int D) { return (size_t)6 * 16 * ((M + 15) / 16) * digit_chunks(D) * 16; }
 
 __global__ __launch_bounds__(256) void head_digits_kernel(const uint16_t* __restrict__ x,
@@ -605,46 +605,57 @@ __global__ __launch_bounds__(128 * NH * KP) __attribute__((amdgpu_waves_per_eu(2
   for (int b = 0; b < 6; ++b)
 #pragma unroll
     for (int f = 0; f < 4; ++f) acc[b][f] = i32x4{0, 0, 0, 0};
-  // three-stage ring: the loads of steps s + 1 and s + 2 are in flight during step s's MFMAs
-  // (loads complete in issue order, so a step's operands are waited for with 20 loads pending)
-  u32x4 A[3][6], Bf[3][4];
-  auto load = [&](int st, int step) {
+  // rings: the table fragments (HBM) are loaded three steps ahead, the digit tiles (L2) one step
+  // ahead, a step's digit tiles issued before its table fragments: loads complete in issue order,
+  // so waiting for step s's digit tiles leaves the table loads of steps s + 2 and s + 3 in flight
+  u32x4 A[2][6], Bf[4][4];
+  auto loadA = [&](int st, int step) {
     // steps KS .. KSp - 1 multiply zero digits with a re-read of the last table step; loads past
-    // KSp (the ring's last two) re-read step KSp - 1 and are not used
+    // KSp (the rings' overrun) re-read step KSp - 1 and are not used
     const uint32_t oa = (uint32_t)(4 * (step < KSp ? step : KSp - 1));
-    const uint32_t oe = (uint32_t)(4 * (step < KS ? step : KS - 1));
 #pragma unroll
     for (int b = 0; b < 6; ++b) A[st][b] = *(const u32x4*)(Ab + (ao + b * plane + oa * 256));
+  };
+  auto loadB = [&](int st, int step) {
+    const uint32_t oe = (uint32_t)(4 * (step < KS ? step : KS - 1));
 #pragma unroll
     for (int f = 0; f < 4; ++f) Bf[st][f] = ld_nt((const u32x4*)(Eb + (eo + oe * 1024 + 256 * f)));
   };
-  auto mma = [&](int st) {
+  auto mma = [&](int sa, int sb) {
 #pragma unroll
     for (int b = 0; b < 6; ++b)
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        acc[b][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, A[st][b]),
-                                                          __builtin_bit_cast(i32x4, Bf[st][f]), acc[b][f], 0, 0, 0);
+        acc[b][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, A[sa][b]),
+                                                          __builtin_bit_cast(i32x4, Bf[sb][f]), acc[b][f], 0, 0, 0);
   };
-  // this wave's k part: whole groups of three steps, the last part the shortest
-  const int Q = (KSp / 3 + KP - 1) / KP * 3;
+  // this wave's k part: whole groups of four steps, the last part the shortest
+  const int Q = (KSp / 4 + KP - 1) / KP * 4;
   const int s0 = kp * Q < KSp ? kp * Q : KSp, s1 = s0 + Q < KSp ? s0 + Q : KSp;
-  load(0, s0);
+  loadA(0, s0);
+  loadB(0, s0);
+  loadB(1, s0 + 1);
+  loadB(2, s0 + 2);
   __builtin_amdgcn_sched_barrier(0);
-  load(1, s0 + 1);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int s = s0; s < s1; s += 3) {
-    // sched_barrier keeps each step's loads ahead of the previous step's MFMAs (the scheduler
-    // would otherwise sink them to their uses and expose the load latency at every step)
-    load(2, s + 2);
+  for (int s = s0; s < s1; s += 4) {
+    // sched_barrier keeps each step's loads ahead of its MFMAs (the scheduler would otherwise
+    // sink them to their uses and expose the load latency at every step)
+    loadA(1, s + 1);
+    loadB(3, s + 3);
     __builtin_amdgcn_sched_barrier(0);
-    mma(0);
-    load(0, s + 3);
+    mma(0, 0);
+    loadA(0, s + 2);
+    loadB(0, s + 4);
     __builtin_amdgcn_sched_barrier(0);
-    mma(1);
-    load(1, s + 4);
+    mma(1, 1);
+    loadA(1, s + 3);
+    loadB(1, s + 5);
     __builtin_amdgcn_sched_barrier(0);
-    mma(2);
+    mma(0, 2);
+    loadA(0, s + 4);
+    loadB(2, s + 6);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1, 3);
   }
 
   // exact partial dot products of this k part; parts 1.. hand theirs to part 0 through LDS
