@@ -190,7 +190,7 @@ def test_xcd_layer_decode_equals_five_kernels(tiny_weights, B):
     assert torch.equal(c_x.view(torch.int16), c_5.view(torch.int16))
 
 
-@pytest.mark.parametrize("B", [5, 16, 64])
+@pytest.mark.parametrize("B", [5, 16, 17, 33, 64])   # 17, 33: partial row blocks, idle prologue workgroups
 def test_batched_ssm_prologue_launch_equals_five_kernels(tiny_weights, B):
     """Batch >= 5: dfssm_decode_step with the default setting (the SSM step and the out_proj
     prologue in one launch, g handed over as tagged words) against DFSSM_LAYER_FIVE (separate SSM
