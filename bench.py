@@ -75,7 +75,7 @@ def algorithmic_bytes(cfg, B):
     return weights, state, per_phase
 
 
-LAYER_KERNELS = {"auto": 0, "fused": 1, "five": 2, "item": 3, "multi": 4, "xcd": 5}  # dfssm_set_layer_kernel codes
+LAYER_KERNELS = {"auto": 0, "fused": 1, "five": 2}  # dfssm_set_layer_kernel codes
 LAYER_KERNEL = "auto"
 
 
@@ -408,23 +408,11 @@ def phase_sweep(B, path, layers=12):
     log(f"phase sweep batch {B}: {layers} layers x 5 kernels + head done")
 
 
-TIMELINE1_STAMPS = {0: "start", 16: "A: x loaded (control wave 0)", 17: "A: weights in LDS (stream wave 0)",
-                    14: "A: norm, sum of squares barrier (B1)", 18: "A: norm, xn done (control wave 0)",
-                    19: "B: last B|C poll issued (control wave 0)", 15: "A: norm, xn + max barrier (B2)",
-                    20: "A: quantizer + LoRA partial (control wave 0)", 21: "A: B|C rows published (stream wave 3)",
-                    22: "C: last g poll issued (control wave 0)", 1: "A: quantizer + planes done (B3)",
-                    23: "A: LoRA partials polled (control wave 0)", 24: "A: GEMV done (stream wave 0)",
-                    2: "A: LoRA partials in, GEMV done (B4)", 3: "A: LoRA h summed (B5)",
-                    12: "A: z rows done (stream wave 0)", 4: "B: B|C poll returned", 5: "B: B|C in (B6)",
-                    6: "B: SSM done, g published (B7)", 11: "C: g poll returned", 7: "C: all g in (B8)",
-                    25: "C: g loaded (control wave 0)", 26: "C: norm, sum of squares barrier (B9)",
-                    31: "C: norm, done (control wave 0)", 27: "C: norm, xn + max barrier (B10)",
-                    29: "C: quantizer (control wave 0)", 28: "C: quantizer + LoRA partial (control wave 1)",
-                    30: "C: quantizer (stream wave 0)", 8: "C: quantizer + planes done (B11)",
-                    9: "C: LoRA partials in, GEMV done (B12)", 10: "C: LoRA h summed (B13)", 13: "end"}
-TIMELINE_STAMPS = {0: "start", 1: "A: prologue done (GEMV workgroups)", 2: "A: GEMV done", 3: "A: LoRA h in",
+TIMELINE_STAMPS = {0: "start", 14: "A: x in, sum of squares", 1: "A: prologue done (GEMV workgroups)",
+                   2: "A: GEMV done", 3: "A: LoRA h in",
                    4: "A: epilogue / LoRA rank stored", 5: "B: poll start", 6: "B: item inputs in",
-                   7: "B: SSM done", 8: "C: prologue start", 9: "C: prologue done (g in)", 10: "C: GEMV done",
+                   7: "B: SSM done", 8: "C: prologue start", 15: "C: g in, sum of squares",
+                   9: "C: prologue done", 10: "C: GEMV done",
                    11: "C: LoRA h in", 12: "C: epilogue / LoRA rank stored", 13: "end"}
 
 
@@ -444,24 +432,17 @@ def timeline(B, path, graphs=4):
         raise SystemExit(f"{dfb.LIB_TIMELINE} not built (python -m dfssm.build)")
     _C.LIB_PATH = dfb.LIB_TIMELINE
     lib = _C.lib()
-    for fn in (lib.dfssm_timeline_read, lib.dfssm_timeline1_read):
-        fn.restype = ctypes.c_int
-        fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.dfssm_timeline_read.restype = ctypes.c_int
+    lib.dfssm_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     m, _ = build_model(B, path)
     m.ingest(torch.from_numpy(make_prompts(B, m.cfg.vocab_size, 8)))
     g, _ = m._gen_graph(STEPS_PER_GRAPH)
     for _ in range(graphs):
         g.replay()
     torch.cuda.synchronize()
-    # the layer kernel that ran left its stamps: the item-organised layer (timeline1) or the
-    # phase-organised one
-    buf = np.zeros((64, 256, 32), np.uint64)
-    _C.check(lib.dfssm_timeline1_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline1_read")
-    names, kernel = TIMELINE1_STAMPS, "layer_item_kernel"
-    if not buf.any():
-        buf = np.zeros((64, 256, 16), np.uint64)
-        _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
-        names, kernel = TIMELINE_STAMPS, "layer_fused_kernel"
+    buf = np.zeros((64, 256, 16), np.uint64)
+    _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
+    names, kernel = TIMELINE_STAMPS, "layer_fused_kernel"
     t = buf.astype(np.int64)
     starts = np.where(t[:, :, 0] > 0, t[:, :, 0], np.iinfo(np.int64).max).min(axis=1)
     ends = t[:, :, 13].max(axis=1)

@@ -34,8 +34,7 @@ Derived derive(const dfssm_dims* d) {
 
 struct WsLayout {
   size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
-      proj_t, g_t, h_t, dt_t, bc_t, lp_a, lp_c, g_p, launches1, bc_t1, x_t, ltab, launches_x, proj_x, g_x, h_x,
-      bc_x, dt_x, flag_x, g_s, launches_s, x_s, launches_o, total;
+      proj_t, g_t, h_t, dt_t, bc_t, g_s, launches_s, x_s, launches_o, total;
 };
 
 WsLayout ws_layout(const dfssm_dims* d) {
@@ -68,24 +67,6 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.h_t = off;      off = align_up(off + (size_t)kXRep * kHStride * 4);
   w.dt_t = off;     off = align_up(off + 2 * (size_t)r.B * r.H * 8);
   w.bc_t = off;     off = align_up(off + (size_t)kXRep * kBcStride * 4);
-  // item-organised layer: LoRA partials of in_proj / out_proj, packed g of every item
-  w.lp_a = off;     off = align_up(off + (size_t)kXRep * kLpStride * 8);
-  w.lp_c = off;     off = align_up(off + (size_t)kXRep * kLpStride * 8);
-  w.g_p = off;      off = align_up(off + (size_t)kXRep * kGStride * 8);
-  // its own per-workgroup launch counts (its grid differs from the phase-organised layer's)
-  w.launches1 = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
-  w.bc_t1 = off;    off = align_up(off + (size_t)kXRep * kBcStride * 4);  // its B | C words
-  // multi-layer launch of the phase-organised layer: x handed from layer to layer
-  w.x_t = off;      off = align_up(off + (size_t)2 * kXRep * kXStride * 4);
-  w.ltab = off;     off = align_up(off + (size_t)r.L * sizeof(FusedArgs));  // its per-layer arguments
-  // XCD-partitioned layer: its launch counts and exchange words (per-XCD copies 4 KiB apart)
-  w.launches_x = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
-  w.proj_x = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
-  w.g_x = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
-  w.h_x = off;      off = align_up(off + (size_t)kXcd * kHStride * 4);
-  w.bc_x = off;     off = align_up(off + (size_t)kXcd * kBcStride * 4);
-  w.dt_x = off;     off = align_up(off + (size_t)kXcd * kDtStride * 8);
-  w.flag_x = off;   off = align_up(off + 256);
   // batch >= 5: the SSM + gated-norm prologue launch's tagged g words and launch counts
   w.g_s = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
   w.launches_s = off; off = align_up(off + (size_t)(r.DI / 16 + 16) * r.B * 4);  // 16 LoRA ranks
@@ -128,25 +109,10 @@ PfLayout pf_layout(const Derived& r, int rows) {
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? DFSSM_OK : (int)e; }
 
-// Which layer kernel dfssm_layer_step uses (dfssm_set_layer_kernel).
+// Which layer kernel dfssm_layer_step uses (dfssm_set_layer_kernel). DFSSM_LAYER_AUTO and
+// DFSSM_LAYER_FUSED run the one-launch layer at batch <= 4 where the device and shape take it.
 int g_layer_kernel = DFSSM_LAYER_AUTO;
-// What DFSSM_LAYER_AUTO picks at batch <= 4: the phase-organised layer, one launch per layer
-// (measured at 1.3B, batch 1: 845 us per step; all layers in one launch 850 us; the
-// item-organised layer 917 us).
-constexpr bool kAutoItem = false;
-constexpr bool kAutoMulti = false;
-constexpr bool kAutoXcd = false;
 
-// Whether the current setting runs the XCD-partitioned one-launch layer for these dimensions.
-bool use_xcd_layer(int B, int D, int DI, int H, int P, int N) {
-  const bool want = g_layer_kernel == DFSSM_LAYER_XCD || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoXcd);
-  return want && xcd_layer_supported(B, D, DI, H, P, N);
-}
-// Whether the current setting runs the item-organised one-launch layer for these dimensions.
-bool use_item_layer(int B, int D, int DI, int H, int P) {
-  const bool want = g_layer_kernel == DFSSM_LAYER_ITEM || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoItem);
-  return want && item_layer_grid(B, D, DI, H, P) > 0;
-}
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 bool kdim_ok(int k) { return k > 0 && k % 512 == 0 && k <= 5120; }
@@ -193,20 +159,11 @@ int dfssm_check_dims(const dfssm_dims* d) {
 int dfssm_one_launch_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
   if (!d || dfssm_check_dims(d) != DFSSM_OK) return 0;
   const Derived r = derive(d);
-  const int item = item_plan(cus, blocks_per_cu, r.B, r.D, r.DI, r.H, r.P);
-  if (item > 0) return item;
   return fused_plan(cus, blocks_per_cu, blocks_per_cu, r.B, r.IPO, r.D, r.DI, r.H, r.P, nullptr);
 }
 
-int dfssm_xcd_layer_plan(const dfssm_dims* d, int cus, int blocks_per_cu) {
-  if (!d || dfssm_check_dims(d) != DFSSM_OK) return 0;
-  const Derived r = derive(d);
-  return xcd_plan(cus, blocks_per_cu, r.B, r.D, r.DI, r.H, r.P, r.N);
-}
-
 int dfssm_set_layer_kernel(int which) {
-  if (which != DFSSM_LAYER_AUTO && which != DFSSM_LAYER_FUSED && which != DFSSM_LAYER_FIVE &&
-      which != DFSSM_LAYER_ITEM && which != DFSSM_LAYER_MULTI && which != DFSSM_LAYER_XCD)
+  if (which != DFSSM_LAYER_AUTO && which != DFSSM_LAYER_FUSED && which != DFSSM_LAYER_FIVE)
     return DFSSM_E_RANGE;
   const int prev = g_layer_kernel;
   g_layer_kernel = which;
@@ -422,11 +379,7 @@ static FusedArgs fused_args(const dfssm_model* model, int layer, uint16_t* x, co
   a.gT = (uint32_t*)(ws + w.g_t);
   a.hT = (uint32_t*)(ws + w.h_t);
   a.bcT = (uint32_t*)(ws + w.bc_t);
-  a.lpA = (uint64_t*)(ws + w.lp_a);
-  a.lpC = (uint64_t*)(ws + w.lp_c);
-  a.gP = (uint64_t*)(ws + w.g_p);
   a.dtT = (uint64_t*)(ws + w.dt_t);
-  a.xT = (uint32_t*)(ws + w.x_t);
   a.launches = (uint32_t*)(ws + w.launches);
   a.err = (int*)(ws + w.err);
   a.layer = layer;
@@ -439,88 +392,8 @@ static FusedArgs fused_args(const dfssm_model* model, int layer, uint16_t* x, co
 static int fused_layer(const dfssm_model* model, int layer, uint16_t* x, const dfssm_state* state,
                        void* workspace, void* stream) {
   const Derived r = derive(&model->dims);
-  FusedArgs a = fused_args(model, layer, x, state, workspace);
-  if (use_xcd_layer(r.B, r.D, r.DI, r.H, r.P, r.N)) {
-    const WsLayout w = ws_layout(&model->dims);
-    char* ws = (char*)workspace;
-    a.launches = (uint32_t*)(ws + w.launches_x);
-    a.projT = (uint32_t*)(ws + w.proj_x);
-    a.gT = (uint32_t*)(ws + w.g_x);
-    a.hT = (uint32_t*)(ws + w.h_x);
-    a.bcT = (uint32_t*)(ws + w.bc_x);
-    a.dtT = (uint64_t*)(ws + w.dt_x);
-    a.xflag = (uint32_t*)(ws + w.flag_x);
-    return hip_status(launch_xcd_layer(a, r.B, as_stream(stream)));
-  }
-  if (use_item_layer(r.B, r.D, r.DI, r.H, r.P)) {
-    const WsLayout w = ws_layout(&model->dims);
-    a.launches = (uint32_t*)((char*)workspace + w.launches1);
-    a.bcT = (uint32_t*)((char*)workspace + w.bc_t1);
-    return hip_status(launch_item_layer(a, r.B, as_stream(stream)));
-  }
+  const FusedArgs a = fused_args(model, layer, x, state, workspace);
   return hip_status(launch_fused_layer(a, r.B, as_stream(stream)));
-}
-
-// Strides between the layers of every per-layer pointer the phase-organised layer reads, when
-// each field's layers are equally spaced (one allocation per field, as the Python loader
-// makes them); false otherwise.
-static bool layer_strides(const dfssm_model* model, FusedStrides& st) {
-  const Derived r = derive(&model->dims);
-  const dfssm_layer* L = model->layers;
-  bool ok = true;
-  auto one = [&](auto get) {
-    const long long s = r.L > 1 ? (long long)((const char*)get(L[1]) - (const char*)get(L[0])) : 0;
-    for (int l = 2; l < r.L && ok; ++l)
-      if ((const char*)get(L[l]) - (const char*)get(L[0]) != s * l) ok = false;
-    return s;
-  };
-  st.in_bits = one([](const dfssm_layer& x) { return (const void*)x.in_bits; });
-  st.in_ws = one([](const dfssm_layer& x) { return (const void*)x.in_scale; });
-  st.in_lA = one([](const dfssm_layer& x) { return (const void*)x.in_lA; });
-  st.in_lAs = one([](const dfssm_layer& x) { return (const void*)x.in_lA_s; });
-  st.in_lBq = one([](const dfssm_layer& x) { return (const void*)x.in_lBq; });
-  st.out_bits = one([](const dfssm_layer& x) { return (const void*)x.out_bits; });
-  st.out_ws = one([](const dfssm_layer& x) { return (const void*)x.out_scale; });
-  st.out_lA = one([](const dfssm_layer& x) { return (const void*)x.out_lA; });
-  st.out_lAs = one([](const dfssm_layer& x) { return (const void*)x.out_lA_s; });
-  st.out_lBq = one([](const dfssm_layer& x) { return (const void*)x.out_lBq; });
-  st.conv_w = one([](const dfssm_layer& x) { return (const void*)x.conv_w; });
-  st.conv_b = one([](const dfssm_layer& x) { return (const void*)x.conv_b; });
-  st.A_log = one([](const dfssm_layer& x) { return (const void*)x.A_log; });
-  st.Dp = one([](const dfssm_layer& x) { return (const void*)x.D; });
-  st.dt_bias = one([](const dfssm_layer& x) { return (const void*)x.dt_bias; });
-  st.norm_w = one([](const dfssm_layer& x) { return (const void*)x.norm_w; });
-  st.ln_w = one([](const dfssm_layer& x) { return (const void*)x.ln_w; });
-  st.h = (long long)r.B * r.H * r.P * r.N * (long long)sizeof(float);
-  st.conv = (long long)r.B * r.C * 3 * (long long)sizeof(uint16_t);
-  return ok;
-}
-
-// Whether dfssm_decode_step runs every layer in one launch (strides of the per-layer pointers
-// in st when it does).
-static bool all_layers_one_launch(const dfssm_model* model, FusedStrides& st) {
-  const Derived r = derive(&model->dims);
-  const bool want = g_layer_kernel == DFSSM_LAYER_MULTI || (g_layer_kernel == DFSSM_LAYER_AUTO && kAutoMulti);
-  return want && r.L <= kMaxLayers && fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P, true) &&
-         layer_strides(model, st);
-}
-
-// Every layer of a decode step in one launch of the phase-organised layer, when the setting,
-// the shape and the weight layout allow it; returns DFSSM_E_DIMS (nothing launched) otherwise.
-static int fused_all_layers(const dfssm_model* model, uint16_t* x, const dfssm_state* state, void* workspace,
-                            void* stream) {
-  const Derived r = derive(&model->dims);
-  FusedStrides st{};
-  if (!all_layers_one_launch(model, st)) return DFSSM_E_DIMS;
-  const FusedArgs a = fused_args(model, 0, x, state, workspace);
-  FusedArgs* tab = (FusedArgs*)((char*)workspace + ws_layout(&model->dims).ltab);
-  return hip_status(launch_fused_layers(a, st, tab, r.B, as_stream(stream)));
-}
-
-int dfssm_decode_one_launch(const dfssm_model* model) {
-  if (check_model(model)) return 0;
-  FusedStrides st{};
-  return all_layers_one_launch(model, st) ? 1 : 0;
 }
 
 // Arguments of the matrix-core in_proj (in) or out_proj GEMM of `layer` (batch >= 5).
@@ -687,9 +560,7 @@ int dfssm_layer_step(const dfssm_model* model, int layer, uint16_t* x, const dfs
   int rc = check_layer_args(model, layer, x, state, workspace);
   if (rc) return rc;
   const Derived r = derive(&model->dims);
-  const bool one_launch = g_layer_kernel != DFSSM_LAYER_FIVE &&
-                          (fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P) ||
-                           use_item_layer(r.B, r.D, r.DI, r.H, r.P) || use_xcd_layer(r.B, r.D, r.DI, r.H, r.P, r.N));
+  const bool one_launch = g_layer_kernel != DFSSM_LAYER_FIVE && fused_layer_supported(r.B, r.IPO, r.D, r.DI, r.H, r.P);
   if (one_launch) return fused_layer(model, layer, x, state, workspace, stream);
   if (r.B > 4 && g_layer_kernel != DFSSM_LAYER_FIVE && ssm_prep_supported(r.B, r.DI, r.P)) {
     // four launches: prologue + in_proj, SSM with the out_proj prologue, out_proj
@@ -778,13 +649,8 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
     rc = dfssm_embed(model, tokens, x, workspace, stream);
     if (rc) return rc;
   }
-  rc = fused_all_layers(model, x, state, workspace, stream);
-  if (rc == DFSSM_E_DIMS) {
-    rc = decode_layers(model, x, state, workspace, stream);
-    if (rc) return rc;
-  } else if (rc) {
-    return rc;
-  }
+  rc = decode_layers(model, x, state, workspace, stream);
+  if (rc) return rc;
   return dfssm_lmhead_argmax(model, x, workspace, logits, next, fuse_next_embed ? x : nullptr, stream);
 }
 
@@ -999,9 +865,11 @@ int dfssm_decode_step_static(const dfssm_model* model, const int64_t* tokens, ui
   rc = static_workspace(&model->dims, s, &ws);
   if (rc) return rc;
   rc = dfssm_decode_step(model, tokens, x, state, ws, logits, next, fuse_next_embed, stream);
-  if (rc || !error_out) return rc;
+  if (!error_out) return rc;
+  // also when the step failed after queueing some of its kernels: their flag bits belong to this call
   hipLaunchKernelGGL(take_flag_kernel, dim3(1), dim3(64), 0, s, dfssm_workspace_error_flag(&model->dims, ws), error_out);
-  return hip_status(hipGetLastError());
+  const int rc2 = hip_status(hipGetLastError());
+  return rc ? rc : rc2;
 }
 
 int dfssm_state_density_field(float* h, float* sd_error, int64_t rows, int d_state, const float* thresholds,

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dfssm.h"  // DFSSM_ERR_* bits of the workspace error flag
+
 #define DFSSM_MODE_IN 0
 #define DFSSM_MODE_OUT 1
 #define DFSSM_MODE_SCAFFOLD 2
@@ -86,7 +88,7 @@ constexpr int kGemmMaxRows = 32768;
 struct GemmPro {
   uint32_t* xT;              // (M, N) tagged words of the new x, rewritten by every launch
   uint32_t* launches;        // per-workgroup launch counts (kGemmProMaxWg), zeroed at init
-  int* err;                  // bit 2: a wait timed out
+  int* err;                  // DFSSM_ERR_WAIT_OUT_PROLOGUE: a wait timed out
   const float* norm_w;       // (N) fp32 RMSNorm weight of the next layer
   const int8_t* lB;          // (16, N) its LoRA B, int8 (null: no LoRA intermediate)
   const uint16_t* lBs;       // (16) fp16
@@ -155,7 +157,7 @@ struct SsmPrepArgs {
   SsmArgs s;
   uint32_t* gT;              // (M, H P) tagged words, rewritten by every launch
   uint32_t* launches;        // ((H P / 16 + 16) M) per-workgroup launch counts, zeroed at init
-  int* err;                  // bit 2: a wait timed out
+  int* err;                  // DFSSM_ERR_WAIT_SSM_PROLOGUE: a wait timed out
   const float* norm_w;       // (H P) fp32 gated-RMSNorm weight
   const int8_t* lB;          // (16, H P) LoRA B, int8 (null: no LoRA intermediate)
   const uint16_t* lBs;       // (16) fp16
@@ -281,29 +283,13 @@ struct FusedArgs {
   uint32_t* bcT;             // kXRep copies (stride kBcStride words) of (M, 2 d_state): conv'd B | C
   uint64_t* dtT;             // (M, H, 2): softplus dt and exp(dt A) per head, (tag << 32) | fp32 bits
   uint32_t* launches;        // (G) launch count of each workgroup
-  int* err;                  // error flags (bit 2: a wait timed out)
-  // item-organised layer (layer1.hip) only:
-  uint64_t* lpA;             // kXRep copies (stride kLpStride) of (M, G) LoRA partials of in_proj, two words each
-  uint64_t* lpC;             // kXRep copies (stride kLpStride) of (M, 16 SC) LoRA partials of out_proj
-  uint64_t* gP;              // kXRep copies (stride kGStride) of (M, items, 6): gated SSM output,
-                             // three fp16 values and the tag per word
-  // phase-organised layer: the launch's layers and their tags. Every launch takes the tags
-  // epoch * n_layer + layer + 1 (mod 2^16) of its own layers, so that no word left by another
-  // launch or layer carries a tag a poll waits for.
+  int* err;                  // error flags (DFSSM_ERR_WAIT_LAYER: a wait timed out)
+  // the launch's layer: every launch takes the tag epoch * n_layer + layer + 1 (mod 2^16), so
+  // that no word left by the previous launch carries a tag a poll waits for
   int layer, n_layer;
-  uint32_t* xT;              // multi-layer launch: 2 x kXRep copies (stride kXStride words) of (M, D)
-                             // tagged x words, layer l's output in buffer l % 2
-  uint32_t* xflag;           // XCD-partitioned layer: a tagged word XCD 0 sets once all of g is in
   int D, DI, N, H, P, IPO, C;
 };
 
-// Byte distance between consecutive layers of every per-layer pointer of FusedArgs: the
-// multi-layer launch runs layer l on the pointers of layer 0 advanced by l strides.
-struct FusedStrides {
-  long long in_bits, in_ws, in_lA, in_lAs, in_lBq, out_bits, out_ws, out_lA, out_lAs, out_lBq, conv_w, conv_b,
-      A_log, Dp, dt_bias, norm_w, ln_w, h, conv;
-};
-constexpr int kXStride = 4 * 5120 + 64;  // words between copies of xT (>= 4 * d_model)
 // Words that many workgroups poll (the LoRA intermediates, B | C) are written in kXRep copies at
 // different addresses, so that their polls spread over memory channels instead of queueing on one
 // cache line.
@@ -311,35 +297,12 @@ constexpr int kXRep = 8;
 constexpr int kHStride = 1024;   // words between copies of hT (>= 2 * 4 * 16)
 constexpr int kBcStride = 1088;  // words between copies of bcT (>= 4 * 256)
 constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
-// The XCD-partitioned one-launch layer (batch <= 4): 8 XCDs x 32 workgroups (one per CU; workgroups
-// go to the XCDs round robin); XCD x owns the SSM heads x H/8 .. (x + 1) H/8 - 1, computes their in_proj
-// rows, the B | C rows and the dt rows itself and exchanges them, and its LoRA intermediates,
-// through its own L2 (XCD-scope words: hT, bcT in copy x, dtT at x kDtStride, projT); only g
-// crosses XCDs. 0 = not usable on this device / shape.
-constexpr int kXcd = 8, kXcdWg = 32, kXcdGrid = kXcd * kXcdWg;
-constexpr int kDtStride = 2 * 4 * 320 + 64;  // u64 words between the XCDs' dt words (>= 2 M H)
-int xcd_plan(int cus, int per_cu, int M, int D, int DI, int H, int P, int N);
-bool xcd_layer_supported(int M, int D, int DI, int H, int P, int N);
-hipError_t launch_xcd_layer(const FusedArgs& a, int M, hipStream_t s);
 constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
-
-// The item-organised one-launch layer (layer1.hip): grid = one workgroup per SSM item (head,
-// 16-row block), all co-resident; 0 = not usable on this device / shape.
-constexpr int kLpStride = 4 * 256 * 2 + 64;  // words between copies of lpA / lpC
-constexpr int kGStride = 4 * 256 * 6 + 64;   // words between copies of gP
-int item_layer_grid(int M, int D, int DI, int H, int P);
-hipError_t launch_item_layer(const FusedArgs& a, int M, hipStream_t s);
-int item_plan(int cus, int per_cu, int M, int D, int DI, int H, int P);
-bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P, bool multi = false);
+bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);
 // Grid of the one-launch layer on a device with `cus` CUs where per_cu32 / per_cu64 workgroups of
 // the 32- / 64-row-group instantiations fit per CU; 0 = use the five-kernel form. *rc_out = RC.
 int fused_plan(int cus, int per_cu32, int per_cu64, int M, int IPO, int D, int DI, int H, int P, int* rc_out);
 hipError_t launch_fused_layer(const FusedArgs& a, int M, hipStream_t s);
-// Layers a.layer .. a.n_layer - 1 in one launch (the phase-organised layer looped over layers,
-// x handed from each layer's phase C to the next layer's phase A as tagged words).
-// tab: device memory for n_layer FusedArgs (filled by the launch's first kernel).
-constexpr int kMaxLayers = 256;
-hipError_t launch_fused_layers(const FusedArgs& a, const FusedStrides& st, FusedArgs* tab, int M, hipStream_t s);
 hipError_t launch_dequant_lora_b(const int8_t* B, const uint16_t* Bs, int K, uint16_t* out, hipStream_t s);
 
 hipError_t launch_proj(const ProjArgs& a, int M, int mode, hipStream_t s);

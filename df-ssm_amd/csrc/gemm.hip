@@ -91,7 +91,7 @@ __device__ __forceinline__ void gemm_in_prologue(const GemmPro& p, int D, int m,
     for (int j = 0; j < kProPJ; ++j) good = good && (tid + 1024 * j >= np || pro_tag_ok(xv[j], tag));
     if (good) break;
     if (it == (1u << 18)) {
-      atomicOr(p.err, 4);
+      atomicOr(p.err, DFSSM_ERR_WAIT_OUT_PROLOGUE);
       break;
     }
     __builtin_amdgcn_s_sleep(1);

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   const int64_t t64 = a.tok_tc > 0 ? a.tokens[(size_t)(m / a.tok_tc) * a.tok_ld + a.tok_t0 + m % a.tok_tc] : a.tokens[m];
   const int t = (t64 < 0 || t64 >= a.V) ? 0 : (int)t64;
   if (t64 < 0 || t64 >= a.V) {
-    if (threadIdx.x == 0) atomicOr(a.err_flag, 1);
+    if (threadIdx.x == 0) atomicOr(a.err_flag, DFSSM_ERR_TOKEN_RANGE);
   }
   for (int k = threadIdx.x; k < a.D; k += 256)
     a.x[(size_t)m * a.D + k] = a.f16 ? emb_value<true>(a.emb, a.emb_scale, a.D / 8, t >> 6, t & 63, k)

@@ -184,7 +184,7 @@ __device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int
     for (int j = 0; j < NJ; ++j) good = good && sp_tag_ok(gv[j], tag);
     if (good) break;
     if (it == kSpSpin) {
-      atomicOr(a.err, 4);
+      atomicOr(a.err, DFSSM_ERR_WAIT_SSM_PROLOGUE);
       break;
     }
     __builtin_amdgcn_s_sleep(1);

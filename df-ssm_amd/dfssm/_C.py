@@ -54,7 +54,6 @@ _SIGS = {
     "dfssm_error_string": (ctypes.c_char_p, [c_int]),
     "dfssm_check_dims": (c_int, [ctypes.POINTER(Dims)]),
     "dfssm_one_launch_plan": (c_int, [ctypes.POINTER(Dims), c_int, c_int]),
-    "dfssm_xcd_layer_plan": (c_int, [ctypes.POINTER(Dims), c_int, c_int]),
     "dfssm_set_layer_kernel": (c_int, [c_int]),
     "dfssm_tiled_bits_bytes": (c_size_t, [c_int, c_int]),
     "dfssm_tiled_emb_bytes": (c_size_t, [c_int, c_int]),
@@ -71,7 +70,6 @@ _SIGS = {
     "dfssm_workspace_error_flag": (P, [ctypes.POINTER(Dims), P]),
     "dfssm_embed": (c_int, [ctypes.POINTER(Model), P, P, P, P]),
     "dfssm_layer_step": (c_int, [ctypes.POINTER(Model), c_int, P, ctypes.POINTER(State), P, P]),
-    "dfssm_decode_one_launch": (c_int, [ctypes.POINTER(Model)]),
     "dfssm_layer_phase": (c_int, [ctypes.POINTER(Model), c_int, c_int, P, ctypes.POINTER(State), P, P]),
     "dfssm_lmhead_argmax": (c_int, [ctypes.POINTER(Model), P, P, P, P, P, P]),
     "dfssm_decode_step": (c_int, [ctypes.POINTER(Model), P, P, ctypes.POINTER(State), P, P, P, c_int, P]),

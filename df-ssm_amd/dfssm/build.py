@@ -25,7 +25,7 @@ BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libdfssm_hip.so")
 # profiling variant: the one-launch layer with per-phase wall-clock stamps (-DDFSSM_TIMELINE)
 LIB_TIMELINE = os.path.join(PKG, "libdfssm_hip_timeline.so")
-TIMELINE_SRCS = ("fused.hip", "layer1.hip")
+TIMELINE_SRCS = ("fused.hip",)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 5
+#define DFSSM_ABI_VERSION 6
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
@@ -36,6 +36,18 @@ extern "C" {
 #define DFSSM_E_RANGE (-5)       /* index (layer, token count, size) out of range */
 #define DFSSM_E_SCRATCH (-6)     /* the static workspace is too small for these dimensions */
 #define DFSSM_E_CAPTURE (-7)     /* the call must not run under stream capture */
+
+/* Bits of the workspace error flag (dfssm_workspace_error_flag), set by the kernels and left set
+ * until the caller clears the flag. No counterpart in the reference (its gather raises a device
+ * assert on a bad token id, and its kernels never wait on each other). */
+#define DFSSM_ERR_TOKEN_RANGE 1          /* a token id outside [0, vocab) reached the embedding gather
+                                            (row 0 was used) */
+#define DFSSM_ERR_WAIT_LAYER 4           /* a bounded wait between workgroups of the one-launch layer
+                                            (batch <= 4) timed out: that layer's output is wrong */
+#define DFSSM_ERR_WAIT_SSM_PROLOGUE 8    /* a bounded wait of the SSM + out_proj-prologue launch
+                                            (batch >= 5, DFSSM_PHASE_SSM_PROLOGUE) timed out */
+#define DFSSM_ERR_WAIT_OUT_PROLOGUE 16   /* a bounded wait of the out_proj + next-prologue launch
+                                            (batch >= 5, DFSSM_PHASE_OUT_PROLOGUE) timed out */
 
 typedef struct dfssm_dims {
   int32_t n_layer, d_model, d_inner, d_state, nheads, headdim, ngroups, vocab_size;
@@ -88,36 +100,16 @@ int dfssm_check_dims(const dfssm_dims* dims);
  * rule can be checked without a GPU. No counterpart in the reference (its layers are separate
  * kernel launches, df_ssm_inference.py:161-207). */
 int dfssm_one_launch_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
-/* Grid of the XCD-partitioned one-launch layer (DFSSM_LAYER_XCD) for these dims on a device with
- * `cus` CUs where `blocks_per_cu` of its workgroups fit per CU, or 0 when that layer cannot run
- * (it needs exactly 8 XCDs x 32 CUs, batch <= 4 and a shape whose per-XCD roles fit 32 workgroups).
- * Exposed so that the rule can be checked without a GPU. No counterpart in the reference. */
-int dfssm_xcd_layer_plan(const dfssm_dims* dims, int cus, int blocks_per_cu);
-
 /* Layer kernel selection for dfssm_layer_step / dfssm_decode_step (process-wide; returns the
- * previous setting, or DFSSM_E_RANGE). At batch <= 4: DFSSM_LAYER_FUSED runs the
- * phase-organised one-launch layer where the shape allows it, else five kernels;
- * DFSSM_LAYER_ITEM runs the item-organised one-launch layer (one workgroup per SSM item, grid a
- * power of two <= 256) where the shape allows it, else as DFSSM_LAYER_FUSED;
- * DFSSM_LAYER_MULTI lets dfssm_decode_step run all layers of a step in one launch of the
- * phase-organised layer (when every per-layer weight pointer is equally spaced from layer to
- * layer, as one allocation per field gives), else as DFSSM_LAYER_FUSED; DFSSM_LAYER_XCD runs the
- * XCD-partitioned one-launch layer (8 XCDs x 32 workgroups, each XCD owning 1/8 of the SSM heads
- * and exchanging its words through its own L2; needs exactly 256 CUs) where the device and the
- * shape allow it, else as DFSSM_LAYER_FUSED; DFSSM_LAYER_FIVE always runs five kernels per layer;
- * DFSSM_LAYER_AUTO (default) is the fastest on the benchmark shape (DFSSM_LAYER_FUSED). All give
- * bit-identical results; the setting exists to compare them. No counterpart in the reference. */
+ * previous setting, or DFSSM_E_RANGE). At batch <= 4, DFSSM_LAYER_AUTO (default) and
+ * DFSSM_LAYER_FUSED run the one-launch layer where the device and the shape allow it, else five
+ * kernels; DFSSM_LAYER_FIVE always runs five kernels per layer (and the five phases at batch >= 5).
+ * All give bit-identical results; the setting exists to compare them. No counterpart in the
+ * reference. */
 #define DFSSM_LAYER_AUTO 0
 #define DFSSM_LAYER_FUSED 1
 #define DFSSM_LAYER_FIVE 2
-#define DFSSM_LAYER_ITEM 3
-#define DFSSM_LAYER_MULTI 4
-#define DFSSM_LAYER_XCD 5
 int dfssm_set_layer_kernel(int which);
-/* 1 when dfssm_decode_step runs all layers of a step in one launch with the current setting on
- * the current device (batch <= 4, a shape the phase-organised layer takes, per-layer weights
- * equally spaced), else 0. No counterpart in the reference. */
-int dfssm_decode_one_launch(const dfssm_model* model);
 
 /* ---- load-time layout ------------------------------------------------------------------ */
 /* Bytes of the tiled copy of a (rows, k/32) sign-bit matrix / of a (vocab, row_bytes) table
@@ -241,9 +233,10 @@ int dfssm_decode_step(const dfssm_model* model, const int64_t* tokens, uint16_t*
  * on one GPU (other streams, other threads) race; calls ordered on one stream do not. The first
  * call on a device, and the first after the dimensions change, clears the array's counters with a
  * fill kernel on `stream` and must not be captured (else DFSSM_E_CAPTURE); later calls may be.
- * error_out (device int, may be NULL) receives the workspace error flag of this call (as
- * dfssm_workspace_error_flag: 1 = token id out of range, 4 = a wait of the one-launch layer timed
- * out), which is then cleared. Every other argument is as in dfssm_decode_step. */
+ * error_out (device int, may be NULL) receives the workspace error flag of this call (the
+ * DFSSM_ERR_* bits), which is then cleared; this also happens when the step fails after queueing
+ * some of its kernels, once the static workspace is set up. Every other argument is as in
+ * dfssm_decode_step. */
 #define DFSSM_STATIC_WORKSPACE_BYTES (24u << 20)
 int dfssm_decode_step_static(const dfssm_model* model, const int64_t* tokens, uint16_t* x,
                              const dfssm_state* state, uint16_t* logits, int64_t* next, int fuse_next_embed,

@@ -27,7 +27,7 @@ def test_header_symbols_exported():
 
 def test_version_and_errors():
     L = _C.lib()
-    assert L.dfssm_version() == 5
+    assert L.dfssm_version() == 6
     assert L.dfssm_error_string(-2).decode().startswith("model dimensions")
 
 
@@ -55,6 +55,20 @@ def test_sizes():
     assert L.dfssm_tiled_emb_bytes(50288, 4096) == 50304 * 4096   # fp16 rows
     assert L.dfssm_workspace_bytes(_dims()) > 0
     assert L.dfssm_workspace_bytes(_dims(batch=65)) == 0
+
+
+def test_static_workspace_covers_batch32():
+    """DFSSM_STATIC_WORKSPACE_BYTES (include/dfssm.h: 24 MiB) holds the decode workspace of batch
+    <= 32 at the 1.3B and 2.7B shapes (dfssm_decode_step_static accepts them) and not of batch 64."""
+    text = open(os.path.join(REPO, "include", "dfssm.h")).read()
+    m = re.search(r"#define DFSSM_STATIC_WORKSPACE_BYTES \((\d+)u << (\d+)\)", text)
+    cap = int(m.group(1)) << int(m.group(2))
+    L = _C.lib()
+    shapes = ({}, {"n_layer": 64, "d_model": 2560, "d_inner": 5120, "nheads": 80})
+    for kw in shapes:
+        for B in (1, 4, 5, 17, 32):
+            assert 0 < L.dfssm_workspace_bytes(_dims(batch=B, **kw)) <= cap, (kw, B)
+        assert L.dfssm_workspace_bytes(_dims(batch=64, **kw)) > cap, kw
 
 
 def test_null_and_shape_rejections_before_launch():

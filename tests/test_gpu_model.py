@@ -110,25 +110,23 @@ def test_1p3b_greedy(w13, B, T, n):
     assert gpu.error_flag() == 0
 
 
-def _require_xcd_layer(gpu, kernel):
-    """The XCD-partitioned layer (kernel 5) must really run for these dims on this device."""
+def _require_one_launch(gpu):
+    """The one-launch layer must really run for these dims on this device."""
     from dfssm import _C
-    if kernel == 5:
-        props = torch.cuda.get_device_properties(0)
-        assert _C.lib().dfssm_xcd_layer_plan(gpu.dims, props.multi_processor_count, 1) == 256
+    props = torch.cuda.get_device_properties(0)
+    assert _C.lib().dfssm_one_launch_plan(gpu.dims, props.multi_processor_count, 1) > 0
 
 
-@pytest.mark.parametrize("kernel", [3, 1, 5])   # DFSSM_LAYER_ITEM, DFSSM_LAYER_FUSED, DFSSM_LAYER_XCD
-@pytest.mark.parametrize("B", [1, 3])
-def test_one_launch_layer_equals_five_kernels(tiny_weights, B, kernel):
-    """dfssm_layer_step (one launch at batch <= 4: the item-organised layer, the phase-organised
-    one or the XCD-partitioned one) against dfssm_layer_phase 0..4 (the five-kernel form) on the
-    same inputs: x, SSM state and conv state identical bit for bit."""
+@pytest.mark.parametrize("B", [1, 2, 3, 4])
+def test_one_launch_layer_equals_five_kernels(tiny_weights, B):
+    """dfssm_layer_step (one launch at batch <= 4) against dfssm_layer_phase 0..4 (the five-kernel
+    form) on the same inputs: x, SSM state and conv state identical bit for bit."""
     from dfssm import _C
     w = tiny_weights
-    print(f"one-launch kernel {kernel} B={B}", flush=True)
+    kernel = 1  # DFSSM_LAYER_FUSED
+    print(f"one-launch layer B={B}", flush=True)
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
-    _require_xcd_layer(gpu, kernel)
+    _require_one_launch(gpu)
     gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, 5)))  # non-trivial state
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
@@ -162,7 +160,6 @@ def _decode_run(w, B, kernel, steps, prompt_len=5):
     gpu.ingest(torch.from_numpy(make_prompts(B, w.cfg.vocab_size, prompt_len)))
     prev = lib.dfssm_set_layer_kernel(kernel)
     try:
-        one = lib.dfssm_decode_one_launch(gpu._model)
         out = []
         for _ in range(steps):
             lg, nx = gpu.decode_step_eager(None)
@@ -171,17 +168,16 @@ def _decode_run(w, B, kernel, steps, prompt_len=5):
     finally:
         lib.dfssm_set_layer_kernel(prev)
     assert gpu.error_flag() == 0
-    return one, out, gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
+    return out, gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
 
 
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
-def test_xcd_layer_decode_equals_five_kernels(tiny_weights, B):
-    """dfssm_decode_step with the XCD-partitioned layer (DFSSM_LAYER_XCD) against the five-kernel
+def test_one_launch_decode_equals_five_kernels(tiny_weights, B):
+    """dfssm_decode_step with the one-launch layer (DFSSM_LAYER_FUSED) against the five-kernel
     form, 6 greedy steps: logits, tokens, x and both states identical bit for bit."""
-    print(f"xcd decode B={B}", flush=True)
-    one_x, out_x, x_x, h_x, c_x = _decode_run(tiny_weights, B, 5, 6)
-    one_5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
-    assert one_x == 0 and one_5 == 0
+    print(f"one-launch decode B={B}", flush=True)
+    out_x, x_x, h_x, c_x = _decode_run(tiny_weights, B, 1, 6)
+    out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
     for (lx, nx), (l5, n5) in zip(out_x, out_5):
         assert torch.equal(lx.view(torch.int16), l5.view(torch.int16))
         assert torch.equal(nx, n5)
@@ -196,9 +192,8 @@ def test_batched_ssm_prologue_launch_equals_five_kernels(tiny_weights, B):
     prologue in one launch, g handed over as tagged words) against DFSSM_LAYER_FIVE (separate SSM
     and prologue kernels), 6 greedy steps: logits, tokens, x and both states identical bit for bit."""
     print(f"ssm+prologue decode B={B}", flush=True)
-    one_a, out_a, x_a, h_a, c_a = _decode_run(tiny_weights, B, 0, 6)
-    one_5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
-    assert one_a == 0 and one_5 == 0
+    out_a, x_a, h_a, c_a = _decode_run(tiny_weights, B, 0, 6)
+    out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
     for (la, na), (l5, n5) in zip(out_a, out_5):
         assert torch.equal(la.view(torch.int16), l5.view(torch.int16))
         assert torch.equal(na, n5)
@@ -262,8 +257,8 @@ def test_fused_phases_wide_model_batch64():
                     vocab_size=4096, kw=4)
     w = make_weights(c, seed=11)
     print("wide model d_model 4608 B=64 decode", flush=True)
-    one_a, out_a, x_a, h_a, c_a = _decode_run(w, 64, 0, 3)
-    one_5, out_5, x_5, h_5, c_5 = _decode_run(w, 64, 2, 3)
+    out_a, x_a, h_a, c_a = _decode_run(w, 64, 0, 3)
+    out_5, x_5, h_5, c_5 = _decode_run(w, 64, 2, 3)
     for (la, na), (l5, n5) in zip(out_a, out_5):
         assert torch.equal(la.view(torch.int16), l5.view(torch.int16))
         assert torch.equal(na, n5)
@@ -272,27 +267,8 @@ def test_fused_phases_wide_model_batch64():
     assert torch.equal(c_a.view(torch.int16), c_5.view(torch.int16))
 
 
-@pytest.mark.parametrize("B", [1, 2, 3, 4])
-def test_all_layers_one_launch_equals_five_kernels(tiny_weights, B):
-    """dfssm_decode_step with every layer of a step in one launch (DFSSM_LAYER_MULTI: x handed
-    from layer to layer as tagged words) against the five-kernel form, 6 steps: logits, tokens,
-    x and both states identical bit for bit."""
-    print(f"multi-layer launch B={B}", flush=True)
-    one, out_m, x_m, h_m, c_m = _decode_run(tiny_weights, B, 4, 6)
-    assert one == 1, "the multi-layer launch did not apply"
-    one5, out_5, x_5, h_5, c_5 = _decode_run(tiny_weights, B, 2, 6)
-    assert one5 == 0
-    for t, ((lm, nm), (l5, n5)) in enumerate(zip(out_m, out_5)):
-        assert torch.equal(lm.view(torch.int16), l5.view(torch.int16)), f"step {t}: logits differ"
-        assert torch.equal(nm, n5), f"step {t}: tokens differ"
-    assert torch.equal(x_m.view(torch.int16), x_5.view(torch.int16))
-    assert torch.equal(h_m, h_5)
-    assert torch.equal(c_m.view(torch.int16), c_5.view(torch.int16))
-
-
-@pytest.mark.parametrize("kernel", [3, 1, 5])
 @pytest.mark.parametrize("B", [1, 4])
-def test_one_launch_layer_wide_model(B, kernel):
+def test_one_launch_layer_wide_model(B):
     """d_model 4096 (128 out_proj groups of 32 rows, the widest grid use): the one-launch layer
     against the five-kernel form, bit for bit."""
     from dfssm import _C
@@ -300,9 +276,10 @@ def test_one_launch_layer_wide_model(B, kernel):
     c = DFSSMConfig(n_layer=1, d_model=4096, d_inner=4096, d_state=128, nheads=64, headdim=64, ngroups=1,
                     vocab_size=1000, kw=4)
     w = make_weights(c, seed=5)
-    print(f"wide one-launch kernel {kernel} B={B}", flush=True)
+    kernel = 1  # DFSSM_LAYER_FUSED
+    print(f"wide one-launch layer B={B}", flush=True)
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
-    _require_xcd_layer(gpu, kernel)
+    _require_one_launch(gpu)
     gpu.ingest(torch.from_numpy(make_prompts(B, c.vocab_size, 3)))
     lib = _C.lib()
     x0, h0, c0 = gpu.x.clone(), gpu.h_state.clone(), gpu.conv_state.clone()
