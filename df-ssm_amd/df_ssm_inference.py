@@ -35,17 +35,79 @@ from dfssm import _C  # noqa: E402
 from dfssm.format import DFSSMWeights, EMB_I8, LORA_RANK, read_dfssm  # noqa: E402
 
 
+def _untile_signs(tiled: torch.Tensor, rows: int, k: int) -> torch.Tensor:
+    """(rows, k) int8 +-1 matrix from the tiled sign bits of dfssm_tile_bits
+    ([rows_pad/64][k/128][64 rows][4 words], word h of chunk c = columns 128c + 32h .. + 31, bit b =
+    column + b, 1 = +1) -- the matrix the reference unpacks at load (df_ssm_inference.py:23-29)."""
+    rp = (rows + 63) // 64 * 64
+    words = tiled.view(rp // 64, k // 128, 64, 4).permute(0, 2, 1, 3).reshape(rp, k // 32)[:rows]
+    words = words.to(torch.int64) & 0xFFFFFFFF
+    shifts = torch.arange(32, device=tiled.device, dtype=torch.int64)
+    bits = (words[:, :, None] >> shifts) & 1                     # (rows, k/32, 32): column 32j + b
+    return (2 * bits - 1).to(torch.int8).reshape(rows, k)
+
+
 class LayerWeights:
-    """Device tensors of one layer. Names follow the reference's LayerWeights
-    (df_ssm_inference.py:32-44) where the meaning is the same; the scaffold is kept as tiled sign
-    bits (in_bits / out_bits) and the LoRA factors stay int8 with their fp16 row scales."""
+    """Device tensors of one layer, with the reference's LayerWeights attributes
+    (df_ssm_inference.py:32-44, built at :70-98): in_scale / out_scale, conv_weight, conv_bias,
+    A_log, D, dt_bias, norm_weight, layer_norm_weight as stored; in_w_T / out_w_T ((K, N) int8 +-1,
+    pre-transposed) and the fp16-dequantized in_lora_A (N, 16), in_lora_B (16, K), out_lora_A,
+    out_lora_B are read-only views built on first access (the kernels never read them).
+    What the kernels read: the scaffold as tiled sign bits (in_bits / out_bits, 1 bit per weight),
+    the LoRA factors as stored in the file (int8 in_lA / in_lB with fp16 row scales in_lA_s /
+    in_lB_s, likewise out_*), and the load-time fp16 LoRA-B tables in_lora_Bq / out_lora_Bq."""
     __slots__ = (
         "in_bits", "in_scale", "out_bits", "out_scale",
-        "in_lora_A", "in_lora_A_scale", "in_lora_B", "in_lora_B_scale",
-        "out_lora_A", "out_lora_A_scale", "out_lora_B", "out_lora_B_scale",
+        "in_lA", "in_lA_s", "in_lB", "in_lB_s",
+        "out_lA", "out_lA_s", "out_lB", "out_lB_s",
         "conv_weight", "conv_bias", "A_log", "D", "dt_bias",
         "norm_weight", "layer_norm_weight", "in_lora_Bq", "out_lora_Bq",
+        "dims", "_compat",
     )
+
+    def _view(self, name, build):
+        if self._compat is None:
+            self._compat = {}
+        if name not in self._compat:
+            self._compat[name] = build()
+        return self._compat[name]
+
+    @property
+    def in_w_T(self) -> torch.Tensor:
+        """(d_model, in_proj_out) int8 +-1: the reference's in_w_T (df_ssm_inference.py:72-74)."""
+        D, IPO = self.dims[0], self.dims[2]
+        return self._view("in_w_T", lambda: _untile_signs(self.in_bits, IPO, D).t().contiguous())
+
+    @property
+    def out_w_T(self) -> torch.Tensor:
+        """(d_inner, d_model) int8 +-1: the reference's out_w_T (df_ssm_inference.py:87-89)."""
+        D, DI = self.dims[0], self.dims[1]
+        return self._view("out_w_T", lambda: _untile_signs(self.out_bits, D, DI).t().contiguous())
+
+    @staticmethod
+    def _deq(a: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+        return (a.float() * s.float().unsqueeze(1)).half()
+
+    @property
+    def in_lora_A(self) -> torch.Tensor:
+        """(in_proj_out, 16) fp16 = (lA * lA_s).half(), df_ssm_inference.py:82."""
+        return self._view("in_lora_A", lambda: self._deq(self.in_lA, self.in_lA_s))
+
+    @property
+    def in_lora_B(self) -> torch.Tensor:
+        """(16, d_model) fp16 = (lB * lB_s).half(), df_ssm_inference.py:83 (the table the kernels
+        read, in_lora_Bq)."""
+        return self.in_lora_Bq
+
+    @property
+    def out_lora_A(self) -> torch.Tensor:
+        """(d_model, 16) fp16, df_ssm_inference.py:96."""
+        return self._view("out_lora_A", lambda: self._deq(self.out_lA, self.out_lA_s))
+
+    @property
+    def out_lora_B(self) -> torch.Tensor:
+        """(16, d_inner) fp16, df_ssm_inference.py:97 (= out_lora_Bq)."""
+        return self.out_lora_Bq
 
 
 def _require_gpu(device) -> torch.device:
@@ -66,9 +128,16 @@ def _dev(a: np.ndarray, dev) -> torch.Tensor:
     return torch.from_numpy(a).to(dev)
 
 
-# Bits of the workspace error flag (set by the kernels, read and cleared by DFSSMModel).
-ERR_TOKEN_RANGE = 1    # a token id outside [0, vocab) reached the embedding gather (row 0 was used)
-ERR_WAIT_TIMEOUT = 4   # a bounded wait inside the one-launch layer timed out (workgroups not co-resident)
+# Bits of the workspace error flag (include/dfssm.h DFSSM_ERR_*; set by the kernels, read and
+# cleared by DFSSMModel). Each bounded wait between workgroups has its own bit, named for the
+# launch whose wait gave up.
+ERR_TOKEN_RANGE = 1          # a token id outside [0, vocab) reached the embedding gather (row 0 was used)
+ERR_WAIT_LAYER = 4           # the one-launch layer (batch <= 4)
+ERR_WAIT_SSM_PROLOGUE = 8    # the SSM + out_proj-prologue launch (batch >= 5)
+ERR_WAIT_OUT_PROLOGUE = 16   # the out_proj + next-layer-prologue launch (batch >= 5)
+
+_WAIT_CAUSE = ("(its workgroups were not all running at once, e.g. because another process or stream "
+               "shared the GPU, or a workgroup it waited for failed)")
 
 
 def describe_error_flag(flag: int) -> str:
@@ -76,10 +145,13 @@ def describe_error_flag(flag: int) -> str:
     causes = []
     if flag & ERR_TOKEN_RANGE:
         causes.append("token id out of range [0, vocab) in a device token tensor (embedding row 0 was used)")
-    if flag & ERR_WAIT_TIMEOUT:
-        causes.append("a wait between workgroups of the one-launch layer timed out (the GPU did not run all "
-                      "its workgroups at once, e.g. because another process or stream shared it)")
-    rest = flag & ~(ERR_TOKEN_RANGE | ERR_WAIT_TIMEOUT)
+    if flag & ERR_WAIT_LAYER:
+        causes.append("a wait between workgroups of the one-launch layer (batch <= 4) timed out " + _WAIT_CAUSE)
+    if flag & ERR_WAIT_SSM_PROLOGUE:
+        causes.append("a wait of the SSM + gated-norm prologue launch (batch >= 5) timed out " + _WAIT_CAUSE)
+    if flag & ERR_WAIT_OUT_PROLOGUE:
+        causes.append("a wait of the out_proj + next-layer prologue launch (batch >= 5) timed out " + _WAIT_CAUSE)
+    rest = flag & ~(ERR_TOKEN_RANGE | ERR_WAIT_LAYER | ERR_WAIT_SSM_PROLOGUE | ERR_WAIT_OUT_PROLOGUE)
     if rest:
         causes.append(f"unknown error bits {rest:#x}")
     return "; ".join(causes)
@@ -195,11 +267,12 @@ class DFSSMModel:
             F = {k: v[li] for k, v in fields.items()}
             lw = LayerWeights()
             lw.in_bits, lw.in_scale = F["in_bits"], F["in_scale"]
-            lw.in_lora_A, lw.in_lora_A_scale = F["in_lA"], F["in_lA_s"]
-            lw.in_lora_B, lw.in_lora_B_scale = F["in_lB"], F["in_lB_s"]
+            lw.in_lA, lw.in_lA_s = F["in_lA"], F["in_lA_s"]
+            lw.in_lB, lw.in_lB_s = F["in_lB"], F["in_lB_s"]
             lw.out_bits, lw.out_scale = F["out_bits"], F["out_scale"]
-            lw.out_lora_A, lw.out_lora_A_scale = F["out_lA"], F["out_lA_s"]
-            lw.out_lora_B, lw.out_lora_B_scale = F["out_lB"], F["out_lB_s"]
+            lw.out_lA, lw.out_lA_s = F["out_lA"], F["out_lA_s"]
+            lw.out_lB, lw.out_lB_s = F["out_lB"], F["out_lB_s"]
+            lw.dims, lw._compat = (D, DI, IPO), None
             lw.conv_weight, lw.conv_bias = F["conv_w"], F["conv_b"]
             lw.A_log, lw.D, lw.dt_bias = F["A_log"], F["D"], F["dt_bias"]
             lw.norm_weight, lw.layer_norm_weight = F["norm_w"], F["ln_w"]
@@ -355,18 +428,24 @@ class DFSSMModel:
         self._graph = self._capture(lambda: self._decode(self._tok, self.logits, self._next, fuse=True))
 
     def forward(self, token_ids):
-        """token_ids (batch,) int64 -> fp16 logits (batch, vocab); advances the state by one token."""
+        """token_ids (batch,) int64 -> fp16 logits (batch, vocab); advances the state by one token.
+
+        Like the reference's forward (df_ssm_inference.py:219-224) this only enqueues work: for
+        token ids already on the device it never waits for the GPU, so the reference's loop
+        `logits = forward(t); t = logits.argmax(-1)` (:234-236) stays asynchronous. Host token ids
+        (lists, CPU tensors) are range-checked here (IndexError, nothing launched); device ids
+        out of range set ERR_TOKEN_RANGE in the error flag (row 0 is used), which check_errors(),
+        generate(), decode(), prefill() and ingest() report."""
         tok = torch.as_tensor(token_ids).view(-1)
         if tok.numel() != self.batch_size:
             raise ValueError(f"expected {self.batch_size} token ids, got {tok.numel()}")
-        _check_token_range(tok, self.cfg.vocab_size)
+        if tok.device.type != "cuda":
+            _check_token_range(tok, self.cfg.vocab_size)
         self._tok.copy_(tok.to(self.device, torch.int64))
         if self._graph is None:
             self._capture_graph()
         self._graph.replay()
-        out = self.logits.clone()
-        self.check_errors()
-        return out
+        return self.logits.clone()
 
     def _gen_graph(self, S: int):
         if S not in self._gen_graphs:
@@ -580,9 +659,10 @@ class DFSSMModel:
 
     def error_flag(self) -> int:
         """The workspace error flag (synchronizes): 0, or an OR of ERR_TOKEN_RANGE (1: a token id
-        outside [0, vocab) reached the embedding gather, which then read row 0) and
-        ERR_WAIT_TIMEOUT (4: a bounded wait between workgroups of the one-launch layer timed out,
-        so that layer's output is wrong). The flag stays set until clear_error_flag()."""
+        outside [0, vocab) reached the embedding gather, which then read row 0) and the wait
+        bits ERR_WAIT_LAYER (4), ERR_WAIT_SSM_PROLOGUE (8), ERR_WAIT_OUT_PROLOGUE (16): a bounded
+        wait between workgroups of that launch timed out, so its output is wrong. The flag stays
+        set until clear_error_flag()."""
         off = self._err - self.workspace.data_ptr()
         return int(self.workspace[off:off + 4].view(torch.int32).item())
 

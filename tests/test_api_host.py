@@ -24,7 +24,7 @@ def _dims(**kw):
     ({"batch": 4}, 256, 1, 256),
     ({"batch": 5}, 256, 1, 0),         # batch >= 5 always runs five kernels
     ({}, 140, 1, 0),                   # 133 in_proj groups + 16 LoRA workgroups do not fit
-    ({}, 2048, 1, 256),                # item-organised layer: one workgroup per SSM item
+    ({}, 2048, 1, 1024),               # one workgroup per CU, at most 1024
     ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 256, 1, 256),
     ({"batch": 65}, 256, 1, 0),
 ])
@@ -32,29 +32,33 @@ def test_one_launch_plan(kw, cus, per_cu, grid):
     assert _C.lib().dfssm_one_launch_plan(_dims(**kw), cus, per_cu) == grid
 
 
-@pytest.mark.parametrize("kw,cus,per_cu,grid", [
-    ({}, 256, 1, 256),                 # 1.3B shape on MI355X: 8 XCDs x 32 CUs
-    ({"batch": 4}, 256, 1, 256),
-    ({}, 256, 0, 0),                   # the instantiation does not fit a CU
-    ({}, 304, 1, 0),                   # not 8 x 32 CUs
-    ({"batch": 5}, 256, 1, 0),         # batch >= 5: five kernels
-    ({"d_model": 2560, "d_inner": 5120, "nheads": 80}, 256, 1, 256),   # 2.7B: 26 phase-A groups per XCD
-    ({"d_model": 512, "d_inner": 1024, "nheads": 16}, 256, 1, 256),    # the tests' tiny model
-    ({"d_model": 4096, "d_inner": 4096}, 256, 1, 256),                 # 16 out_proj groups per XCD
-    ({"d_model": 512, "d_inner": 1024, "nheads": 32}, 256, 1, 256),    # 4 heads x 32 rows per XCD: 2 row groups
-    ({"d_model": 5120, "d_inner": 5120, "nheads": 80}, 256, 1, 256),   # 20 out_proj groups = 2 x 10 z groups
-    ({"d_model": 4096, "d_inner": 2048, "nheads": 32}, 256, 1, 0),     # 16 out_proj groups > 2 x 4 z groups
-])
-def test_xcd_layer_plan(kw, cus, per_cu, grid):
-    assert _C.lib().dfssm_xcd_layer_plan(_dims(**kw), cus, per_cu) == grid
-
-
 def test_describe_error_flag():
+    """Every bit names its own source (the launch whose bounded wait gave up), as include/dfssm.h
+    defines them."""
     assert dfi.describe_error_flag(0) == ""
+    assert (dfi.ERR_TOKEN_RANGE, dfi.ERR_WAIT_LAYER, dfi.ERR_WAIT_SSM_PROLOGUE, dfi.ERR_WAIT_OUT_PROLOGUE) == \
+        (1, 4, 8, 16)
     assert "token id out of range" in dfi.describe_error_flag(dfi.ERR_TOKEN_RANGE)
-    assert "timed out" in dfi.describe_error_flag(dfi.ERR_WAIT_TIMEOUT)
-    both = dfi.describe_error_flag(dfi.ERR_TOKEN_RANGE | dfi.ERR_WAIT_TIMEOUT | 16)
-    assert "out of range" in both and "timed out" in both and "0x10" in both
+    layer = dfi.describe_error_flag(dfi.ERR_WAIT_LAYER)
+    ssm = dfi.describe_error_flag(dfi.ERR_WAIT_SSM_PROLOGUE)
+    out = dfi.describe_error_flag(dfi.ERR_WAIT_OUT_PROLOGUE)
+    assert "one-launch layer" in layer and "timed out" in layer
+    assert "SSM" in ssm and "timed out" in ssm and "one-launch" not in ssm
+    assert "out_proj" in out and "timed out" in out and "one-launch" not in out
+    assert len({layer, ssm, out}) == 3
+    every = dfi.describe_error_flag(1 | 4 | 8 | 16 | 64)
+    assert all(x in every for x in ("out of range", layer, ssm, out, "0x40"))
+
+
+def test_error_bits_match_header():
+    """The Python constants are the C header's DFSSM_ERR_* values."""
+    import os
+    import re
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "dfssm.h")).read()
+    vals = dict(re.findall(r"#define DFSSM_ERR_(\w+) (\d+)", hdr))
+    assert {k: int(v) for k, v in vals.items()} == {
+        "TOKEN_RANGE": dfi.ERR_TOKEN_RANGE, "WAIT_LAYER": dfi.ERR_WAIT_LAYER,
+        "WAIT_SSM_PROLOGUE": dfi.ERR_WAIT_SSM_PROLOGUE, "WAIT_OUT_PROLOGUE": dfi.ERR_WAIT_OUT_PROLOGUE}
 
 
 def _hostless_model(B=2):

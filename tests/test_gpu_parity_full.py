@@ -166,6 +166,69 @@ def test_2p7b_layers_prefill_300_chunked():
     assert torch.equal(pf.decode(4), st.decode(4))
 
 
+# ------------------------------------------------------------------------------ wide prefill vs the oracle
+@pytest.mark.parametrize("case", ["tiny_b16_t33", "2p7b_layers_b64_t6"])
+def test_generate_wide_prefill_vs_oracle(case):
+    """generate(prompt=...) whose prefill takes the many-row kernels (prep_rows_kernel,
+    expand_bits_kernel, gemm_wide_kernel: one chunk of >= 256 rows), against the oracle's
+    step-by-step ingestion: greedy tokens and the logits of one more step identical, state within
+    1e-3. The tiny model at batch 16 with a 33-token prompt (512 prefill rows); config 4's layer
+    shapes with the full vocabulary at batch 64 with a 6-token prompt (320 rows)."""
+    if case == "tiny_b16_t33":
+        from dfssm.synth import config_tiny
+        c, B, T, n = config_tiny(n_layer=3), 16, 33, 4
+    else:
+        c = DFSSMConfig(n_layer=2, d_model=2560, d_inner=5120, d_state=128, nheads=80, headdim=64, ngroups=1,
+                        vocab_size=50288, kw=4)
+        B, T, n = 64, 6, 2
+    assert B * (T - 1) >= 256  # the wide path
+    w = make_weights(c, seed=21)
+    print(f"wide prefill vs oracle: {case}", flush=True)
+    prompts = make_prompts(B, c.vocab_size, T, base_seed=4000)
+    orc = O.OracleModel(w, B)
+    ref, _ = orc.generate(prompts, n)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    got = gpu.generate(n_tokens=n, prompt=torch.from_numpy(prompts), return_tokens=True, verbose=False)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    lg = _np16(gpu.forward(torch.from_numpy(ref[:, -1]).to(DEV))).astype(np.float32)
+    lo, _ = orc.step(ref[:, -1])
+    assert np.abs(lg - lo.astype(np.float32)).max() == 0.0
+    assert np.abs(gpu.h_state.cpu().numpy() - orc.h).max() <= 1e-3 * np.abs(orc.h).max()
+    gpu.check_errors()
+
+
+def test_config4_full_depth_vs_oracle_fixture():
+    """The whole config-4 model (2.7B shape, 64 layers, vocabulary 50288; bench.py's weights) at
+    batch 4 against the oracle's run committed in tests/golden/oracle_2p7b_64layer_b4.npz
+    (tests/golden/make_config4_golden.py): a 129-token prompt prefilled in two chunks of 64 tokens
+    (256 rows each: the wide kernels and a chunk boundary), 4 greedy tokens, then one more step:
+    tokens identical, and the SHA-256 of its fp16 logits, of the fp32 SSM state and of the conv
+    state equal to the oracle's."""
+    import hashlib
+    import os
+    from dfssm.synth import config_2p7b
+
+    def sha(a):
+        return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oracle_2p7b_64layer_b4.npz"))
+    w = make_weights(config_2p7b(), seed=0)
+    B = g["prompt"].shape[0]
+    print("config 4 full depth (64 layers) vs oracle fixture, batch 4", flush=True)
+    gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
+    gpu.PREFILL_MAX_ROWS = 256
+    got = gpu.generate(n_tokens=g["tokens"].shape[1], prompt=torch.from_numpy(g["prompt"]), return_tokens=True,
+                       verbose=False)
+    np.testing.assert_array_equal(got.cpu().numpy(), g["tokens"])
+    lg = _np16(gpu.forward(torch.from_numpy(g["tokens"][:, -1]).to(DEV)))
+    np.testing.assert_array_equal(lg[:, :8].view(np.uint16), g["logits_head"].view(np.uint16))
+    assert sha(lg) == str(g["logits_sha256"])
+    np.testing.assert_array_equal(gpu._next.cpu().numpy(), g["next_token"])
+    assert sha(gpu.h_state.cpu().numpy()) == str(g["state_sha256"])
+    assert sha(_np16(gpu.conv_state)) == str(g["conv_sha256"])
+    gpu.check_errors()
+
+
 # ------------------------------------------------------------------------------ files from the exporter
 @pytest.mark.parametrize("emb_code", [EMB_F16, EMB_I8])
 @pytest.mark.parametrize("B", [1, 5])

@@ -2,8 +2,11 @@
 for callers that cannot allocate) against dfssm_decode_step with a caller-allocated workspace:
 from identical states and tokens, logits, greedy tokens, the next-step input x and both states
 must be bit-identical, step after step. Two calls in a row with different inputs, the second
-smaller (batch 4, then batch 1, then the 1.3B shape at batch 1), so that the array is reused
-and re-cleared when the dimensions change; the error flag reported through error_out is 0.
+smaller (batch 4, then batch 1, then the 1.3B shape at batch 1; at batch >= 5, where the array
+also holds the per-workgroup launch counts and tagged words of the fused SSM and out_proj
+launches and the batched head's digit planes: batch 17, then 5, then the 1.3B shape at batch
+32), so that the array is reused and re-cleared when the dimensions change; the error flag
+reported through error_out is 0.
 """
 import ctypes
 
@@ -56,15 +59,29 @@ def _run_pair(m: DFSSMModel, steps: int, seed: int):
     assert m.error_flag() == 0
 
 
-def test_static_decode_matches_workspace_decode():
+@pytest.fixture(scope="module")
+def w13():
+    return make_weights(config_1p3b(), seed=0)
+
+
+def test_static_decode_matches_workspace_decode(w13):
     w = make_weights(config_tiny(n_layer=3), seed=0)
     print("static decode: tiny model, batch 4", flush=True)
     _run_pair(DFSSMModel.from_weights(w, device=DEV, batch_size=4), steps=5, seed=3000)
     print("static decode: tiny model, batch 1 (smaller, after batch 4)", flush=True)
     _run_pair(DFSSMModel.from_weights(w, device=DEV, batch_size=1), steps=5, seed=3100)
     print("static decode: 1.3B shape, batch 1", flush=True)
-    w13 = make_weights(config_1p3b(), seed=0)
     _run_pair(DFSSMModel.from_weights(w13, device=DEV, batch_size=1), steps=3, seed=3200)
+
+
+def test_static_decode_batched_launches(w13):
+    w = make_weights(config_tiny(n_layer=3), seed=1)
+    print("static decode: tiny model, batch 17", flush=True)
+    _run_pair(DFSSMModel.from_weights(w, device=DEV, batch_size=17), steps=4, seed=3300)
+    print("static decode: tiny model, batch 5 (smaller, after batch 17)", flush=True)
+    _run_pair(DFSSMModel.from_weights(w, device=DEV, batch_size=5), steps=4, seed=3400)
+    print("static decode: 1.3B shape, batch 32", flush=True)
+    _run_pair(DFSSMModel.from_weights(w13, device=DEV, batch_size=32), steps=3, seed=3500)
 
 
 def test_static_decode_rejects_oversized_dims():
