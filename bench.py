@@ -408,10 +408,12 @@ def phase_sweep(B, path, layers=12):
     log(f"phase sweep batch {B}: {layers} layers x 5 kernels + head done")
 
 
-TIMELINE_STAMPS = {0: "start", 14: "A: x in, sum of squares", 1: "A: prologue done (GEMV workgroups)",
+TIMELINE_STAMPS = {0: "start", 16: "A: x arrived (wave 0)", 18: "A: sum of squares barrier",
+                   14: "A: x normalized", 20: "A: amax barrier", 1: "A: prologue done (GEMV workgroups)",
                    2: "A: GEMV done", 3: "A: LoRA h in",
                    4: "A: epilogue / LoRA rank stored", 5: "B: poll start", 6: "B: item inputs in",
-                   7: "B: SSM done", 8: "C: prologue start", 15: "C: g in, sum of squares",
+                   7: "B: SSM done", 8: "C: prologue start", 17: "C: g arrived (wave 0)", 19: "C: sum of squares barrier",
+                   15: "C: g normalized", 21: "C: amax barrier",
                    9: "C: prologue done", 10: "C: GEMV done",
                    11: "C: LoRA h in", 12: "C: epilogue / LoRA rank stored", 13: "end"}
 
@@ -440,7 +442,7 @@ def timeline(B, path, graphs=4):
     for _ in range(graphs):
         g.replay()
     torch.cuda.synchronize()
-    buf = np.zeros((64, 256, 16), np.uint64)
+    buf = np.zeros((64, 256, 24), np.uint64)
     _C.check(lib.dfssm_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "timeline_read")
     names, kernel = TIMELINE_STAMPS, "layer_fused_kernel"
     t = buf.astype(np.int64)

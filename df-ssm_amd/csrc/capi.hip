@@ -63,7 +63,7 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.launches = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
   w.gtick = off;    off = align_up(off + (size_t)r.head_groups * 4);
   w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
-  w.g_t = off;      off = align_up(off + (size_t)r.B * r.DI * 4);
+  w.g_t = off;      off = align_up(off + (size_t)kGRep * kGStride * 4);
   w.h_t = off;      off = align_up(off + (size_t)kXRep * kHStride * 4);
   w.dt_t = off;     off = align_up(off + 2 * (size_t)r.B * r.H * 8);
   w.bc_t = off;     off = align_up(off + (size_t)kXRep * kBcStride * 4);

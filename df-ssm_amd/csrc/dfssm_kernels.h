@@ -277,7 +277,7 @@ struct FusedArgs {
   // words exchanged between workgroups of a launch: (tag << 16) | fp16 bits, tag = the launch's
   // epoch mod 2^16
   uint32_t* projT;           // (M, IPO): gate z sigma(z) | conv'd xBC (dt rows unused)
-  uint32_t* gT;              // (M, DI): gated SSM output
+  uint32_t* gT;              // kGRep copies (stride kGStride words) of (M, DI): gated SSM output, in gpos order
   uint32_t* hT;              // kXRep copies (stride kHStride words) of (2, M, 16): LoRA intermediates of
                              // in_proj / out_proj; consumer workgroup w polls copy w % kXRep
   uint32_t* bcT;             // kXRep copies (stride kBcStride words) of (M, 2 d_state): conv'd B | C
@@ -296,6 +296,8 @@ struct FusedArgs {
 constexpr int kXRep = 8;
 constexpr int kHStride = 1024;   // words between copies of hT (>= 2 * 4 * 16)
 constexpr int kBcStride = 1088;  // words between copies of bcT (>= 4 * 256)
+constexpr int kGRep = 8;                   // copies of the gated output words of the one-launch layer
+constexpr int kGStride = 4 * 5120 + 1088;  // words between them (>= 4 * d_inner)
 constexpr int kFusedMaxGroups = 256;  // in_proj row groups of 64
 constexpr int kFusedMaxGrid = 1024;   // workgroups of the one-launch layer
 bool fused_layer_supported(int M, int IPO, int D, int DI, int H, int P);

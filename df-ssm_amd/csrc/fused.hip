@@ -89,7 +89,7 @@ __device__ __forceinline__ int bix() {
 // at the end of the launch to dfssm_timeline[launch % kTlSlots][workgroup][stamp]; read on the host
 // with dfssm_timeline_read. Product builds compile TL(k) to nothing.
 #ifdef DFSSM_TIMELINE
-constexpr int kTlSlots = 64, kTlWg = 256, kTlStamps = 16;
+constexpr int kTlSlots = 64, kTlWg = 256, kTlStamps = 24;
 __device__ unsigned long long dfssm_timeline[kTlSlots][kTlWg][kTlStamps];
 __shared__ unsigned long long tl_s[kTlStamps];
 #define TL(k)                                                                   \
@@ -119,9 +119,9 @@ struct FusedLds {
   // 8j + 2 (s % 4) + s / 4 holds the columns 32j + s + 8b in its bytes b = 0..3 (s = 0..7)
   uint32_t q[M][kFMaxK / 4];
   int T[M][64][kFW + 1];  // per-wave GEMV partials of each row (padded against bank conflicts)
-  double rd[M][kFW];   // per-wave partial sums of squares
-  double rh[M][kFW];   // per-wave partial LoRA sums
-  float rf[M][kFW];    // per-wave partial amax
+  double rd[M][kFW];   // per-wave partial sums of squares (0 for waves without activations)
+  double rh[M][kFW];   // per-wave partial LoRA sums (likewise)
+  float rf[M][kFW];    // per-wave partial amax (likewise)
   int ri[M][kFW];      // per-wave partial sum q (0 for waves without activations)
   float hl[M][DFSSM_LORA_R];
   float xs[M];
@@ -150,7 +150,9 @@ struct ConvPend {
 // Position of column c of the gated output g among its tagged words (K = d_inner): the thread
 // that holds column c in the phase-C prologue (t = c / 8, columns 8t..8t+7) polls its 8 words as
 // 4 adjacent pairs, pair p at 64-bit index p K / 8 + t, so that each wave-wide poll of one pair
-// is one contiguous 512 bytes.
+// is one contiguous 512 bytes. The words are written in kGRep copies kGStride words apart (phase-C
+// workgroup w polls copy w % kGRep): 64 workgroups polling one 16 KiB block queue on the few
+// memory channels it maps to (one copy: 736 us per decode step at batch 1, eight: 722 us).
 __device__ __forceinline__ int gpos(int c, int K) {
   const int t = c >> 3, i = c & 7;
   return 2 * ((i >> 1) * (K >> 3) + t) + (i & 1);
@@ -307,6 +309,7 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
         av[m] = pi.av[m];
       }
     }
+    TL(OUT ? 17 : 16);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       double part = 0.0;
@@ -318,14 +321,19 @@ __device__ __forceinline__ void norm_rows(FusedLds<M>& L, const PIn<M>& pi, cons
       const double wsum = wave_sum_dpp_f64(part);
       if (lane == 0) L.rd[m][wave] = wsum;
     }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) L.rd[m][wave] = 0.0;
   }
   lds_barrier();
+  TL(OUT ? 19 : 18);
   if (dw) {
     const float wv[8] = {pi.w0[0], pi.w0[1], pi.w0[2], pi.w0[3], pi.w1[0], pi.w1[1], pi.w1[2], pi.w1[3]};
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      double ss = 0.0;
-      for (int w = 0; w < nd; ++w) ss += L.rd[m][w];
+      double ss = 0.0;  // every wave's partial, all loads in flight together (0 from the other waves)
+#pragma unroll
+      for (int w = 0; w < kFW; ++w) ss += L.rd[m][w];
       const float var = (float)ss * (1.0f / (float)K);
       const float r = 1.0f / sqrt_rn(var + 1e-5f);
       float mxm = 0.0f;
@@ -358,7 +366,7 @@ __device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t a, int b) {
 // Thread t = 4j + b holds q of columns 32j + 8b + s (s = 0..7) as the bytes b of the dwords s of
 // block j; after the quad transpose it holds the dwords s = b and s = b + 4 and stores them as one
 // 64-bit word at dword 8j + 2b (each wave-wide store 512 contiguous bytes).
-template <int M>
+template <int M, int TLI>  // TLI: timeline stamp after the barrier (profiling builds)
 __device__ __forceinline__ void quantize_rows(FusedLds<M>& L, const u32x4 (&xn)[M], const float (&mx)[M], int K) {
   const int tid = tix(), lane = tid & 63, wave = tid >> 6, nd = K >> 9;
   const bool dw = wave < nd;
@@ -368,14 +376,19 @@ __device__ __forceinline__ void quantize_rows(FusedLds<M>& L, const u32x4 (&xn)[
       const float wmax = wave_max_dpp_f32(mx[m]);
       if (lane == 0) L.rf[m][wave] = wmax;
     }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) L.rf[m][wave] = 0.0f;
   }
   lds_barrier();
+  TL(TLI);
   if (dw) {
     const int b = tid & 3;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float amax = L.rf[m][0];
-      for (int w = 1; w < nd; ++w) amax = fmaxf(amax, L.rf[m][w]);
+#pragma unroll
+      for (int w = 1; w < kFW; ++w) amax = fmaxf(amax, L.rf[m][w]);
       const float xs = quant_scale(amax);
       const float rinv = quant_rcp(xs);
       if (tid == 0) L.xs[m] = xs;
@@ -512,13 +525,17 @@ __device__ __forceinline__ void lora_rank(FusedLds<M>& L, const uint16_t* x, con
       const double hw = wave_sum_dpp_f64(hacc);
       if (lane == 0) L.rh[m][wave] = hw;
     }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) L.rh[m][wave] = 0.0;
   }
   lds_barrier();
   if (tid < kXRep) {  // one copy per thread
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       double t = 0.0;
-      for (int w = 0; w < nd; ++w) t += L.rh[m][w];
+#pragma unroll
+      for (int w = 0; w < kFW; ++w) t += L.rh[m][w];
       st_dev(hout + tid * kHStride + m * DFSSM_LORA_R + r, tagged(tag, f2h((float)t)));
     }
   }
@@ -689,11 +706,11 @@ __device__ __forceinline__ void ssm_item(FusedLds<M>& L, const FusedArgs& a, int
   hv.y = __builtin_fmaf(I.abar, h0.y, X * h2f((uint16_t)(bp >> 16)));
   double acc = (double)h2f((uint16_t)cp) * (double)hv.x + (double)h2f((uint16_t)(cp >> 16)) * (double)hv.y;
   st_dev((uint64_t*)state_row(a, t), __builtin_bit_cast(uint64_t, hv));
-  acc = wave_sum_dpp_f64(acc);
-  if (lane == 0) {
+  acc = wave_sum_dpp_f64(acc);  // the same value in every lane
+  if (lane < kGRep) {            // lane c writes copy c (one store instruction for all copies)
     const float y = r16((float)acc + xv * Dh);
     const float gv = r16(y * h2f(I.gate[wave]));
-    st_dev(a.gT + (size_t)t.m * a.DI + gpos(t.head * a.P + p, a.DI), tagged(tag, f2h(gv)));
+    st_dev(a.gT + (size_t)lane * kGStride + (size_t)t.m * a.DI + gpos(t.head * a.P + p, a.DI), tagged(tag, f2h(gv)));
   }
 }
 
@@ -747,7 +764,7 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       float mx[M];
       norm_rows<M, false>(L, pa, nullptr, a.D, 0u, a.err, xn, mx);  // x loaded ahead, no polls
       TL(14);
-      quantize_rows<M>(L, xn, mx, a.D);
+      quantize_rows<M, 20>(L, xn, mx, a.D);
     }
     lds_barrier();  // q published
     TL(1);
@@ -813,9 +830,9 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     {
       u32x4 xn[M];
       float mx[M];
-      norm_rows<M, true>(L, pc, a.gT, a.DI, tag, a.err, xn, mx);
+      norm_rows<M, true>(L, pc, a.gT + (size_t)(wg % kGRep) * kGStride, a.DI, tag, a.err, xn, mx);
       TL(15);
-      quantize_rows<M>(L, xn, mx, a.DI);
+      quantize_rows<M, 21>(L, xn, mx, a.DI);
     }
     lds_barrier();  // q published
     TL(9);
@@ -838,7 +855,8 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     }
   } else if (wg < gC + DFSSM_LORA_R) {
     lds_barrier();
-    lora_rank<M, true>(L, nullptr, a.gT, a.DI, a.norm_w, a.out_lBq, wg - gC, hC, tag_now(), a.err, tag_now());
+    lora_rank<M, true>(L, nullptr, a.gT + (size_t)(wg % kGRep) * kGStride, a.DI, a.norm_w, a.out_lBq, wg - gC, hC,
+                       tag_now(), a.err, tag_now());
     TL(12);
   }
   lds_barrier();  // every wave has read the launch count
