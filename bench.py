@@ -283,8 +283,9 @@ def cpu_baseline(model_path, prompt, n_tokens):
     """The reference's cpu_inference.c (oracle/_ref, HEADDIM 64) on the same .dfssm file and prompt,
     timed on this host: warm-up step, reset, the prompt untimed, n_tokens timed greedy steps
     (cpu_inference_driver.py:186-204). Run twice in child processes, so that OpenMP reads its
-    settings at load: 4 threads (the reference's published setting, README.md:67) and the physical
-    cores of one socket (at most the 16 CPUs a one-GPU box shares), both with
+    settings at load: 4 threads (the reference's published setting, README.md:67) and every
+    physical core this process may use -- SMT siblings counted once, capped by the cgroup's CPU
+    quota and by one socket's cores and the 16 CPUs a one-GPU box shares -- both with
     OMP_PROC_BIND=close OMP_PLACES=cores and the NumPy BLAS threads set to match."""
     import subprocess
     from oracle import ref_driver
@@ -292,7 +293,8 @@ def cpu_baseline(model_path, prompt, n_tokens):
         log("reference CPU kernels unavailable (not built or no AVX-512 VNNI on this host)")
         return None
     info = ref_driver.cpu_description()
-    socket_threads = max(1, min(info["cores_per_socket"], info["allowed_cpus"], 16))
+    socket_threads = max(1, min(info["cores_per_socket"], info["usable_cores"], 16))
+    log(f"host CPUs: {info}")
     runs = []
     for threads in sorted({4, socket_threads}):
         env = dict(os.environ)

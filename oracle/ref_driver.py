@@ -131,12 +131,44 @@ def cpu_description() -> dict:
             if "cpu cores" in cur:
                 cores[cur["physical id"]] = int(cur["cpu cores"])
     try:
-        allowed = len(os.sched_getaffinity(0))
+        allowed_set = sorted(os.sched_getaffinity(0))
     except (AttributeError, OSError):
-        allowed = os.cpu_count() or 1
+        allowed_set = list(range(os.cpu_count() or 1))
     per_socket = max(cores.values()) if cores else (os.cpu_count() or 1)
+    phys_allowed = _physical_cores(allowed_set)
+    quota = _cgroup_cpu_quota()
+    usable = phys_allowed if quota is None else max(1, min(phys_allowed, int(quota)))
     return {"model": model, "sockets": max(1, len(phys)), "cores_per_socket": per_socket,
-            "logical_cpus": os.cpu_count(), "allowed_cpus": allowed}
+            "logical_cpus": os.cpu_count(), "allowed_cpus": len(allowed_set),
+            "allowed_physical_cores": phys_allowed, "cgroup_cpu_quota": quota, "usable_cores": usable}
+
+
+def _physical_cores(cpus) -> int:
+    """Number of distinct physical cores among `cpus` (SMT siblings counted once), from
+    /sys/devices/system/cpu/cpuN/topology/thread_siblings_list; len(cpus) if that is unreadable."""
+    groups = set()
+    for c in cpus:
+        try:
+            groups.add(open(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list").read().strip())
+        except OSError:
+            return len(cpus)
+    return max(1, len(groups))
+
+
+def _cgroup_cpu_quota():
+    """CPUs this process's cgroup may use (quota / period), or None when unlimited or unknown:
+    cgroup v2 cpu.max ("max 100000" or "<quota> <period>"), else v1 cpu.cfs_quota_us / cfs_period_us."""
+    try:
+        q, p = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        return None if q == "max" else float(q) / float(p)
+    except (OSError, ValueError):
+        pass
+    try:
+        q = float(open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read())
+        p = float(open("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read())
+        return None if q <= 0 else q / p
+    except (OSError, ValueError):
+        return None
 
 
 def main(argv=None) -> int:
