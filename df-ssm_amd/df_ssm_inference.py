@@ -672,8 +672,8 @@ class DFSSMModel:
 
     def check_errors(self) -> None:
         """Read the workspace error flag (synchronizes); if it is set, clear it and raise
-        DFSSMError naming the cause. generate(), decode(), forward(), prefill() and ingest()
-        call it after their work."""
+        DFSSMError naming the cause. generate(), decode(), prefill() and ingest() call it after
+        their work; forward() does not (it only enqueues, as the reference's forward does)."""
         flag = self.error_flag()
         if flag:
             self.clear_error_flag()
