@@ -32,6 +32,8 @@ sys.path.insert(0, REPO)
 
 PEAK_GBS = 8000.0     # MI355X HBM3E, GB/s
 STEPS_PER_GRAPH = 8
+SCAFFOLD_WS_BYTES = 64 << 10   # DFSSM_SCAFFOLD_WORKSPACE_BYTES
+SCAFFOLD_ERR_OFFSET = 1024     # DFSSM_SCAFFOLD_ERROR_OFFSET
 
 
 def log(msg):
@@ -368,12 +370,13 @@ def scaffold_microbench(Ms=(1, 4, 16, 32), min_bytes=1 << 30, reps=3):
             xs = (torch.rand(M, device=dev, generator=g) * 0.04 + 0.01).half()
             h = torch.empty(M, 16, dtype=torch.float16, device=dev)
             y = torch.empty(M, N, dtype=torch.float16, device=dev)
+            xw = torch.zeros(SCAFFOLD_WS_BYTES // 4, dtype=torch.int32, device=dev)  # exchange workspace
 
             def call(i):
                 _C.check(lib.dfssm_scaffold_lora_gemm(
                     bits[i].data_ptr(), ws[i].data_ptr(), q.data_ptr(), xs.data_ptr(), xn.data_ptr(),
                     lA[i].data_ptr(), lAs[i].data_ptr(), lBq[i].data_ptr(), M, N, K, h.data_ptr(), None,
-                    y.data_ptr(), _C.stream()), "scaffold_lora_gemm")
+                    y.data_ptr(), xw.data_ptr(), _C.stream()), "scaffold_lora_gemm")
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
                 for i in range(n):
@@ -387,6 +390,8 @@ def scaffold_microbench(Ms=(1, 4, 16, 32), min_bytes=1 << 30, reps=3):
             e1.record()
             e1.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+            if int(xw[SCAFFOLD_ERR_OFFSET // 4].item()):
+                raise RuntimeError("scaffold op: a wait for the LoRA intermediates timed out")
             b = scaffold_op_bytes(M, N, K)
             gbs = b / (us * 1e-6) / 1e9
             res[M] = {"us_per_call": round(us, 3), "bytes_per_call": b, "gbs": round(gbs, 1),
@@ -644,7 +649,8 @@ def scaffold_roofline(sc):
     return {"bound": "hbm", "kernel": "dfssm_scaffold_lora_gemm in_proj (K 2048 -> N 8512), M = 1, "
                                       f"{r['weight_copies']} rotated weight copies",
             "achieved": r["gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
-            "bytes_per_launch": r["bytes_per_call"], "us_per_launch": r["us_per_call"], "traffic": None}
+            "bytes_per_launch": r["bytes_per_call"], "us_per_launch": r["us_per_call"],
+            "traffic": measured_traffic(1, "scaffold in_proj M=1")}
 
 
 def main():
@@ -665,6 +671,8 @@ def main():
     ap.add_argument("--phase-sweep", type=int, default=0,
                     help="only run the five layer kernels on 12 layers and the head at this batch (counter runs)")
     ap.add_argument("--scaffold", type=int, default=1, help="run the rotated scaffold microbench (0: skip)")
+    ap.add_argument("--scaffold-only", type=int, default=0,
+                    help="run only the rotated scaffold microbench at this M (a short program for counter runs)")
     ap.add_argument("--timeline", type=int, default=0,
                     help="only print the per-phase timeline of the one-launch layer at this batch (1..4), "
                          "from the profiling build libdfssm_hip_timeline.so")
@@ -684,6 +692,9 @@ def main():
         return
     if a.timeline:
         print(json.dumps(timeline(a.timeline, a.model_path)), flush=True)
+        return
+    if a.scaffold_only:
+        print(json.dumps(scaffold_microbench(Ms=(a.scaffold_only,))), flush=True)
         return
     if a.decode_only:
         path = a.model_path if a.shape == "1p3b" else a.model_path_2p7b

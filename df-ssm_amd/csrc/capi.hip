@@ -227,14 +227,23 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
 int dfssm_scaffold_lora_gemm(const uint32_t* tiled_bits, const uint16_t* wscale, const int8_t* q,
                              const uint16_t* xscale, const uint16_t* xn, const int8_t* lA, const uint16_t* lA_s,
                              const uint16_t* lBq, int M, int N, int K, uint16_t* lora_h, int32_t* acc_out,
-                             uint16_t* y_out, void* stream) {
+                             uint16_t* y_out, void* workspace, void* stream) {
   if (!tiled_bits || !wscale || !q || !xscale || !xn || !lA || !lA_s || !lBq || !lora_h || !y_out)
     return DFSSM_E_NULL;
   if (M < 1 || M > 64) return DFSSM_E_BATCH;
   if (N <= 0 || !kdim_ok(K)) return DFSSM_E_DIMS;
-  if (!aligned16(tiled_bits) || !aligned16(q) || !aligned16(xn) || !aligned16(lBq) || !aligned16(lA))
+  if (!aligned16(tiled_bits) || !aligned16(q) || !aligned16(xn) || !aligned16(lBq) || !aligned16(lA) ||
+      !aligned16(workspace))
     return DFSSM_E_ALIGN;
   hipStream_t s = as_stream(stream);
+  // one launch: rank workgroups compute the intermediates once and hand them over. Its GEMV runs on
+  // the VALU, M K values per workgroup: at M K > 8192 (out_proj K = 4096 at M = 4: 10.8 us per call
+  // against 8.5) the matrix-core GEMM below is faster.
+  if (workspace && M <= 4 && M * K <= 8192 && (N + 63) / 64 <= kScafMaxGroups) {
+    ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, lA, lA_s, nullptr, N, K, xn, lBq, lora_h,
+                   (uint32_t*)workspace};
+    return hip_status(launch_scaffold_xchg(a, M, s));
+  }
   if (M == 1 && N >= kScaffoldGemvMinN) {  // one launch, the GEMV's workgroups compute the intermediates
     ScaffoldArgs a{tiled_bits, q, xscale, wscale, acc_out, y_out, lA, lA_s, nullptr, N, K, xn, lBq, lora_h};
     return hip_status(launch_scaffold(a, M, s));

@@ -121,7 +121,18 @@ struct ScaffoldArgs {
   const uint16_t* xn;        // (M, K) fp16
   const uint16_t* lBq;       // (16, K) fp16(B_i8 * B_s)
   uint16_t* h_out;           // (M, 16) fp16
+  // exchange workspace of the one-launch LoRA form (rank workgroups hand the intermediates to the
+  // GEMV workgroups as tagged words): per-workgroup call counts, an error word, then kScafRep
+  // copies of the 16 M tagged words; null: the intermediates are computed in every workgroup
+  uint32_t* ws;
 };
+constexpr int kScafGrid = 256;                    // workgroups of every exchange launch
+constexpr int kScafMaxGroups = kScafGrid - 16;    // 64-row output groups after the 16 rank workgroups
+constexpr int kScafErr = kScafGrid, kScafWords = kScafGrid + 64;
+constexpr int kScafRep = 8, kScafStride = 1024;  // copies of the tagged intermediates, words apart
+constexpr size_t kScafWsBytes = (size_t)(kScafWords + kScafRep * kScafStride) * 4;
+static_assert(kScafWsBytes <= DFSSM_SCAFFOLD_WORKSPACE_BYTES, "scaffold exchange workspace");
+static_assert(kScafErr * 4 == DFSSM_SCAFFOLD_ERROR_OFFSET, "scaffold exchange error word");
 
 // LoRA intermediates of the stand-alone scaffold op: h[m][r] = fp16(sum_k xn[m][k] * lBq[r][k]).
 struct LoraHArgs {
@@ -316,6 +327,7 @@ hipError_t launch_gemm(const GemmArgs& a, int mode, hipStream_t s);
 size_t gemm_wide_w8_bytes(int N, int K);
 hipError_t launch_gemm_wide(const GemmArgs& a, int mode, int8_t* w8, hipStream_t s);
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s);
+hipError_t launch_scaffold_xchg(const ScaffoldArgs& a, int M, hipStream_t s);  // a.ws set, M <= 4
 hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s);
 hipError_t launch_ssm(const SsmArgs& a, int M, hipStream_t s);
 hipError_t launch_conv(const ConvArgs& a, int M, hipStream_t s);

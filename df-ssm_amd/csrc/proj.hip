@@ -342,6 +342,7 @@ __global__ __launch_bounds__(kPrepRowsT) void prep_rows_kernel(PrepArgs a, int M
 constexpr int kNT = 1024;
 constexpr int kNW = kNT / 64;
 constexpr int kMaxCPW = (kMaxK / 128 + kNW - 1) / kNW;
+constexpr uint32_t kScafSpinMax = 1u << 18;  // polls of the intermediates before giving up
 
 template <int M>
 struct ProjLds {
@@ -493,50 +494,51 @@ __global__ __launch_bounds__(kNT) void proj_kernel(ProjArgs a) {
 // are exact in fp32, so this is lora_h_kernel's sum in another order (fp64 sums of exact products:
 // the same value while they stay exact, the assumption the one-launch layer's LoRA split makes
 // too). Workgroup 0 writes the intermediates out.
-template <int M, bool LORA>
+template <int M, bool LORA, int KB>
 __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
+  constexpr int K = 512 * KB, CH = K / 128, NB = K / 64;
+  constexpr int CPW = (CH + kNW - 1) / kNW;  // sign-bit chunks per wave
+  constexpr int QB = (NB + kNW - 1) / kNW;   // 64-value q blocks per wave and row
+  constexpr int XI = (K / 8 + kNT - 1) / kNT;  // xn vectors per thread and row
   __shared__ ProjLds<M> L;
-  __shared__ __attribute__((aligned(16))) uint16_t xns[LORA ? M : 1][LORA ? kMaxK : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t xns[LORA ? M : 1][LORA ? K : 8];
   __shared__ int Sred[kNW][M];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x;
-  const int K = a.K, CH = K / 128, NB = K / 64;
   // ---- small operands first: q bytes of this wave's 64-value blocks, the xn rows (to LDS) and
-  // this wave's LoRA-B row (rank = wave) ----
-  // (unconditional loads from clamped indices: a load in a branch makes the compiler wait for
-  // every outstanding load where the paths join)
-  constexpr int kQB = (kMaxK / 64 + kNW - 1) / kNW;  // 64-value blocks per wave and row
-  int8_t qv[M][kQB];
+  // this wave's LoRA-B row (rank = wave). Every load is unconditional: a load in a branch makes the
+  // compiler wait for every outstanding load where the paths join. Indices past the operand (only
+  // where K / 64 or K / 128 is not a multiple of the 16 waves) re-read its last block. ----
+  int8_t qv[M][QB];
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int j = 0; j < kQB; ++j) {
+    for (int j = 0; j < QB; ++j) {
       const int b = wave + kNW * j;
-      qv[m][j] = a.q[(size_t)m * K + 64 * (b < NB ? b : NB - 1) + lane];
+      const int bc = (NB % kNW == 0 || b < NB) ? b : NB - 1;
+      qv[m][j] = a.q[(size_t)m * K + 64 * bc + lane];
     }
-  constexpr int kLB = kMaxK / 512;  // 512-column blocks
-  constexpr int kXI = (kMaxK / 8 + kNT - 1) / kNT;  // xn vectors per thread and row
-  u32x4 bq[kLB], xv8[LORA ? M : 1][kXI];
+  u32x4 bq[KB], xv8[LORA ? M : 1][XI];
   if (LORA) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-      for (int i = 0; i < kXI; ++i) {
+      for (int i = 0; i < XI; ++i) {
         const int c = tid + kNT * i;  // 8-column vector of row m (stored to LDS below)
         xv8[m][i] = *(const u32x4*)(a.xn + (size_t)m * K + 8 * (c < K / 8 ? c : K / 8 - 1));
       }
 #pragma unroll
-    for (int v = 0; v < kLB; ++v)
-      bq[v] = *(const u32x4*)(a.lBq + (size_t)wave * K + 512 * (v < K / 512 ? v : K / 512 - 1) + 8 * lane);
+    for (int v = 0; v < KB; ++v)
+      bq[v] = *(const u32x4*)(a.lBq + (size_t)wave * K + 512 * v + 8 * lane);
   }
   __builtin_amdgcn_sched_barrier(0);  // the small loads stay ahead of the bit stream
   // ---- the sign-bit chunks and the epilogue row data ----
   const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + lane;
-  u32x4 wb[kMaxCPW];
+  u32x4 wb[CPW];
 #pragma unroll
-  for (int j = 0; j < kMaxCPW; ++j) {  // chunks past CH re-read the last one (not used)
+  for (int j = 0; j < CPW; ++j) {
     const int c = wave + kNW * j;
-    wb[j] = ld_nt(bits + (size_t)(c < CH ? c : CH - 1) * 64);
+    wb[j] = ld_nt(bits + (size_t)((CH % kNW == 0 || c < CH) ? c : CH - 1) * 64);
   }
   const int n = g * 64 + lane;
   const bool erow = tid < M * 64 && n < a.N;
@@ -559,7 +561,7 @@ __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-      for (int i = 0; i < kXI; ++i) {
+      for (int i = 0; i < XI; ++i) {
         const int c = tid + kNT * i;
         *(u32x4*)&xns[m][8 * (c < K / 8 ? c : K / 8 - 1)] = xv8[m][i];
       }
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
   for (int m = 0; m < M; ++m) {
     qsum[m] = 0;
 #pragma unroll
-    for (int j = 0; j < kQB; ++j) {
+    for (int j = 0; j < QB; ++j) {
       const int b = wave + kNW * j;
       if (b < NB) {  // wave-uniform
         const int q = qv[m][j];
@@ -593,15 +595,13 @@ __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
     for (int m = 0; m < M; ++m) {
       double acc = 0.0;  // this lane's columns 512 v + 8 lane .. + 7, then one wave sum
 #pragma unroll
-      for (int v = 0; v < kLB; ++v) {
-        if (v < K / 512) {  // uniform
-          const u32x4 xv = *(const u32x4*)&xns[m][512 * v + 8 * lane];
+      for (int v = 0; v < KB; ++v) {
+        const u32x4 xv = *(const u32x4*)&xns[m][512 * v + 8 * lane];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = h2f((uint16_t)(xv[e >> 1] >> (16 * (e & 1))));
-            const float b = h2f((uint16_t)(bq[v][e >> 1] >> (16 * (e & 1))));
-            acc += (double)(x * b);
-          }
+        for (int e = 0; e < 8; ++e) {
+          const float x = h2f((uint16_t)(xv[e >> 1] >> (16 * (e & 1))));
+          const float b = h2f((uint16_t)(bq[v][e >> 1] >> (16 * (e & 1))));
+          acc += (double)(x * b);
         }
       }
       const double t = wave_sum_dpp_f64(acc);
@@ -625,7 +625,7 @@ __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
 #pragma unroll
     for (int b = 0; b < 8; ++b) cnt[m][b] = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxCPW; ++j) {
+  for (int j = 0; j < CPW; ++j) {
     const int c = wave + kNW * j;
     if (c < CH) {
 #pragma unroll
@@ -679,6 +679,212 @@ __global__ __launch_bounds__(kNT) void scaffold_fused_kernel(ScaffoldArgs a) {
       }
       a.y_out[(size_t)m * a.N + n] = f2h(out);
     }
+  }
+}
+
+// The stand-alone scaffold op with LoRA in one launch, the intermediates computed once: workgroups
+// 0..15 are rank workgroups (h[m][r] for every row m, published as tagged words in kScafRep copies),
+// workgroups 16.. run the GEMV of 64 output rows each and poll the 16 M words of their copy before
+// the epilogue. A rank workgroup never waits and is dispatched before every GEMV workgroup, so every
+// wait ends. Every launch has kScafGrid workgroups (those past the output rows only count the call),
+// and each workgroup index keeps its own call count in the workspace: all counts are equal at a
+// launch's start, so the count + 1 is the tag of the launch's words, known to every workgroup
+// without any exchange.
+__device__ __forceinline__ uint32_t scaf_tag(uint32_t c) { return (c + 1u) & 0xffffu; }
+
+template <int M, int KB>
+__global__ __launch_bounds__(kNT) void scaffold_xchg_kernel(ScaffoldArgs a) {
+  constexpr int K = 512 * KB, CH = K / 128, NB = K / 64;
+  constexpr int CPW = (CH + kNW - 1) / kNW;
+  __shared__ int Tred[kNW][M][64];  // per-wave row partials of the GEMV
+  __shared__ int Sred[kNW][M];      // per-wave sums of q
+  __shared__ float hl[M][DFSSM_LORA_R];
+  __shared__ double Rred[M][kNW];   // rank workgroups: per-wave partial sums
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // An offset the compiler cannot see is zero: the count's address then looks per-lane, so the
+  // count stays in a vector register, waited for where it is used (a uniform load goes to a scalar
+  // register at once, which waits for it before the data loads are issued).
+  uint32_t zoff = 0u;
+  asm volatile("" : "+v"(zoff));
+  // every argument into registers at once: the compiler otherwise loads the argument block in
+  // three dependent pieces around the branches below, a scalar-memory round trip each
+  asm volatile("" ::"s"(a.bits), "s"(a.q), "s"(a.xscale), "s"(a.wscale), "s"(a.acc_out), "s"(a.y_out),
+               "s"(a.lA), "s"(a.lAs), "s"(a.xn), "s"(a.lBq), "s"(a.h_out), "s"(a.ws), "s"(a.N));
+  uint32_t* ws = a.ws;
+  uint32_t* cnt = ws + blockIdx.x + zoff;
+  if (blockIdx.x < DFSSM_LORA_R) {
+    // ---- rank workgroup r: h[m][r] for all rows; thread t < K / 8 owns columns 8t..8t+7 ----
+    const int r = blockIdx.x;
+    const int c = tid < K / 8 ? tid : K / 8 - 1;  // waves past the row re-read its last vector
+    const uint32_t e = ld_dev(cnt);  // first: the tagged stores wait for it
+    u32x4 xv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) xv[m] = *(const u32x4*)(a.xn + (size_t)m * K + 8 * c);
+    const u32x4 bv = *(const u32x4*)(a.lBq + (size_t)r * K + 8 * c);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      double acc = 0.0;
+      if (wave < KB) {  // uniform
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float x = h2f((uint16_t)(xv[m][k >> 1] >> (16 * (k & 1))));
+          const float b = h2f((uint16_t)(bv[k >> 1] >> (16 * (k & 1))));
+          acc += (double)(x * b);
+        }
+      }
+      const double s = wave_sum_dpp_f64(acc);
+      if (lane == 0) Rred[m][wave] = s;
+    }
+    lds_barrier();
+    if (tid < kScafRep) {  // one copy per thread
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < kNW; ++w) t += Rred[m][w];
+        const uint16_t hb = f2h((float)t);
+        st_dev(ws + kScafWords + tid * kScafStride + m * DFSSM_LORA_R + r, (scaf_tag(e) << 16) | hb);
+        if (tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + r] = hb;
+      }
+    }
+    if (tid == 0) st_dev(cnt, e + 1u);
+    return;
+  }
+  const int g = blockIdx.x - DFSSM_LORA_R;
+  if (g * 64 >= a.N) {  // past the output rows: count the call
+    if (tid == 0) st_dev(cnt, ld_dev(cnt) + 1u);
+    return;
+  }
+  // ---- GEMV workgroup: wave w owns the 128-column chunks c = w + 16 j of its 64 rows; it loads the
+  // q bytes of exactly those columns and builds their bit planes itself (wave-uniform ballots, in
+  // scalar registers), so the GEMV needs no exchange between waves. All loads unconditional. ----
+  int8_t qv[M][CPW][2];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int c = wave + kNW * j;
+      const int cc = (CH % kNW == 0 || c < CH) ? c : CH - 1;
+      qv[m][j][0] = a.q[(size_t)m * K + 128 * cc + lane];
+      qv[m][j][1] = a.q[(size_t)m * K + 128 * cc + 64 + lane];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  const u32x4* bits = (const u32x4*)a.bits + (size_t)g * CH * 64 + lane;
+  u32x4 wb[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int c = wave + kNW * j;
+    wb[j] = ld_nt(bits + (size_t)((CH % kNW == 0 || c < CH) ? c : CH - 1) * 64);
+  }
+  const int n = g * 64 + lane;
+  const bool erow = tid < M * 64 && n < a.N;
+  const int em = tid >> 6;
+  const int nc = n < a.N ? n : a.N - 1, mc = em < M ? em : M - 1;
+  const uint16_t ws_raw = a.wscale[nc], xs_raw = a.xscale[mc];
+  const u32x4 la = *(const u32x4*)(a.lA + (size_t)nc * DFSSM_LORA_R);
+  const uint16_t as_raw = a.lAs[nc];
+  const uint32_t e = ld_dev(cnt);
+  __builtin_amdgcn_sched_barrier(0);
+  // first poll of this workgroup's copy of the intermediates, completed after the GEMV
+  const uint32_t* hsrc = ws + kScafWords + (g % kScafRep) * kScafStride;
+  uint32_t hv = tid < M * DFSSM_LORA_R ? ld_dev(hsrc + tid) : 0u;
+  // ---- planes and GEMV, chunk by chunk ----
+  int qsum[M];
+  uint32_t cntb[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    qsum[m] = 0;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) cntb[m][b] = 0;
+  }
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int c = wave + kNW * j;
+    if (c < CH) {  // wave-uniform
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint32_t pl[2][16];
+        planes64(qv[m][j][0], pl[0]);
+        planes64(qv[m][j][1], pl[1]);
+        qsum[m] += qv[m][j][0] + qv[m][j][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = wb[j][i];
+#pragma unroll
+          for (int b = 0; b < 8; ++b) cntb[m][b] += __builtin_popcount(w & pl[i >> 1][8 * (i & 1) + b]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    int t = 0;
+#pragma unroll
+    for (int b = 0; b < 7; ++b) t += (int)(cntb[m][b] << b);
+    t -= (int)(cntb[m][7] << 7);
+    Tred[wave][m][lane] = t;
+    const int s = wave_sum_dpp_i32(qsum[m]);
+    if (lane == 0) Sred[wave][m] = s;
+  }
+  if (tid < M * DFSSM_LORA_R) {  // the intermediates (bounded wait)
+    const uint32_t tag = scaf_tag(e);
+    for (uint32_t it = 0; (hv >> 16) != tag; ++it) {
+      if (it == kScafSpinMax) {
+        atomicOr((int*)(ws + kScafErr), 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      hv = ld_dev(hsrc + tid);
+    }
+    hl[tid / DFSSM_LORA_R][tid % DFSSM_LORA_R] = h2f((uint16_t)hv);
+  }
+  lds_barrier();
+  if (erow) {
+    const int m = em;
+    int T = 0, S = 0;
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) {
+      T += Tred[w][m][lane];
+      S += Sred[w][m];
+    }
+    const int acc = 2 * T - S;
+    if (a.acc_out) a.acc_out[(size_t)m * a.N + n] = acc;
+    const float y = r16(r16(r16((float)acc) * h2f(xs_raw)) * h2f(ws_raw));
+    const float as = h2f(as_raw);
+    double lo = 0.0;
+#pragma unroll
+    for (int rr = 0; rr < DFSSM_LORA_R; ++rr) {
+      const float aq = r16((float)(int8_t)(la[rr >> 2] >> (8 * (rr & 3))) * as);
+      lo += (double)hl[m][rr] * (double)aq;
+    }
+    a.y_out[(size_t)m * a.N + n] = f2h(r16((float)lo + y));
+  }
+  if (tid == 0) st_dev(cnt, e + 1u);
+}
+
+template <int M>
+static hipError_t launch_scaffold_x(const ScaffoldArgs& a, hipStream_t s) {
+  const dim3 grid(kScafGrid);
+  switch (a.K / 512) {
+#define DFSSM_SCAF_KB(kb) \
+  case kb: hipLaunchKernelGGL((scaffold_xchg_kernel<M, kb>), grid, dim3(kNT), 0, s, a); break;
+    DFSSM_SCAF_KB(1) DFSSM_SCAF_KB(2) DFSSM_SCAF_KB(3) DFSSM_SCAF_KB(4) DFSSM_SCAF_KB(5)
+    DFSSM_SCAF_KB(6) DFSSM_SCAF_KB(7) DFSSM_SCAF_KB(8) DFSSM_SCAF_KB(9) DFSSM_SCAF_KB(10)
+#undef DFSSM_SCAF_KB
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_scaffold_xchg(const ScaffoldArgs& a, int M, hipStream_t s) {
+  if (a.K > kMaxK || a.K % 512 || M < 1 || M > 4 || !a.ws || !a.xn || !a.lBq || !a.h_out || !a.lA ||
+      !a.lAs || !a.y_out || !a.wscale || !a.xscale || a.N < 1 || (a.N + 63) / 64 > kScafMaxGroups)
+    return hipErrorInvalidValue;
+  switch (M) {
+    case 1: return launch_scaffold_x<1>(a, s);
+    case 2: return launch_scaffold_x<2>(a, s);
+    case 3: return launch_scaffold_x<3>(a, s);
+    default: return launch_scaffold_x<4>(a, s);
   }
 }
 
@@ -789,22 +995,33 @@ hipError_t launch_prep(const PrepArgs& a, int M, int mode, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int M, bool LORA>
+static hipError_t launch_scaffold_k(const ScaffoldArgs& a, int groups, hipStream_t s) {
+  switch (a.K / 512) {
+#define DFSSM_SCAF_KB(kb) \
+  case kb: hipLaunchKernelGGL((scaffold_fused_kernel<M, LORA, kb>), dim3(groups), dim3(kNT), 0, s, a); break;
+    DFSSM_SCAF_KB(1) DFSSM_SCAF_KB(2) DFSSM_SCAF_KB(3) DFSSM_SCAF_KB(4) DFSSM_SCAF_KB(5)
+    DFSSM_SCAF_KB(6) DFSSM_SCAF_KB(7) DFSSM_SCAF_KB(8) DFSSM_SCAF_KB(9) DFSSM_SCAF_KB(10)
+#undef DFSSM_SCAF_KB
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_scaffold(const ScaffoldArgs& a, int M, hipStream_t s) {
   const int groups = (a.N + 63) / 64;
   if (a.K > kMaxK || a.K % 512 || M < 1 || M > 4) return hipErrorInvalidValue;
   if (a.xn) {  // LoRA with the intermediates computed in the same launch (M = 1)
     if (M != 1 || !a.lBq || !a.h_out || !a.lA || !a.lAs || !a.y_out) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((scaffold_fused_kernel<1, true>), dim3(groups), dim3(kNT), 0, s, a);
-    return hipGetLastError();
+    return launch_scaffold_k<1, true>(a, groups, s);
   }
   if (a.lA) return hipErrorInvalidValue;  // LoRA without xn: the GEMM path
   switch (M) {
-    case 1: hipLaunchKernelGGL((scaffold_fused_kernel<1, false>), dim3(groups), dim3(kNT), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((scaffold_fused_kernel<2, false>), dim3(groups), dim3(kNT), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((scaffold_fused_kernel<3, false>), dim3(groups), dim3(kNT), 0, s, a); break;
-    default: hipLaunchKernelGGL((scaffold_fused_kernel<4, false>), dim3(groups), dim3(kNT), 0, s, a); break;
+    case 1: return launch_scaffold_k<1, false>(a, groups, s);
+    case 2: return launch_scaffold_k<2, false>(a, groups, s);
+    case 3: return launch_scaffold_k<3, false>(a, groups, s);
+    default: return launch_scaffold_k<4, false>(a, groups, s);
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_tile_bits(const uint32_t* src, uint32_t* dst, int N, int KW, hipStream_t s) {

@@ -61,7 +61,7 @@ _SIGS = {
     "dfssm_tile_embedding": (c_int, [P, P, c_int, c_int, P]),
     "dfssm_dequant_lora_b": (c_int, [P, P, c_int, P, P]),
     "dfssm_scaffold_gemm": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
-    "dfssm_scaffold_lora_gemm": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, P]),
+    "dfssm_scaffold_lora_gemm": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, P, P]),
     "dfssm_rmsnorm_quantize": (c_int, [P, P, c_int, c_int, P, P, P, P]),
     "dfssm_conv_step": (c_int, [P, P, c_int, P, P, c_int, c_int, P]),
     "dfssm_ssm_step": (c_int, [P, P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),

@@ -40,11 +40,34 @@ def scaffold_gemm(tiled_bits: torch.Tensor, q: torch.Tensor, N: int, xscale=None
     return (acc, y) if want_y else acc
 
 
+SCAFFOLD_WORKSPACE_BYTES = 64 << 10   # DFSSM_SCAFFOLD_WORKSPACE_BYTES
+SCAFFOLD_ERROR_OFFSET = 1024          # DFSSM_SCAFFOLD_ERROR_OFFSET
+_scaffold_ws = {}
+
+
+def scaffold_workspace(device) -> torch.Tensor:
+    """The exchange workspace of dfssm_scaffold_lora_gemm for `device` (zeroed at allocation, one
+    per device; calls on one device are ordered by torch's current stream)."""
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    if key not in _scaffold_ws:
+        _scaffold_ws[key] = torch.zeros(SCAFFOLD_WORKSPACE_BYTES // 4, dtype=torch.int32, device=dev)
+    return _scaffold_ws[key]
+
+
+def scaffold_error(workspace: torch.Tensor) -> int:
+    """The workspace's error word (synchronizes): non-zero after a call whose wait timed out."""
+    return int(workspace[SCAFFOLD_ERROR_OFFSET // 4].item())
+
+
 def scaffold_lora_gemm(tiled_bits: torch.Tensor, wscale: torch.Tensor, q: torch.Tensor, xscale: torch.Tensor,
-                       xn: torch.Tensor, lA: torch.Tensor, lA_s: torch.Tensor, lBq: torch.Tensor, N: int):
+                       xn: torch.Tensor, lA: torch.Tensor, lA_s: torch.Tensor, lBq: torch.Tensor, N: int,
+                       workspace="auto"):
     """One projection with its LoRA (dfssm_scaffold_lora_gemm): returns (acc int32 (M, N),
     y fp16 (M, N), lora_h fp16 (M, 16)). q (M, K) int8 with fp16 scales xscale (M,), xn (M, K) fp16,
-    lA (N, 16) int8, lA_s (N,) fp16, lBq (16, K) fp16, wscale (N,) fp16."""
+    lA (N, 16) int8, lA_s (N,) fp16, lBq (16, K) fp16, wscale (N,) fp16. workspace: "auto" (the
+    device's exchange workspace: one launch at M <= 4), None (no workspace) or an int32 tensor of
+    SCAFFOLD_WORKSPACE_BYTES, zeroed before its first use."""
     _need(q, torch.int8, "q")
     _need(xn, torch.float16, "xn")
     _need(lBq, torch.float16, "lBq")
@@ -55,11 +78,19 @@ def scaffold_lora_gemm(tiled_bits: torch.Tensor, wscale: torch.Tensor, q: torch.
     acc = torch.empty(M, N, dtype=torch.int32, device=q.device)
     y = torch.empty(M, N, dtype=torch.float16, device=q.device)
     h = torch.empty(M, 16, dtype=torch.float16, device=q.device)
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError('workspace must be "auto", None or a tensor')
+        workspace = scaffold_workspace(q.device)
+    elif workspace is not None:
+        _need(workspace, torch.int32, "workspace")
+        if workspace.numel() * 4 < SCAFFOLD_WORKSPACE_BYTES:
+            raise ValueError(f"workspace must hold {SCAFFOLD_WORKSPACE_BYTES} bytes")
     _C.check(_C.lib().dfssm_scaffold_lora_gemm(
         tiled_bits.data_ptr(), wscale.contiguous().data_ptr(), q.contiguous().data_ptr(),
         xscale.contiguous().data_ptr(), xn.contiguous().data_ptr(), lA.contiguous().data_ptr(),
         lA_s.contiguous().data_ptr(), lBq.contiguous().data_ptr(), M, N, K, h.data_ptr(), acc.data_ptr(),
-        y.data_ptr(), _C.stream()), "scaffold_lora_gemm")
+        y.data_ptr(), _C.ptr(workspace), _C.stream()), "scaffold_lora_gemm")
     return acc, y, h
 
 

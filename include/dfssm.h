@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DFSSM_ABI_VERSION 6
+#define DFSSM_ABI_VERSION 7
 
 #define DFSSM_OK 0
 #define DFSSM_E_NULL (-1)        /* a required pointer is NULL */
@@ -146,11 +146,20 @@ int dfssm_scaffold_gemm(const uint32_t* tiled_bits, const int8_t* q, const uint1
  * fp16 are the normalized activations the LoRA reads (q their int8 quantization with scales
  * xscale); lBq (16, K) is the load-time fp16 LoRA-B table (dfssm_dequant_lora_b); lA (N, 16) int8
  * and lA_s (N) fp16 as stored in the file. lora_h (M, 16) fp16 receives the intermediates.
- * M = 1..64 (1..4 on the packed-bit VALU GEMV, 5..64 on the int8 matrix cores). */
+ * M = 1..64 (1..4 on the packed-bit VALU GEMV, 5..64 on the int8 matrix cores).
+ * workspace (no counterpart in the reference; NULL allowed): DFSSM_SCAFFOLD_WORKSPACE_BYTES of
+ * device memory, 16-byte aligned and zeroed once before its first use. With it, M <= 4, M K <=
+ * 8192 and N <= 15 360 run as one launch in which 16 workgroups compute the intermediates once and
+ * hand them to the GEMV workgroups through the workspace (the same results as without it). Calls that share a
+ * workspace must not overlap. The word at byte offset DFSSM_SCAFFOLD_ERROR_OFFSET is non-zero
+ * after a call whose wait for the intermediates timed out (its y is then wrong); it stays set
+ * until the caller clears it. */
+#define DFSSM_SCAFFOLD_WORKSPACE_BYTES (64u << 10)
+#define DFSSM_SCAFFOLD_ERROR_OFFSET 1024u
 int dfssm_scaffold_lora_gemm(const uint32_t* tiled_bits, const uint16_t* wscale, const int8_t* q,
                              const uint16_t* xscale, const uint16_t* xn, const int8_t* lA, const uint16_t* lA_s,
                              const uint16_t* lBq, int M, int N, int K, uint16_t* lora_h, int32_t* acc_out,
-                             uint16_t* y_out, void* stream);
+                             uint16_t* y_out, void* workspace, void* stream);
 
 /* RMSNorm + int8 quantization of M rows (the prologue of every projection):
  * xn = fp16((x * r) * w), q = int8 activations, s = fp16 scales.

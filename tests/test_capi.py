@@ -27,7 +27,7 @@ def test_header_symbols_exported():
 
 def test_version_and_errors():
     L = _C.lib()
-    assert L.dfssm_version() == 6
+    assert L.dfssm_version() == 7
     assert L.dfssm_error_string(-2).decode().startswith("model dimensions")
 
 

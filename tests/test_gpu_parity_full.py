@@ -2,8 +2,10 @@
 reference calls them.
 
 * config 1: the scaffold projection with its rank-16 int8 LoRA as one operator
-  (dfssm_scaffold_lora_gemm) at in_proj / out_proj shapes, M in {1, 4, 16, 32}: int32
-  accumulators, LoRA intermediates and y bit-exact against the oracle;
+  (dfssm_scaffold_lora_gemm) at in_proj / out_proj shapes (and the 2.7B and edge shapes),
+  M in {1, 2, 3, 4, 16, 32}, with and without the exchange workspace: int32 accumulators, LoRA
+  intermediates and y bit-exact against the oracle; one workspace shared by consecutive calls of
+  different shapes;
 * config 3 at batch 32: the 1.3B model (48 layers, vocab 50288) greedy, identical tokens and
   logits at every step (the batched exact head at 32 rows);
 * config 4's dimensions at batch 64 with the full 50288-token vocabulary (2 layers so that the
@@ -37,14 +39,9 @@ def _np16(t):
 
 
 # ------------------------------------------------------------------------------ config 1
-@pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096)])
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 32])
-def test_scaffold_lora_op_bit_exact(N, K, M):
-    """BASELINE config 1: packed bits with fp16 row scales ~U(0.01, 0.05), int8 activations
-    ~N(0, 40) clipped with fp16 per-token scales, rank-16 int8 LoRA A/B; xn is the fp16 vector
-    the activations quantize (the LoRA reads it, df_ssm_inference.py:173)."""
-    print(f"scaffold+lora N={N} K={K} M={M}", flush=True)
-    rng = np.random.default_rng([1, N, K, M])
+def _lora_op_case(N, K, M, seed):
+    """Inputs of one scaffold + LoRA call (BASELINE config 1 distributions) and its oracle outputs."""
+    rng = np.random.default_rng([1, N, K, M, seed])
     bits = rng.integers(0, 2**32, (N, K // 32), dtype=np.uint64).astype(np.uint32)
     ws = rng.uniform(0.01, 0.05, N).astype(np.float16)
     xn = rng.normal(0, 1, (M, K)).astype(np.float16)
@@ -53,21 +50,60 @@ def test_scaffold_lora_op_bit_exact(N, K, M):
     lAs = (1.7e-3 * rng.uniform(0.5, 1.5, N)).astype(np.float16)
     lB = np.clip(np.rint(rng.normal(0, 20, (16, K))), -127, 127).astype(np.int8)
     lBs = (rng.uniform(0.5, 1.5, 16) / (20 * np.sqrt(K))).astype(np.float16)
-
     tb = ops.tile_bits(torch.from_numpy(bits.view(np.int32)).to(DEV), N, K)
     lBq = torch.empty(16, K, dtype=torch.float16, device=DEV)
     tB, tBs = torch.from_numpy(lB).to(DEV), _h(lBs)  # kept alive until the kernel has run
     _C.check(_C.lib().dfssm_dequant_lora_b(tB.data_ptr(), tBs.data_ptr(), K, lBq.data_ptr(), _C.stream()))
     torch.cuda.synchronize()
-    acc, y, h = ops.scaffold_lora_gemm(tb, _h(ws), torch.from_numpy(q).to(DEV), _h(xs), _h(xn),
-                                       torch.from_numpy(lA).to(DEV), _h(lAs), lBq, N)
+    args = (tb, _h(ws), torch.from_numpy(q).to(DEV), _h(xs), _h(xn), torch.from_numpy(lA).to(DEV), _h(lAs), lBq, N)
     acc_r = O.scaffold_acc(bits, q)
     h_r = O.lora_h(xn, lB, lBs)
     y_r = O.dequant_lora(acc_r, xs, ws, h_r, lA, lAs)
+    assert np.abs(y_r.astype(np.float32)).max() > 0
+    return args, (acc_r, h_r, y_r)
+
+
+def _check_lora_op(out, ref):
+    acc, y, h = out
+    acc_r, h_r, y_r = ref
     np.testing.assert_array_equal(acc.cpu().numpy(), acc_r)
     np.testing.assert_array_equal(_np16(h).view(np.uint16), h_r.view(np.uint16))
     np.testing.assert_array_equal(_np16(y).view(np.uint16), y_r.view(np.uint16))
-    assert np.abs(y_r.astype(np.float32)).max() > 0
+
+
+@pytest.mark.parametrize("N,K", [(8512, 2048), (2048, 4096), (10576, 2560), (2560, 5120), (64, 512)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 32])
+@pytest.mark.parametrize("xchg", [True, False])
+def test_scaffold_lora_op_bit_exact(N, K, M, xchg):
+    """BASELINE config 1: packed bits with fp16 row scales ~U(0.01, 0.05), int8 activations
+    ~N(0, 40) clipped with fp16 per-token scales, rank-16 int8 LoRA A/B; xn is the fp16 vector
+    the activations quantize (the LoRA reads it, df_ssm_inference.py:173). xchg: with the exchange
+    workspace (one launch at M <= 4), else without."""
+    print(f"scaffold+lora N={N} K={K} M={M} xchg={xchg}", flush=True)
+    args, ref = _lora_op_case(N, K, M, 0)
+    wsx = torch.zeros(ops.SCAFFOLD_WORKSPACE_BYTES // 4, dtype=torch.int32, device=DEV) if xchg else None
+    _check_lora_op(ops.scaffold_lora_gemm(*args, workspace=wsx), ref)
+    if xchg:
+        assert ops.scaffold_error(wsx) == 0
+
+
+def test_scaffold_lora_op_shared_workspace():
+    """One exchange workspace across consecutive calls whose grids cover different numbers of output
+    rows, batches and K (every call must find the words of its own call, not of an earlier one), the
+    same call twice in a row, and calls in between that take the matrix-core path (M K > 8192) and
+    leave the workspace alone."""
+    wsx = torch.zeros(ops.SCAFFOLD_WORKSPACE_BYTES // 4, dtype=torch.int32, device=DEV)
+    cases = [(8512, 2048, 1), (2048, 4096, 1), (64, 512, 4), (10576, 2560, 2), (8512, 2048, 1),
+             (2048, 4096, 3), (2048, 4096, 3)]
+    for i, (N, K, M) in enumerate(cases):
+        print(f"shared workspace call {i}: N={N} K={K} M={M}", flush=True)
+        args, ref = _lora_op_case(N, K, M, i)
+        _check_lora_op(ops.scaffold_lora_gemm(*args, workspace=wsx), ref)
+    assert ops.scaffold_error(wsx) == 0
+    counts = wsx[:256].cpu().numpy()
+    one_launch = sum(M <= 4 and M * K <= 8192 for N, K, M in cases)
+    assert one_launch == 5
+    assert (counts == one_launch).all()  # every workgroup index counted every one-launch call
 
 
 # ------------------------------------------------------------------------------ config 3, B = 32
