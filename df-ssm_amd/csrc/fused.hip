@@ -724,6 +724,15 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   // included). Tag of layer l at epoch e: e L + l + 1 (mod 2^16); every launch of a workgroup
   // index advances its epoch, so a word left by the previous launch never carries the tag a poll
   // waits for.
+  // every argument into registers at once: the compiler otherwise loads the launch-count pointer
+  // first and waits for it before loading the rest of the argument block (one more scalar-memory
+  // round trip before the first data load)
+  asm volatile("" ::"s"(a.in_bits), "s"(a.in_ws), "s"(a.in_lA), "s"(a.in_lAs), "s"(a.in_lBq), "s"(a.out_bits),
+               "s"(a.out_ws), "s"(a.out_lA), "s"(a.out_lAs), "s"(a.out_lBq), "s"(a.conv_w), "s"(a.conv_b));
+  asm volatile("" ::"s"(a.A_log), "s"(a.Dp), "s"(a.dt_bias), "s"(a.norm_w), "s"(a.ln_w), "s"(a.h), "s"(a.conv),
+               "s"(a.x), "s"(a.projT), "s"(a.gT), "s"(a.hT), "s"(a.bcT), "s"(a.dtT), "s"(a.launches), "s"(a.err));
+  asm volatile("" ::"s"(a.layer), "s"(a.n_layer), "s"(a.D), "s"(a.DI), "s"(a.N), "s"(a.H), "s"(a.P), "s"(a.IPO),
+               "s"(a.C));
   const uint32_t epoch_raw = ld_dev(a.launches + bix());
   const int G = gridDim.x, wg = bix();
   auto tag_now = [&]() {
