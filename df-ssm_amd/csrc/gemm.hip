@@ -176,7 +176,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   extern __shared__ __attribute__((aligned(16))) int8_t qs[];  // MP rows x QS bytes; then partials
   __shared__ float hl[MP][DFSSM_LORA_R];
   __shared__ float xsl[MP];
-  __shared__ uint32_t zero_s;  // read back as 0 in every row block (see below)
   __shared__ uint32_t tag_s;  // PRO: this launch's tag
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // PRO: launch count of this workgroup (read at the start, advanced once its tag is known)
@@ -290,7 +289,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   const bool lora = MODE != DFSSM_MODE_SCAFFOLD || a.lA;
   // partial LoRA terms [slot][rt][ib][e][lane] (fp64), after the int32 partials in the dynamic LDS
   double* lod = (double*)(qs + gemm_part_bytes(MI, RT));
-  if (tid == 0) zero_s = 0u;
   if (PRO && tid == 0) {  // read by every thread after the loop's barriers
     tag_s = (epoch + 1u) & 0xffffu;
     st_dev(cnt, epoch + 1u);
@@ -373,12 +371,38 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
       if (tid < MP * DFSSM_LORA_R) hl[tid >> 4][tid & 15] = tid < MB * DFSSM_LORA_R ? hv : 0.0f;
       if (tid < MP) xsl[tid] = tid < MB ? xsv : 0.0f;
     }
+    // the epilogue's old values -- conv state (in_proj) or residual row (out_proj) of this lane's
+    // accumulator elements -- issued now and used after the MFMA loop and the LoRA term:
+    // unconditional loads from clamped in-bounds indices (a load in a branch makes the compiler
+    // wait for it where the paths join, before the MFMA loop)
+    uint16_t pold[kEI][3];
+    if constexpr (MODE == DFSSM_MODE_IN || MODE == DFSSM_MODE_OUT) {
+#pragma unroll
+      for (int ii = 0; ii < kEI; ++ii) {
+        const int i0 = kq + KQ * ii;
+        const int i = i0 < 4 * MI ? i0 : 4 * MI - 1;
+        const int mb0 = (i >> 2) * 16 + 4 * j + (i & 3);
+        const int mm = m0 + (mb0 < MB ? mb0 : MB - 1);
+        if (MODE == DFSSM_MODE_IN) {
+          const int chc = ch < 0 ? 0 : (ch < a.conv_c ? ch : a.conv_c - 1);
+          const uint16_t* cs = a.conv_state ? a.conv_state + ((size_t)mm * a.conv_c + chc) * 3 : a.out;
+          pold[ii][0] = cs[0];
+          pold[ii][1] = cs[1];
+          pold[ii][2] = cs[2];
+        } else {
+          pold[ii][0] = a.out[(size_t)mm * a.ld_out + (nrow ? n : a.N - 1)];
+        }
+      }
+    }
     lds_barrier();
 
     // ---- MFMA over this wave's chunks ----
-    // The byte expansion of the bits does not change between row blocks; a volatile zero from
-    // LDS keeps the compiler from hoisting all 24 expanded operands (96 registers) out of the loop.
-    const uint32_t zero = *(volatile uint32_t*)&zero_s;
+    // The byte expansion of the bits does not change between row blocks; a zero the compiler
+    // cannot see through keeps it from hoisting all 24 expanded operands (96 registers) out of
+    // the loop. (A volatile LDS word read through a generic pointer is a FLAT load, whose wait
+    // is vmcnt(0): it held the MFMA loop until every earlier load, the epilogue's, had landed.)
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
     v4i acc[MI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[i] = v4i{0, 0, 0, 0};
@@ -437,6 +461,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
       }
     }
     lds_barrier();
+    // the old values are waited for here, on every path: consumed only inside the lanes'
+    // branches below, they would stay pending (as far as the compiler can tell) into the next
+    // row block, whose q-tile loads would then wait for them
+    if constexpr (MODE == DFSSM_MODE_IN) {
+#pragma unroll
+      for (int ii = 0; ii < kEI; ++ii) asm volatile("" ::"v"(pold[ii][0]), "v"(pold[ii][1]), "v"(pold[ii][2]));
+    } else if constexpr (MODE == DFSSM_MODE_OUT) {
+#pragma unroll
+      for (int ii = 0; ii < kEI; ++ii) asm volatile("" ::"v"(pold[ii][0]));
+    }
 
     // ---- epilogue: wave (rt, kq) finishes accumulator elements i = kq, kq + KQ, ... < 4 MI ----
     if (nrow && kq < 4 * MI) {
@@ -470,7 +504,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
         if (MODE == DFSSM_MODE_IN) {
           if (conv_row) {
             uint16_t* cs = a.conv_state + ((size_t)m * a.conv_c + ch) * 3;
-            const uint16_t s0 = cs[0], s1 = cs[1], s2 = cs[2];
+            const uint16_t s0 = pold[ii][0], s1 = pold[ii][1], s2 = pold[ii][2];
             const uint16_t xo = f2h(out);
             cs[0] = s1;
             cs[1] = s2;
@@ -487,7 +521,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
           }
           *op = f2h(out);
         } else {
-          const uint16_t xv = f2h(h2f(*op) + out);
+          const uint16_t xv = f2h(h2f(pold[ii][0]) + out);
           *op = xv;
           if (PRO) st_dev(p.xT + (size_t)m * a.N + n, (tag_s << 16) | xv);
         }
