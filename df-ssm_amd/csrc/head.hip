@@ -14,6 +14,8 @@
 #include "common.h"
 #include "dfssm_kernels.h"
 
+#include <type_traits>
+
 namespace dfssm {
 
 // Vocabulary limit of the heads: at most 1024 table groups of 64 rows (V <= 65536), so that the
@@ -32,6 +34,40 @@ template <bool F16>
 __device__ __forceinline__ uint16_t emb_value(const uint8_t* emb, const uint16_t* scale, int CH, int tg, int tl, int k) {
   if (F16) return ((const uint16_t*)(emb + (((size_t)tg * CH + (k >> 3)) * 64 + tl) * 16))[k & 7];
   return f2h((float)(int8_t)emb[(((size_t)tg * CH + (k >> 4)) * 64 + tl) * 16 + (k & 15)] * h2f(scale[tg * 64 + tl]));
+}
+
+// (value, index) pair reductions of the argmax: the larger value wins, on equal values the
+// smaller index. Candidates enter through `>` comparisons against -inf, so no NaN is ever a best:
+// a total order, and the result does not depend on the order of the reduction. DPP steps move the
+// pairs between lanes in the VALU (an LDS shuffle costs a round trip per step).
+__device__ __forceinline__ void argmax_take(float& b, int& bi, float ob, int oi) {
+  if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& b, int& bi) {
+  argmax_take(b, bi, dpp_f32<CTRL>(b), dpp_i32<CTRL>(bi));
+}
+// over the 16 lanes of every DPP row: each lane ends with its row's pair
+__device__ __forceinline__ void row_argmax_dpp(float& b, int& bi) {
+  argmax_dpp_step<0xB1>(b, bi);   // quad_perm 1,0,3,2
+  argmax_dpp_step<0x4E>(b, bi);   // quad_perm 2,3,0,1
+  argmax_dpp_step<0x124>(b, bi);  // row_ror 4
+  argmax_dpp_step<0x128>(b, bi);  // row_ror 8
+}
+// over the wave: each lane ends with the wave's pair
+__device__ __forceinline__ void wave_argmax_dpp(float& b, int& bi) {
+  row_argmax_dpp(b, bi);
+  float rb[4];
+  int ri[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    rb[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 16 * r));
+    ri[r] = __builtin_amdgcn_readlane(bi, 16 * r);
+  }
+  b = rb[0];
+  bi = ri[0];
+#pragma unroll
+  for (int r = 1; r < 4; ++r) argmax_take(b, bi, rb[r], ri[r]);
 }
 
 // The last workgroup's argmax over the NG per-workgroup (max, first index) pairs of every row
@@ -64,12 +100,7 @@ __device__ __forceinline__ void argmax_pairs(const HeadArgs& a, int M, int NG, i
         b = pv[r][q];
         bi = pi[r][q];
       }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(b, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
-    }
+    wave_argmax_dpp(b, bi);
     if (lane == 0 && m < M) {
       // no comparable logit (all NaN): report token 0 rather than an index outside the table
       if (bi < 0 || bi >= a.V) bi = 0;
@@ -81,9 +112,8 @@ __device__ __forceinline__ void argmax_pairs(const HeadArgs& a, int M, int NG, i
 
 // x_next[m] = the embedding of token toks[m], m < M, by NT threads in 16-byte table chunks (16
 // int8 or 8 fp16 values), KB chunks per thread loaded before any is converted and stored.
-template <bool F16, int NT>
+template <bool F16, int NT, int KB = 8>
 __device__ __forceinline__ void embed_next(const HeadArgs& a, const int* toks, int M, int D) {
-  constexpr int KB = 8;
   const int CH = F16 ? D / 8 : D / 16, n = M * CH;
   for (int c0 = (int)threadIdx.x; c0 < n; c0 += NT * KB) {
     u32x4 ch[KB];
@@ -188,12 +218,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
       best = h2f(lh);
       bidx = v;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(bidx, o, 64);
-      if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
-    }
+    wave_argmax_dpp(best, bidx);
     if (lane == 0) {
       a.part_val[(size_t)m * gridDim.x + g] = best;
       a.part_idx[(size_t)m * gridDim.x + g] = bidx;
@@ -391,12 +416,7 @@ __global__ __launch_bounds__(256) void head_i8_kernel(HeadArgs a) {
     best = h2f(lh);
     bidx = v;
   }
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) {  // within the 16 lanes of the row group
-    const float ob = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(bidx, o, 64);
-    if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
-  }
+  row_argmax_dpp(best, bidx);  // the 16 lanes of the row group
   if (rl == 0 && jg < M) {
     pv[wave][jg] = best;
     pix[wave][jg] = bidx;
@@ -495,20 +515,13 @@ hipError_t launch_tile_emb(const uint8_t* src, uint8_t* dst, int V, int D, hipSt
 // a tiled GEMM. head_digits_kernel computes the final RMSNorm of every row once and writes the
 // six base-256 digit planes of X = xf 2^24, tiled for the A operand: tile t = b NH + h holds
 // digit b of rows 16 h .. 16 h + 15, laid out [tile][16-byte k chunk][16 rows][16 bytes]
-// (NH = ceil(M / 16); rows M .. 16 NH - 1 and the chunks past D are zero).
-// head_i8b_kernel<NH, KP>: a workgroup of 2 NH KP waves owns two table groups (128 vocabulary
-// rows). Wave w takes k part w / (2 NH) (the k steps are split in KP parts so that more waves
-// keep loads in flight; part 0 adds the others' exact partials from LDS), row block h and table
-// group from w % (2 NH) = 2 h + group. Per 64-wide k step a lane loads its 16 bytes of the 6
-// digit tiles of h (A: row l % 16, k block l / 16) and of the group's 4 fragments of 16 rows (B:
-// row 16 f + l % 16, same k block); the loads of the next two steps are in flight during a
-// step's 24 MFMAs. The accumulator layout D[4 (l / 16) + e][l % 16] leaves lane l with all six
-// digit sums S_b of (m = 16 h + 4 (l / 16) + e, v = 64 g + 16 f + l % 16) in its own registers:
-// T = sum_b S_b 256^b (int64) = sum_k X_k E[v][k] exactly, the logit fp16(fp32(T 2^-24) *
-// s_E[v]) as in the 1..4-row kernel. The table streams from HBM once; the digit planes
-// (6 * 16 NH * D bytes) stay in L2. Argmax: per-workgroup (max, first index) pairs written
-// through to the coherent level, the last workgroup (arrival ticket) reduces them and writes the
-// next tokens and their embedding.
+// (NH = ceil(M / 16); rows M .. 16 NH - 1 and the chunks past D are zero). head_i8s_kernel (below)
+// multiplies them with the table on the int8 matrix cores: the accumulator layout
+// D[4 (l / 16) + e][l % 16] of v_mfma_i32_16x16x64_i8 leaves lane l with all six digit sums S_b of
+// (m = 16 h + 4 (l / 16) + e, v = 16 fragment + l % 16) in its own registers, T = sum_b S_b 256^b
+// (int64) = sum_k X_k E[v][k] exactly, and the logit is fp16(fp32(T 2^-24) * s_E[v]) as in the
+// 1..4-row kernel. The table streams from HBM once; the digit planes (6 * 16 NH * D bytes) from L2
+// into each workgroup's LDS.
 // ---------------------------------------------------------------------------------------------
 // 16-byte k chunks per digit-plane row: D / 16 rounded up to whole groups of four 64-wide k steps
 // (the rings run four steps per iteration without a tail; the padding is zero)
@@ -523,6 +536,12 @@ __global__ __launch_bounds__(256) void head_digits_kernel(const uint16_t* __rest
   const int CH = D / 16, h = m >> 4, rr = m & 15;
   const int CHp = digit_chunks(D);  // the planes are zero past column D
   const uint16_t* xm = x + (size_t)(m < M ? m : 0) * D;
+  // the first digit chunk of this thread (x and norm_f), loaded with the sum-of-squares pass so
+  // that the digits need no second memory round trip (clamped in-bounds; chunks past D are zero)
+  const int c0 = tid < CH ? tid : CH - 1;
+  const u32x4 x00 = *(const u32x4*)(xm + 16 * c0), x01 = *(const u32x4*)(xm + 16 * c0 + 8);
+  const f32x4* nfp0 = (const f32x4*)(norm_f + 16 * c0);
+  const f32x4 n00 = nfp0[0], n01 = nfp0[1], n02 = nfp0[2], n03 = nfp0[3];
   float r = 0.0f;
   if (m < M) {  // uniform over the workgroup
     double ps = 0.0;
@@ -544,9 +563,14 @@ __global__ __launch_bounds__(256) void head_digits_kernel(const uint16_t* __rest
 #pragma unroll
       for (int j = 0; j < 4; ++j) pk[b][j] = 0u;
     if (m < M && c < CH) {
-      const u32x4 x0 = *(const u32x4*)(xm + 16 * c), x1 = *(const u32x4*)(xm + 16 * c + 8);
-      const f32x4* nfp = (const f32x4*)(norm_f + 16 * c);
-      const f32x4 n4[4] = {nfp[0], nfp[1], nfp[2], nfp[3]};
+      u32x4 x0 = x00, x1 = x01;
+      f32x4 n4[4] = {n00, n01, n02, n03};
+      if (c != tid) {  // the second and later chunks of a thread (D > 4096)
+        x0 = *(const u32x4*)(xm + 16 * c);
+        x1 = *(const u32x4*)(xm + 16 * c + 8);
+        const f32x4* nfp = (const f32x4*)(norm_f + 16 * c);
+        n4[0] = nfp[0]; n4[1] = nfp[1]; n4[2] = nfp[2]; n4[3] = nfp[3];
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const uint32_t w = i < 8 ? x0[i >> 1] : x1[(i - 8) >> 1];
@@ -567,166 +591,202 @@ __global__ __launch_bounds__(256) void head_digits_kernel(const uint16_t* __rest
   }
 }
 
-// (at most 256 registers per lane: with more, the accumulators move through AGPR copies)
-// KP: k parts (waves) per (row block, table group); 128 NH KP <= 512 threads keeps 2 waves per SIMD
-template <int NH, int KP>
-__global__ __launch_bounds__(128 * NH * KP) __attribute__((amdgpu_waves_per_eu(2))) void head_i8b_kernel(HeadArgs a, int M) {
-  constexpr int MP = 16 * NH, NWP = 2 * NH;  // waves per k part
-  __shared__ long long tpart[KP > 1 ? KP - 1 : 1][NWP][16][64];
-  __shared__ float wbest[2][MP];
-  __shared__ int widx[2][MP];
+// ---------------------------------------------------------------------------------------------
+// head_i8s_kernel<NH>: the digit-plane GEMM of the batched exact head with the digit tiles staged
+// in LDS. A workgroup of 8 waves owns a run of fragments (16 vocabulary rows each). The 16 NH
+// activation rows are split into NRG row groups of NHW = NH / NRG row blocks (NRG = 2 at 64 rows,
+// else 1); wave w computes row group w / (8 / NRG) against F fragments, so that each wave reads
+// 6 NHW digit tiles per 64-wide k step from LDS for 6 NHW F MFMAs (at 64 rows in one group the
+// 24-tile reads bound the loop). The digit tiles of CK k steps (all row blocks, 6 NH CK KiB) are
+// copied into LDS by the whole workgroup one chunk ahead (double buffer, one barrier per chunk),
+// so the waves read them through the LDS queue (lgkmcnt) instead of re-reading L2 through the
+// vector-memory queue, where loads complete in issue order and a digit-tile wait was also a wait
+// for the table loads issued before it. The table fragments (HBM) stream through a register ring
+// kHsDB steps deep; between table loads the queue holds one batch of staging loads per chunk,
+// issued a chunk before its use. Logits, argmax and the next embedding as in the other heads.
+// ---------------------------------------------------------------------------------------------
+constexpr int kHsWaves = 8, kHsThreads = 64 * kHsWaves, kHsDB = 4;  // steps per loop turn = kHsDB
+
+__host__ __device__ constexpr int hs_nrg(int NH) { return NH == 4 ? 2 : 1; }                   // row groups
+__host__ __device__ constexpr int hs_frags(int NH) { return NH / hs_nrg(NH) <= 2 ? 2 : 1; }    // fragments per wave
+__host__ __device__ constexpr int hs_ck(int NH) { return NH <= 2 ? 4 : 2; }                    // k steps per chunk
+__host__ __device__ constexpr int hs_wg_frags(int NH) { return kHsWaves / hs_nrg(NH) * hs_frags(NH); }
+__host__ __device__ constexpr size_t hs_lds_bytes(int NH) { return (size_t)2 * 6 * NH * hs_ck(NH) * 1024; }
+
+template <int NH>
+__global__ __launch_bounds__(kHsThreads) __attribute__((amdgpu_waves_per_eu(2))) void head_i8s_kernel(HeadArgs a, int M) {
+  constexpr int NRG = hs_nrg(NH), NHW = NH / NRG, WPG = kHsWaves / NRG;
+  constexpr int F = hs_frags(NH), CK = hs_ck(NH);
+  constexpr int NT = 6 * NH;                      // staged digit tiles per k step: tile t = b NH + h
+  constexpr int NTW = 6 * NHW;                    // tiles of a wave's row group
+  constexpr int AG = NTW <= 12 ? NTW : NTW / 2;   // tiles read from LDS at a time
+  constexpr int CHUNK = NT * CK * 64;             // 16-byte vectors per staged chunk
+  constexpr int SV = (CHUNK + kHsThreads - 1) / kHsThreads;
+  constexpr int MP = 16 * NH;
+  extern __shared__ __attribute__((aligned(16))) u32x4 abuf[];  // [2][NT][CK][64]
+  __shared__ float wbest[kHsWaves][16 * NHW];
+  __shared__ int widx[kHsWaves][16 * NHW];
   __shared__ bool is_last;
   __shared__ int next_tok[MP];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: operand bases in SGPRs
-  const int kp = wave / NWP, wl = wave % NWP;
-  const int h = wl >> 1, vh = wl & 1, jg = lane >> 4, rl = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave / WPG, wf = wave % WPG;     // row group, fragment slot
+  const int jg = lane >> 4, rl = lane & 15;
   const int D = a.D, CH = D / 16, KS = D / 64;
-  const int ngrp = (a.V + 63) / 64;
-  const int g = 2 * (int)blockIdx.x + vh;
-  const bool gok = g < ngrp;           // wave-uniform; a wave past the table computes on group
-  const int gc = gok ? g : ngrp - 1;   // ngrp - 1 (in bounds) and discards the result
-  // row scales of this lane's 4 vocabulary rows: loaded first, used at the end
-  uint16_t sc[4];
+  const int nfr = (a.V + 15) / 16;                // fragments of 16 rows (the table has 64-row groups)
+  const int CHp = digit_chunks(D);
+  const int fb0 = (int)blockIdx.x * WPG * F + wf * F;  // this wave's first fragment
+  // the wave's fragments (clamped into the table: past it a wave recomputes the last one and
+  // discards the result) and their row scales (loaded first, used at the end)
+  int fr[F];
+  uint16_t sc[F];
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    const int v = gc * 64 + 16 * f + rl;
+  for (int f = 0; f < F; ++f) {
+    fr[f] = fb0 + f < nfr ? fb0 + f : nfr - 1;
+    const int v = 16 * fr[f] + rl;
     sc[f] = a.emb_scale[v < a.V ? v : a.V - 1];
   }
-  // operand addresses: a workgroup-uniform base plus a 32-bit lane offset (scalar-base loads)
-  const char* Eb = (const char*)a.emb + (size_t)gc * CH * 1024;   // table group gc
-  const int CHp = digit_chunks(D), KSp = CHp / 4;                 // k steps incl. zero padding
-  const char* Ab = (const char*)a.hdig + (size_t)h * CHp * 256;   // row block h of digit plane 0
-  const uint32_t eo = (uint32_t)(jg * 64 + rl) * 16;              // + 1024 (4 s) + 256 f
-  const uint32_t ao = (uint32_t)(jg * 16 + rl) * 16;              // + b * plane + 256 (4 s)
-  const uint32_t plane = (uint32_t)NH * CHp * 256;                // one digit plane, bytes
-  i32x4 acc[6][4];
-#pragma unroll
-  for (int b = 0; b < 6; ++b)
-#pragma unroll
-    for (int f = 0; f < 4; ++f) acc[b][f] = i32x4{0, 0, 0, 0};
-  // rings: the table fragments (HBM) are loaded three steps ahead, the digit tiles (L2) one step
-  // ahead, a step's digit tiles issued before its table fragments: loads complete in issue order,
-  // so waiting for step s's digit tiles leaves the table loads of steps s + 2 and s + 3 in flight
-  u32x4 A[2][6], Bf[4][4];
-  auto loadA = [&](int st, int step) {
-    // steps KS .. KSp - 1 multiply zero digits with a re-read of the last table step; loads past
-    // KSp (the rings' overrun) re-read step KSp - 1 and are not used
-    const uint32_t oa = (uint32_t)(4 * (step < KSp ? step : KSp - 1));
-#pragma unroll
-    for (int b = 0; b < 6; ++b) A[st][b] = *(const u32x4*)(Ab + (ao + b * plane + oa * 256));
+  // table fragment f at k step s: group g = fr / 4, rows 16 (fr % 4) + rl, 16-byte chunk 4 s + jg
+  const char* Eb = (const char*)a.emb;
+  auto tab = [&](int f, int s) -> const u32x4* {
+    const int g = fr[f] >> 2;
+    return (const u32x4*)(Eb + ((size_t)g * CH + 4 * s + jg) * 1024 + (size_t)((fr[f] & 3) * 16 + rl) * 16);
   };
-  auto loadB = [&](int st, int step) {
-    const uint32_t oe = (uint32_t)(4 * (step < KS ? step : KS - 1));
+  // staging: vector v of chunk c is tile t = v / (CK 64), step c CK + (v / 64) % CK, lane v % 64
+  const char* Ab = (const char*)a.hdig;
+  auto stage_load = [&](u32x4* sv, int c) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) Bf[st][f] = ld_nt((const u32x4*)(Eb + (eo + oe * 1024 + 256 * f)));
-  };
-  auto mma = [&](int sa, int sb) {
-#pragma unroll
-    for (int b = 0; b < 6; ++b)
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-        acc[b][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, A[sa][b]),
-                                                          __builtin_bit_cast(i32x4, Bf[sb][f]), acc[b][f], 0, 0, 0);
-  };
-  // this wave's k part: whole groups of four steps, the last part the shortest
-  const int Q = (KSp / 4 + KP - 1) / KP * 4;
-  const int s0 = kp * Q < KSp ? kp * Q : KSp, s1 = s0 + Q < KSp ? s0 + Q : KSp;
-  loadA(0, s0);
-  loadB(0, s0);
-  loadB(1, s0 + 1);
-  loadB(2, s0 + 2);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int s = s0; s < s1; s += 4) {
-    // sched_barrier keeps each step's loads ahead of its MFMAs (the scheduler would otherwise
-    // sink them to their uses and expose the load latency at every step)
-    loadA(1, s + 1);
-    loadB(3, s + 3);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0, 0);
-    loadA(0, s + 2);
-    loadB(0, s + 4);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(1, 1);
-    loadA(1, s + 3);
-    loadB(1, s + 5);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0, 2);
-    loadA(0, s + 4);
-    loadB(2, s + 6);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(1, 3);
-  }
-
-  // exact partial dot products of this k part; parts 1.. hand theirs to part 0 through LDS
-  long long T[4][4];
-#pragma unroll
-  for (int f = 0; f < 4; ++f)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      long long t = 0;
-#pragma unroll
-      for (int b = 0; b < 6; ++b) t += (long long)acc[b][f][e] << (8 * b);
-      T[f][e] = t;
+    for (int i = 0; i < SV; ++i) {
+      const int v0 = tid + kHsThreads * i, v = v0 < CHUNK ? v0 : CHUNK - 1;
+      const int t = v / (CK * 64), r = v - t * (CK * 64);
+      sv[i] = *(const u32x4*)(Ab + ((size_t)t * CHp + 4 * c * CK) * 256 + (size_t)r * 16);
     }
-  if (kp > 0) {
+  };
+  auto stage_store = [&](const u32x4* sv, int buf) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int i = 0; i < SV; ++i) {
+      const int v = tid + kHsThreads * i;
+      if (CHUNK % kHsThreads == 0 || v < CHUNK) abuf[buf * CHUNK + v] = sv[i];
+    }
+  };
+  // accumulators: wave tile j = b NHW + hh is digit b of row block rg NHW + hh (LDS tile b NH + rg NHW + hh)
+  i32x4 acc[NTW][F];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tpart[kp - 1][wl][4 * f + e][lane] = T[f][e];
-  }
+  for (int t = 0; t < NTW; ++t)
+#pragma unroll
+    for (int f = 0; f < F; ++f) acc[t][f] = i32x4{0, 0, 0, 0};
+  u32x4 Bf[kHsDB][F];
+  u32x4 sv[SV];
+  // prologue: chunk 0 staged (its loads first), the table steps 0 .. DB - 1 in flight
+  stage_load(sv, 0);
+#pragma unroll
+  for (int d = 0; d < kHsDB; ++d)
+#pragma unroll
+    for (int f = 0; f < F; ++f) Bf[d][f] = ld_nt(tab(f, d < KS ? d : KS - 1));
+  stage_store(sv, 0);
   lds_barrier();
-  if (kp == 0) {
+  const int NC = KS / CK;
+  // one loop turn = kHsDB k steps; the last turn issues no table loads (there is no step after
+  // it: loads there would only delay the epilogue, and loads in a branch would make every chunk's
+  // staging wait count on the fewest loads in flight, draining the ring)
+  auto turn = [&](int it, auto last) {
+    constexpr bool LAST = decltype(last)::value;
 #pragma unroll
-    for (int q = 0; q < KP - 1; ++q)
+    for (int u = 0; u < kHsDB; ++u) {
+      const int step = kHsDB * it + u;
+      const int c = step / CK, buf = c & 1;
+      if (u % CK == 0) {
+        stage_load(sv, c + 1 < NC ? c + 1 : NC - 1);  // the next chunk
+        // sched_barrier pins the loads where they are issued: the scheduler would otherwise sink
+        // them to the end of the unrolled steps, and the next step's table wait would then
+        // expose the whole load latency
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const u32x4* At = abuf + buf * CHUNK + (step - c * CK) * 64 + lane;
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int j0 = 0; j0 < NTW; j0 += AG) {
+        u32x4 A[AG];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) T[f][e] += tpart[q][wl][4 * f + e][lane];
-  }
-
-  // logits (part 0) and the best of this lane per row e (vocabulary rows increase with f)
-  float best[4];
-  int bidx[4];
+        for (int j = 0; j < AG; ++j) {
+          const int b = (j0 + j) / NHW, hh = (j0 + j) % NHW;
+          A[j] = At[((b * NH + rg * NHW + hh) * CK) * 64];
+        }
+        // every read of the group issued before its MFMAs (the scheduler would otherwise reuse
+        // two registers and wait an LDS round trip for every four MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) { best[e] = -INFINITY; bidx[e] = 0x7fffffff; }
+        for (int j = 0; j < AG; ++j)
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    const int v = g * 64 + 16 * f + rl;
-    const float sv = h2f(sc[f]);
+          for (int f = 0; f < F; ++f)
+            acc[j0 + j][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, A[j]),
+                                                                 __builtin_bit_cast(i32x4, Bf[u][f]), acc[j0 + j][f], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!LAST) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = 16 * h + 4 * jg + e;
-      const long long T_ = T[f][e];
-      if (kp == 0 && gok && m < M && v < a.V) {
-        const uint16_t lh = f2h((float)((double)T_ * 0x1p-24) * sv);
-        if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
-        const float lv = h2f(lh);
-        if (lv > best[e]) { best[e] = lv; bidx[e] = v; }
+        for (int f = 0; f < F; ++f) Bf[u][f] = ld_nt(tab(f, step + kHsDB));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (u % CK == CK - 1) {  // end of chunk c: the next chunk into the other buffer
+        stage_store(sv, buf ^ 1);
+        lds_barrier();
       }
     }
+  };
+#pragma nounroll
+  for (int it = 0; it < KS / kHsDB - 1; ++it) turn(it, std::false_type{});
+  turn(KS / kHsDB - 1, std::true_type{});
+
+  // exact dot products: lane l holds activation rows 16 (rg NHW + hh) + 4 jg + e of vocabulary
+  // rows 16 fr[f] + rl; T = sum_b S_b 256^b (int64)
+  float best[NHW][4];
+  int bidx[NHW][4];
+#pragma unroll
+  for (int hh = 0; hh < NHW; ++hh)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { best[hh][e] = -INFINITY; bidx[hh][e] = 0x7fffffff; }
+#pragma unroll
+  for (int f = 0; f < F; ++f) {
+    const int v = 16 * (fb0 + f) + rl;
+    const float svv = h2f(sc[f]);
+#pragma unroll
+    for (int hh = 0; hh < NHW; ++hh)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        long long T = 0;
+#pragma unroll
+        for (int b = 0; b < 6; ++b) T += (long long)acc[b * NHW + hh][f][e] << (8 * b);
+        const int m = 16 * (rg * NHW + hh) + 4 * jg + e;
+        if (fb0 + f < nfr && m < M && v < a.V) {
+          const uint16_t lh = f2h((float)((double)T * 0x1p-24) * svv);
+          if (a.logits) a.logits[(size_t)m * a.V + v] = lh;
+          const float lv = h2f(lh);
+          if (lv > best[hh][e]) { best[hh][e] = lv; bidx[hh][e] = v; }  // v increases with f
+        }
+      }
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float b = best[e];
-    int bi = bidx[e];
+  for (int hh = 0; hh < NHW; ++hh)
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {  // the 16 lanes of row group jg
-      const float ob = __shfl_xor(b, o, 16);
-      const int oi = __shfl_xor(bi, o, 16);
-      if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+    for (int e = 0; e < 4; ++e) {
+      row_argmax_dpp(best[hh][e], bidx[hh][e]);  // the 16 lanes of row group jg
+      if (rl == 0) {
+        wbest[wave][16 * hh + 4 * jg + e] = best[hh][e];
+        widx[wave][16 * hh + 4 * jg + e] = bidx[hh][e];
+      }
     }
-    if (kp == 0 && rl == 0) {
-      wbest[vh][16 * h + 4 * jg + e] = b;
-      widx[vh][16 * h + 4 * jg + e] = bi;
-    }
-  }
   __syncthreads();
   const int NGW = (int)gridDim.x;
-  if (tid < M) {
-    float b = wbest[0][tid];
-    int bi = widx[0][tid];
-    if (wbest[1][tid] > b || (wbest[1][tid] == b && widx[1][tid] < bi)) { b = wbest[1][tid]; bi = widx[1][tid]; }
+  if (tid < M) {  // row tid: the waves of its row group
+    const int g = tid / (16 * NHW), rw = tid % (16 * NHW);
+    float vb[WPG];
+    int vi[WPG];
+#pragma unroll
+    for (int w = 0; w < WPG; ++w) { vb[w] = wbest[g * WPG + w][rw]; vi[w] = widx[g * WPG + w][rw]; }
+    float b = vb[0];
+    int bi = vi[0];
+#pragma unroll
+    for (int w = 1; w < WPG; ++w) argmax_take(b, bi, vb[w], vi[w]);
     __hip_atomic_store(a.part_val + (size_t)tid * NGW + blockIdx.x, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(a.part_idx + (size_t)tid * NGW + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -735,10 +795,23 @@ __global__ __launch_bounds__(128 * NH * KP) __attribute__((amdgpu_waves_per_eu(2
   if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(NGW - 1);
   __syncthreads();
   if (!is_last) return;
-  argmax_pairs<NWP * KP, (MP + NWP * KP - 1) / (NWP * KP), kHeadMaxGroups / 128>(a, M, NGW, next_tok);
+  argmax_pairs<kHsWaves, (MP + kHsWaves - 1) / kHsWaves, kHeadMaxGroups / 128>(a, M, NGW, next_tok);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) embed_next<false, 128 * NH * KP>(a, next_tok, M, D);
+  // the embedding in one round of loads up to 20 chunks per thread (64 rows of 2560 bytes)
+  constexpr int KBE = (MP * 320 + kHsThreads - 1) / kHsThreads < 20 ? (MP * 320 + kHsThreads - 1) / kHsThreads : 20;
+  if (a.x_next) embed_next<false, kHsThreads, KBE>(a, next_tok, M, D);
+}
+
+template <int NH>
+static hipError_t launch_head_i8s(const HeadArgs& a, int M, hipStream_t s) {
+  const size_t shm = hs_lds_bytes(NH);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_i8s_kernel<NH>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (e != hipSuccess) return e;
+  const int nfr = (a.V + 15) / 16, per = hs_wg_frags(NH);
+  hipLaunchKernelGGL((head_i8s_kernel<NH>), dim3((nfr + per - 1) / per), dim3(kHsThreads), shm, s, a, M);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -862,12 +935,7 @@ __global__ __launch_bounds__(kHT) void head_mfma_kernel(HeadArgs a, int M) {
     for (int j = 0; j < 4; ++j) {
       float b = best[ib][j];
       int bi = bidx[ib][j];
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(b, o, 16);
-        const int oi = __shfl_xor(bi, o, 16);
-        if (ob > b || (ob == b && oi < bi)) { b = ob; bi = oi; }
-      }
+      row_argmax_dpp(b, bi);  // the 16 lanes of the row group
       if ((lane & 15) == 0) {
         const int m = ib * 16 + 4 * (lane >> 4) + j;
         wbest[wave][m] = b;
@@ -911,14 +979,12 @@ hipError_t launch_head_batched(const HeadArgs& a, int M, hipStream_t s) {
     hipLaunchKernelGGL(head_digits_kernel, dim3(16 * nh), dim3(256), 0, s, a.x, a.norm_f, (int8_t*)a.hdig, M, nh, a.D);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int grid = ((a.V + 63) / 64 + 1) / 2;
     switch (nh) {
-      case 1: hipLaunchKernelGGL((head_i8b_kernel<1, 4>), dim3(grid), dim3(512), 0, s, a, M); break;
-      case 2: hipLaunchKernelGGL((head_i8b_kernel<2, 2>), dim3(grid), dim3(512), 0, s, a, M); break;
-      case 3: hipLaunchKernelGGL((head_i8b_kernel<3, 1>), dim3(grid), dim3(384), 0, s, a, M); break;
-      default: hipLaunchKernelGGL((head_i8b_kernel<4, 1>), dim3(grid), dim3(512), 0, s, a, M); break;
+      case 1: return launch_head_i8s<1>(a, M, s);
+      case 2: return launch_head_i8s<2>(a, M, s);
+      case 3: return launch_head_i8s<3>(a, M, s);
+      default: return launch_head_i8s<4>(a, M, s);
     }
-    return hipGetLastError();
   }
   if (!a.xf) return hipErrorInvalidValue;
   hipLaunchKernelGGL(final_norm_kernel, dim3(M), dim3(256), 0, s, a.x, a.norm_f, (uint16_t*)a.xf, a.D);

@@ -30,7 +30,7 @@ def tiny_weights():
     return make_weights(config_tiny(n_layer=3), seed=0)
 
 
-@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 16, 32, 64])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 16, 32, 40, 64])
 def test_tiny_forward_stepwise(tiny_weights, B):
     w = tiny_weights
     print(f"tiny forward B={B}", flush=True)

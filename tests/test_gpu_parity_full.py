@@ -159,7 +159,7 @@ def test_2p7b_dims_full_vocab_batch64():
 @pytest.mark.parametrize("B", [1, 5])
 def test_largest_vocab_head(B):
     """The largest supported vocabulary (65536 = 1024 table groups: the most per-workgroup argmax
-    pairs the heads' last workgroup reduces) at B = 1 (head_i8_kernel) and B = 5 (head_i8b_kernel):
+    pairs the heads' last workgroup reduces) at B = 1 (head_i8_kernel) and B = 5 (head_i8s_kernel):
     tokens and final logits identical to the oracle."""
     c = DFSSMConfig(n_layer=1, d_model=512, d_inner=1024, d_state=128, nheads=16, headdim=64, ngroups=1,
                     vocab_size=65536, kw=4)
