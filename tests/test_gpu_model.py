@@ -324,6 +324,48 @@ def test_wide_model_head_batch4(emb_code):
     assert gpu.error_flag() == 0
 
 
+@pytest.mark.parametrize("B", [8, 40, 64])
+def test_batched_head_large_final_norm_values(B):
+    """The batched exact head splits xf 2^24 into six signed base-256 digits; rows whose xf needs
+    only the low four digits (|xf| < 128), five (up to 2^15) or all six (above) must all come out
+    exact. Crafted residual rows through dfssm_lmhead_argmax with the final-norm weight of column 0
+    set to 2000: ordinary rows put xf in column 0 up to ~1e4 (five digits); a large entry in column
+    0 of every fourth row puts it near 3.9e4 (six); the unscaled weight keeps every |xf| below 128
+    (four). Logits and tokens identical to the oracle's head (RMSNorm then the exact int8 head)."""
+    from dfssm import _C
+    w = make_weights(config_tiny(n_layer=1), seed=17)
+    D, V = w.cfg.d_model, w.cfg.vocab_size
+    lib = _C.lib()
+    rng = np.random.default_rng(100 + B)
+    for case in ("four", "five", "six"):
+        wc = make_weights(config_tiny(n_layer=1), seed=17)
+        if case != "four":
+            nf = wc.norm_f.astype(np.float64)
+            nf[0] = 2000.0
+            wc.norm_f = nf.astype(wc.norm_f.dtype)
+        x = rng.normal(0.0, 1.0, (B, D)).astype(np.float16)
+        if case == "six":
+            x[::4, 0] = np.float16(40.0)
+        print(f"head digits ({case}), B={B}", flush=True)
+        gpu = DFSSMModel.from_weights(wc, device=DEV, batch_size=B)
+        xg = torch.from_numpy(x).to(DEV)
+        lg = torch.empty((B, V), dtype=torch.float16, device=DEV)
+        nx = torch.empty(B, dtype=torch.int64, device=DEV)
+        _C.check(lib.dfssm_lmhead_argmax(gpu._model, xg.data_ptr(), gpu.workspace.data_ptr(), lg.data_ptr(),
+                                         nx.data_ptr(), None, _C.stream()))
+        torch.cuda.synchronize()
+        xf = O.rmsnorm(x, wc.norm_f)
+        if case == "six":
+            assert np.abs(xf[::4, 0].astype(np.float32)).min() >= 32768.0
+        lo, no = O.lm_head(wc, xf)
+        assert np.isfinite(lo.astype(np.float32)).all()
+        got = _np16(lg).astype(np.float32)
+        assert np.abs(got - lo.astype(np.float32)).max() == 0.0, case
+        np.testing.assert_array_equal(nx.cpu().numpy(), no)
+        assert gpu.error_flag() == 0
+        del gpu
+
+
 @pytest.fixture(scope="module")
 def tiny_weights_f16():
     # the exporter's fp16 embedding table (format embedding code 0)
