@@ -33,7 +33,7 @@ Derived derive(const dfssm_dims* d) {
 }
 
 struct WsLayout {
-  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hpart, hdig, samp, ticket, err, launches, gtick,
+  size_t proj, g, slots, q, planes, qsum, xs, h, xf, part_val, part_idx, hdig, samp, ticket, err, launches,
       proj_t, g_t, h_t, dt_t, bc_t, g_s, launches_s, x_s, launches_o, total;
 };
 
@@ -53,15 +53,13 @@ WsLayout ws_layout(const dfssm_dims* d) {
   w.xf = off;       off = align_up(off + (size_t)r.B * r.D * 2);
   w.part_val = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
   w.part_idx = off; off = align_up(off + (size_t)r.B * r.head_groups * 4);
-  w.hpart = off;    off = align_up(off + (r.B <= 4 ? (size_t)r.head_groups * (r.D / 512) * r.B * 64 * 8 : 0));
   w.hdig = off;     off = align_up(off + (r.B > 4 ? head_digit_bytes(r.B, r.D) : 0));  // batched int8 head
   w.samp = off;     off = align_up(off + (size_t)r.B * 2 * sample_row_floats(r.V) * 4);  // sampler rows
   w.ticket = off;   off = align_up(off + 4);
   w.err = off;      off = align_up(off + 4);
-  // one-launch layer: arrival ticket, epoch and the tagged exchange words (zeroed by
+  // one-launch layer: per-workgroup launch counts and the tagged exchange words (zeroed by
   // dfssm_workspace_init together with the head's ticket and the error flag)
   w.launches = off; off = align_up(off + (size_t)kFusedMaxGrid * 4);
-  w.gtick = off;    off = align_up(off + (size_t)r.head_groups * 4);
   w.proj_t = off;   off = align_up(off + (size_t)r.B * r.IPO * 4);
   w.g_t = off;      off = align_up(off + (size_t)kGRep * kGStride * 4);
   w.h_t = off;      off = align_up(off + (size_t)kXRep * kHStride * 4);
@@ -615,8 +613,6 @@ int dfssm_lmhead_argmax(const dfssm_model* model, const uint16_t* x, void* works
   a.part_val = (float*)(ws + w.part_val); a.part_idx = (int*)(ws + w.part_idx);
   a.ticket = (unsigned*)(ws + w.ticket);
   a.next = next; a.x_next = x_next;
-  a.hpart = (long long*)(ws + w.hpart);
-  a.gtick = (unsigned*)(ws + w.gtick);
   rc = hip_status(launch_head(a, r.B, as_stream(stream)));
   if (rc) return rc;
   return DFSSM_OK;

@@ -255,8 +255,6 @@ struct HeadArgs {
   int64_t* next;             // (M) greedy tokens
   uint16_t* x_next;          // optional (M, D): embedding of the greedy tokens
   const uint16_t* xf;        // batched head: (M, D) scratch for the final-normed rows
-  long long* hpart;          // int8 head at M <= 4: (groups, D / 512, M, 64) exact partial dot products
-  unsigned* gtick;           // (groups) arrival counters, zero before the first launch, left zero
   const int8_t* hdig;        // int8 head at M >= 5: digit planes, head_digit_bytes(M, D) bytes
 };
 

@@ -276,17 +276,11 @@ __global__ void tile_emb_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
 // and T = sum_b S_b 256^b (int64) = sum_k X_k E[v][k] exactly. The logit is fp16(fp32(T 2^-24) *
 // s_E[v]): the fp64 kernel's value whenever that one's sum is exact, and exact without condition.
 //
-// Work unit: 64 vocabulary rows (one tile group of the table) x a 512-wide k slice, i.e. 32 KiB of
-// table per workgroup and many short workgroups, which the dispatcher keeps balanced over the CUs
-// (a few long workgroups per CU left the last CUs streaming alone). Each workgroup computes the
-// final RMSNorm scale of its rows, the digits of its k slice, and 8 k steps of 64 with two MFMAs
-// each: B = the table (lane l: row 16 w + l % 16, tiled chunk 4 s + l / 16 of the slice), A = the
-// digit rows (lane l: row l % 16 of the tile, the same k block); tile 0 holds digits 0..3 of
-// sequence m at A-rows 4 m + b, tile 1 digits 4, 5 at A-rows 4 m, 4 m + 1, so lane group m = l / 16
-// ends with all six sums of (m, row l % 16) (the output layout is D[4 (l / 16) + e][l % 16]). The
-// slice's partial T goes out with write-through stores; the last of the group's slices to arrive
-// (per-group counter) adds them up, writes the logits and the group's (max, first index) pairs,
-// and the last group reduces those (the global ticket, as in the fp64 kernel).
+// MFMA layout (per 64-wide k step, two MFMAs): B = the table (lane l: row l % 16 of the wave's
+// 16 rows, tiled 16-byte chunk l / 16 of the step), A = the digit rows (lane l: row l % 16 of the
+// A tile, the same k block); tile 0 holds digits 0..3 of sequence m at A-rows 4 m + b, tile 1
+// digits 4, 5 at A-rows 4 m, 4 m + 1, so lane group m = l / 16 ends with all six sums of
+// (m, row l % 16) (the output layout is D[4 (l / 16) + e][l % 16]).
 // ---------------------------------------------------------------------------------------------
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kHKS = 512;  // k slice per workgroup
@@ -298,156 +292,213 @@ __device__ __forceinline__ long long fx24(uint16_t hb) {
   return (hb & 0x8000) ? -X : X;
 }
 
-template <int M>
-__global__ __launch_bounds__(256) void head_i8_kernel(HeadArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t dg[M * 6][kHKS];  // digits of the slice
-  __shared__ double red[4][M];
-  __shared__ float pv[4][M];
-  __shared__ int pix[4][M];
-  __shared__ bool last_g, is_last;
+// ---------------------------------------------------------------------------------------------
+// Work unit: each 1024-thread workgroup (one per CU) owns kHgGroups consecutive 64-row table
+// groups over the whole k range (KP = D / 512 slices of 512, a template parameter so that the
+// slice loop unrolls), so no partial sum leaves the workgroup. Wave w takes table rows
+// 16 (w % 4) .. + 15 of group kHgGroups blockIdx + w / 4 and streams them through a two-slice
+// register ring: slice kp + 2 is issued as soon as slice kp has gone through the MFMAs. The
+// workgroup computes the final norm and the six digit planes of the whole rows once, into LDS
+// (M * 6 * D bytes), two columns per thread; the int32 accumulators hold the sums over all of k
+// (at most 5120 * 128 * 127 < 2^31 in magnitude), recombined in int64. Then the logits, the
+// workgroup's (max, first index) pair per sequence, and the last workgroup (ticket) reduces the
+// pairs and may write the next embedding. Measured at batch 1, 1.3B shape, per head: 25.3 us for
+// the earlier form (256-thread workgroups on 64 rows x a 512-wide slice, partial sums combined by
+// the last slice of each group through a per-group counter); 23.5 us for 256-thread workgroups on
+// one group over all of k (each of the 786 workgroups computed the whole rows' digit planes with
+// four waves, which held back the ring's refill); 20.1 us for this form.
+// ---------------------------------------------------------------------------------------------
+constexpr int kHgThreads = 1024, kHgWaves = kHgThreads / 64, kHgGroups = kHgWaves / 4;
+
+template <int M, int KP>
+__global__ __launch_bounds__(kHgThreads) void head_i8g_kernel(HeadArgs a, int NG) {
+  extern __shared__ __attribute__((aligned(16))) int8_t hg_dg[];  // [M * 6][D] digit planes
+  __shared__ double red[kHgWaves][M];
+  __shared__ float pv[kHgWaves][M];
+  __shared__ int pix[kHgWaves][M];
+  __shared__ int next_tok[M];
+  __shared__ bool is_last;
+  constexpr int D = KP * kHKS, CH = D / 16, PH = D / 2;
+  constexpr int PJ = (PH + kHgThreads - 1) / kHgThreads;  // column pairs per thread (tid + 1024 j)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int jg = lane >> 4, rl = lane & 15;
-  const int D = a.D, CH = D / 16, KP = D / kHKS;
-  const int NG = (int)gridDim.x / KP;
-  const int g = (int)blockIdx.x / KP, kp = (int)blockIdx.x % KP;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int g = kHgGroups * wg + (wave >> 2);           // this wave's table group (may be >= NG)
+  const int gc = g < NG ? g : NG - 1;                    // clamped for the loads
+  const int row = 16 * (wave & 3) + rl, v = g * 64 + row;
 
-  // loads: x for the sum of squares first (so that waiting for it does not wait for the table),
-  // then this slice's x and norm_f, then the 8 table chunks of this lane
-  constexpr int XR = 3;  // 8-element x chunks per thread and row: D <= 5120 = 3 * 2048 - 1024
-  u32x4 xv[M][XR];
+  // loads: x and norm_f of this thread's column pairs (unconditional, from clamped pairs: a load in
+  // a branch makes the compiler wait for every load at the join), the row scale, then the table's
+  // first two slices. Loads complete in issue order, and the scheduler would otherwise move the
+  // table loads ahead of norm_f (the digit planes then waited for the table); sched_barrier pins
+  // each group where it is issued.
+  uint32_t xp[M][PJ];
+  float2 nf[PJ];
 #pragma unroll
-  for (int m = 0; m < M; ++m)
+  for (int j = 0; j < PJ; ++j) {
+    const int p = tid + kHgThreads * j, pc = p < PH ? p : 0;
 #pragma unroll
-    for (int i = 0; i < XR; ++i) {
-      const int k0 = 8 * tid + 2048 * i;
-      xv[m][i] = k0 < D ? *(const u32x4*)(a.x + (size_t)m * D + k0) : u32x4{0u, 0u, 0u, 0u};
-    }
-  const int ks = kp * kHKS + 2 * tid;  // this thread's two slice columns
-  uint32_t xs2[M];
+    for (int m = 0; m < M; ++m) xp[m][j] = *(const uint32_t*)(a.x + (size_t)m * D + 2 * pc);
+    nf[j] = *(const float2*)(a.norm_f + 2 * pc);
+  }
+  const uint16_t es = a.emb_scale[v < a.V ? v : a.V - 1];
+  __builtin_amdgcn_sched_barrier(0);
+  const u32x4* E = (const u32x4*)a.emb + ((size_t)gc * CH + jg) * 64 + 16 * (wave & 3) + rl;
+  u32x4 b0[8], b1[8];
+  auto load_slice = [&](u32x4 (&bf)[8], int kp) {
 #pragma unroll
-  for (int m = 0; m < M; ++m) xs2[m] = *(const uint32_t*)(a.x + (size_t)m * D + ks);
-  const float2 nf = *(const float2*)(a.norm_f + ks);
-  const u32x4* E = (const u32x4*)a.emb + ((size_t)g * CH + kp * (kHKS / 16) + jg) * 64 + 16 * wave + rl;
-  u32x4 buf[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) buf[s] = ld_nt(E + (size_t)(4 * s) * 64);
+    for (int s = 0; s < 8; ++s) bf[s] = ld_nt(E + (size_t)(kp * (kHKS / 16) + 4 * s) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // the second slice before the digit planes at M = 1, after them for more rows (whose digit
+  // registers and a second slice in flight together spilled; at M = 3 so did the first slice)
+  if constexpr (M != 3) load_slice(b0, 0);
+  if constexpr (KP > 1 && M == 1) load_slice(b1, 1);
 
   // final RMSNorm scale of each row (fp64 sum of squares: exact)
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     double ps = 0.0;
 #pragma unroll
-    for (int i = 0; i < XR; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const double v = (double)h2f((uint16_t)(xv[m][i][e >> 1] >> (16 * (e & 1))));
-        ps += v * v;
+    for (int j = 0; j < PJ; ++j)
+      if (tid + kHgThreads * j < PH) {
+        const double x0 = (double)h2f((uint16_t)xp[m][j]), x1 = (double)h2f((uint16_t)(xp[m][j] >> 16));
+        ps += x0 * x0;
+        ps += x1 * x1;
       }
     ps = wave_sum_dpp_f64(ps);
     if (lane == 0) red[wave][m] = ps;
   }
-  __syncthreads();
+  // barriers that order LDS only: a full barrier would first wait for every load of the wave,
+  // the table slices in flight included
+  lds_barrier();
+  // digit planes of xf 2^24 (xf = fp16(x r norm_f), an integer below 2^41 in magnitude): six
+  // signed base-256 digits, the pair's two columns of a plane per 2-byte store
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const double ss = red[0][m] + red[1][m] + red[2][m] + red[3][m];
+    double ss = 0.0;
+#pragma unroll
+    for (int q = 0; q < kHgWaves; ++q) ss += red[q][m];
     const float r = 1.0f / sqrt_rn((float)ss * (1.0f / (float)D) + 1e-5f);
-    uint32_t pk[6] = {0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      long long X = fx24(f2h(r16((h2f((uint16_t)(xs2[m] >> (16 * i))) * r) * (i ? nf.y : nf.x))));
+    for (int j = 0; j < PJ; ++j) {
+      const int p = tid + kHgThreads * j;
+      if (p < PH) {
+        uint32_t pk[6] = {0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int b = 0; b < 5; ++b) {
-        const int d = (int)(int8_t)(X & 0xff);
-        X = (X - d) >> 8;
-        pk[b] |= (uint32_t)(d & 0xff) << (8 * i);
+        for (int h = 0; h < 2; ++h) {
+          long long X = fx24(f2h(r16((h2f((uint16_t)(xp[m][j] >> (16 * h))) * r) * (h ? nf[j].y : nf[j].x))));
+#pragma unroll
+          for (int b = 0; b < 5; ++b) {
+            const int d = (int)(int8_t)(X & 0xff);
+            X = (X - d) >> 8;
+            pk[b] |= (uint32_t)(d & 0xff) << (8 * h);
+          }
+          pk[5] |= (uint32_t)((int)X & 0xff) << (8 * h);
+        }
+#pragma unroll
+        for (int b = 0; b < 6; ++b) *(uint16_t*)(hg_dg + (size_t)(m * 6 + b) * D + 2 * p) = (uint16_t)pk[b];
       }
-      pk[5] |= (uint32_t)((int)X & 0xff) << (8 * i);
     }
-#pragma unroll
-    for (int b = 0; b < 6; ++b) *(uint16_t*)&dg[m * 6 + b][2 * tid] = (uint16_t)pk[b];
   }
-  __syncthreads();
+  if constexpr (M == 3) load_slice(b0, 0);
+  if constexpr (KP > 1 && M > 1) load_slice(b1, 1);
+  lds_barrier();
 
-  // 8 k steps, two MFMAs each; rows without a digit read row 0 and are zeroed by a select
+  // the k steps: two MFMAs each (A = digit rows 4 m + b of tile 0 and 4 m + 4 + b of tile 1, zero
+  // where there is no such digit; rows without a digit read plane 0 and are zeroed by a select)
   const int ma = rl >> 2, ba = rl & 3;
   const bool a0ok = ma < M, a1ok = ma < M && ba < 2;
-  const int8_t* A0p = &dg[a0ok ? ma * 6 + ba : 0][16 * jg];
-  const int8_t* A1p = &dg[a1ok ? ma * 6 + 4 + ba : 0][16 * jg];
+  const int8_t* A0p = hg_dg + (size_t)(a0ok ? ma * 6 + ba : 0) * D + 16 * jg;
+  const int8_t* A1p = hg_dg + (size_t)(a1ok ? ma * 6 + 4 + ba : 0) * D + 16 * jg;
   const i32x4 z4 = {0, 0, 0, 0};
   i32x4 acc0 = z4, acc1 = z4;
+  auto mfma_slice = [&](const u32x4 (&bf)[8], int kp) {
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const i32x4 Bv = __builtin_bit_cast(i32x4, buf[s]);
-    const i32x4 A0r = *(const i32x4*)(A0p + 64 * s);
-    const i32x4 A1r = *(const i32x4*)(A1p + 64 * s);
-    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0ok ? A0r : z4, Bv, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1ok ? A1r : z4, Bv, acc1, 0, 0, 0);
+    for (int s = 0; s < 8; ++s) {
+      const i32x4 Bv = __builtin_bit_cast(i32x4, bf[s]);
+      const i32x4 A0r = *(const i32x4*)(A0p + kp * kHKS + 64 * s);
+      const i32x4 A1r = *(const i32x4*)(A1p + kp * kHKS + 64 * s);
+      acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0ok ? A0r : z4, Bv, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1ok ? A1r : z4, Bv, acc1, 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int kp = 0; kp < KP; ++kp) {
+    if (kp % 2 == 0) {
+      mfma_slice(b0, kp);
+      if (kp + 2 < KP) load_slice(b0, kp + 2);
+    } else {
+      mfma_slice(b1, kp);
+      if (kp + 2 < KP) load_slice(b1, kp + 2);
+    }
   }
-  const int row = 16 * wave + rl;
-  if (jg < M) {
-    const long long T = (long long)acc0[0] + ((long long)acc0[1] << 8) + ((long long)acc0[2] << 16) +
-                        ((long long)acc0[3] << 24) + ((long long)acc1[0] << 32) + ((long long)acc1[1] << 40);
-    __hip_atomic_store(a.hpart + (((size_t)g * KP + kp) * M + jg) * 64 + row, T, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // the partial has reached the device-coherent level
-  __syncthreads();
-  if (tid == 0) last_g = atomicAdd(a.gtick + g, 1u) == (unsigned)(KP - 1);
-  __syncthreads();
-  if (!last_g) return;
 
-  // last slice of group g: logits of its 64 rows, then the group's (max, first index) per row m
-  if (tid == 0) a.gtick[g] = 0u;
+  // logits of the workgroup's rows, its (max, first index) pair per sequence, and the last
+  // workgroup (ticket) reduces the pairs
   float best = -INFINITY;
   int bidx = 0x7fffffff;
-  const int v = g * 64 + row;
   if (jg < M && v < a.V) {
-    long long tp[kHeadMaxKP];  // all slices' partials loaded before any is added
-#pragma unroll
-    for (int q = 0; q < kHeadMaxKP; ++q)
-      tp[q] = __hip_atomic_load(a.hpart + (((size_t)g * KP + (q < KP ? q : KP - 1)) * M + jg) * 64 + row,
-                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    long long T = 0;
-#pragma unroll
-    for (int q = 0; q < kHeadMaxKP; ++q)
-      if (q < KP) T += tp[q];
-    const uint16_t lh = f2h((float)((double)T * 0x1p-24) * h2f(a.emb_scale[v]));
+    const long long T = (long long)acc0[0] + ((long long)acc0[1] << 8) + ((long long)acc0[2] << 16) +
+                        ((long long)acc0[3] << 24) + ((long long)acc1[0] << 32) + ((long long)acc1[1] << 40);
+    const uint16_t lh = f2h((float)((double)T * 0x1p-24) * h2f(es));
     if (a.logits) a.logits[(size_t)jg * a.V + v] = lh;
     best = h2f(lh);
     bidx = v;
   }
-  row_argmax_dpp(best, bidx);  // the 16 lanes of the row group
+  row_argmax_dpp(best, bidx);  // the 16 lanes of the sequence's row group
   if (rl == 0 && jg < M) {
     pv[wave][jg] = best;
     pix[wave][jg] = bidx;
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < M) {
     float b = pv[0][tid];
     int bi = pix[0][tid];
 #pragma unroll
-    for (int w = 1; w < 4; ++w)
-      if (pv[w][tid] > b || (pv[w][tid] == b && pix[w][tid] < bi)) { b = pv[w][tid]; bi = pix[w][tid]; }
-    __hip_atomic_store(a.part_val + (size_t)tid * NG + g, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(a.part_idx + (size_t)tid * NG + g, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 1; q < kHgWaves; ++q) argmax_take(b, bi, pv[q][tid], pix[q][tid]);
+    __hip_atomic_store(a.part_val + (size_t)tid * G + wg, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.part_idx + (size_t)tid * G + wg, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0);  // the pair has reached the device-coherent level
   __syncthreads();
-  if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(NG - 1);
+  if (tid == 0) is_last = atomicAdd(a.ticket, 1u) == (unsigned)(G - 1);
   __syncthreads();
   if (!is_last) return;
-  __shared__ int next_tok[M];
-  argmax_pairs<4, 1, kHeadMaxGroups / 64>(a, M, NG, next_tok);
+  argmax_pairs<kHgWaves, 1, kHeadMaxGroups / kHgGroups / 64>(a, M, G, next_tok);
   if (tid == 0) *a.ticket = 0u;
   __syncthreads();
-  if (a.x_next) embed_next<false, 256>(a, next_tok, M, D);
+  if (a.x_next) embed_next<false, kHgThreads>(a, next_tok, M, D);
 }
 
-template <int M>
-static hipError_t launch_head_i8(const HeadArgs& a, int groups, hipStream_t s) {
-  if (!a.hpart || !a.gtick || a.D % kHKS) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(head_i8_kernel<M>, dim3(groups * (a.D / kHKS)), dim3(256), 0, s, a);
+template <int M, int KP>
+static hipError_t launch_head_i8g_kp(const HeadArgs& a, int groups, hipStream_t s) {
+  const size_t shm = (size_t)M * 6 * a.D;  // at most 120 KiB (M = 4, D = 5120)
+  if (shm > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_i8g_kernel<M, KP>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
+  // the pair arrays hold `groups` pairs per row, the workgroups fewer
+  hipLaunchKernelGGL((head_i8g_kernel<M, KP>), dim3((groups + kHgGroups - 1) / kHgGroups), dim3(kHgThreads), shm,
+                     s, a, groups);
   return hipGetLastError();
+}
+template <int M>
+static hipError_t launch_head_i8g(const HeadArgs& a, int groups, hipStream_t s) {
+  switch (a.D / kHKS) {
+    case 1: return launch_head_i8g_kp<M, 1>(a, groups, s);
+    case 2: return launch_head_i8g_kp<M, 2>(a, groups, s);
+    case 3: return launch_head_i8g_kp<M, 3>(a, groups, s);
+    case 4: return launch_head_i8g_kp<M, 4>(a, groups, s);
+    case 5: return launch_head_i8g_kp<M, 5>(a, groups, s);
+    case 6: return launch_head_i8g_kp<M, 6>(a, groups, s);
+    case 7: return launch_head_i8g_kp<M, 7>(a, groups, s);
+    case 8: return launch_head_i8g_kp<M, 8>(a, groups, s);
+    case 9: return launch_head_i8g_kp<M, 9>(a, groups, s);
+    case 10: return launch_head_i8g_kp<M, 10>(a, groups, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int M, bool F16>
@@ -465,10 +516,10 @@ hipError_t launch_head(const HeadArgs& a, int M, hipStream_t s) {
   if (M < 1 || M > 4 || groups > kHeadMaxGroups || a.D > 512 * kHeadMaxKP) return hipErrorInvalidValue;
   if (!a.f16) {
     switch (M) {
-      case 1: return launch_head_i8<1>(a, groups, s);
-      case 2: return launch_head_i8<2>(a, groups, s);
-      case 3: return launch_head_i8<3>(a, groups, s);
-      default: return launch_head_i8<4>(a, groups, s);
+      case 1: return launch_head_i8g<1>(a, groups, s);
+      case 2: return launch_head_i8g<2>(a, groups, s);
+      case 3: return launch_head_i8g<3>(a, groups, s);
+      default: return launch_head_i8g<4>(a, groups, s);
     }
   }
   // fp16 table: the rows' final-normed values sit in LDS as fp64 (8 D bytes per row, at most
