@@ -486,6 +486,7 @@ static hipError_t launch_head_i8g_kp(const HeadArgs& a, int groups, hipStream_t 
 }
 template <int M>
 static hipError_t launch_head_i8g(const HeadArgs& a, int groups, hipStream_t s) {
+  if (a.D % kHKS) return hipErrorInvalidValue;  // whole 512-wide slices (the kernel's D is KP * 512)
   switch (a.D / kHKS) {
     case 1: return launch_head_i8g_kp<M, 1>(a, groups, s);
     case 2: return launch_head_i8g_kp<M, 2>(a, groups, s);
