@@ -874,7 +874,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   lds_barrier();
   TL_FLUSH(epoch_raw * (uint32_t)a.n_layer + (uint32_t)a.layer);
 #endif
-  if (tix() == 0) st_dev(a.launches + bix(), epoch_raw + 1u);
+  // a plain store: the count is read only by the next launch, after the kernel boundary has made
+  // it visible; a device-scope store here held the launch's end for its write-through to memory
+  // (~0.85 us per layer at batch 1: 697 -> 657 us per decode step)
+  if (tix() == 0) a.launches[bix()] = epoch_raw + 1u;
 }
 
 // The one-launch layer waits between its workgroups, so all G of them must be resident at once:

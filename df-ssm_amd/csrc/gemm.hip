@@ -188,7 +188,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
       const uint32_t ep = ld_dev(cnt);
       if (pi < kProPW * a.M) gemm_in_prologue(p, a.N, pi / kProPW, pi % kProPW, (ep + 1u) & 0xffffu, (uint32_t*)qs);
       lds_barrier();  // every wave has used its tag before the count is advanced
-      if (tid == 0) st_dev(cnt, ep + 1u);
+      if (tid == 0) *cnt = ep + 1u;  // read by the next launch only: a plain store suffices
       return;
     }
     if (tid == 0) epoch = ld_dev(cnt);
@@ -291,7 +291,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   double* lod = (double*)(qs + gemm_part_bytes(MI, RT));
   if (PRO && tid == 0) {  // read by every thread after the loop's barriers
     tag_s = (epoch + 1u) & 0xffffu;
-    st_dev(cnt, epoch + 1u);
+    *cnt = epoch + 1u;  // read by the next launch only: a plain store suffices
   }
   // PRO: the next layer's prologue weights (norm weights and LoRA-B table, 20 N bytes, the first
   // 64 KiB of them) into every XCD's L2 -- workgroups 0..7 are dealt one to each XCD -- so the

@@ -747,12 +747,12 @@ __global__ __launch_bounds__(kNT) void scaffold_xchg_kernel(ScaffoldArgs a) {
         if (tid == 0) a.h_out[(size_t)m * DFSSM_LORA_R + r] = hb;
       }
     }
-    if (tid == 0) st_dev(cnt, e + 1u);
+    if (tid == 0) *cnt = e + 1u;  // read by the next call only: a plain store suffices
     return;
   }
   const int g = blockIdx.x - DFSSM_LORA_R;
   if (g * 64 >= a.N) {  // past the output rows: count the call
-    if (tid == 0) st_dev(cnt, ld_dev(cnt) + 1u);
+    if (tid == 0) *cnt = ld_dev(cnt) + 1u;
     return;
   }
   // ---- GEMV workgroup: wave w owns the 128-column chunks c = w + 16 j of its 64 rows; it loads the
@@ -859,7 +859,7 @@ __global__ __launch_bounds__(kNT) void scaffold_xchg_kernel(ScaffoldArgs a) {
     }
     a.y_out[(size_t)m * a.N + n] = f2h(r16((float)lo + y));
   }
-  if (tid == 0) st_dev(cnt, e + 1u);
+  if (tid == 0) *cnt = e + 1u;
 }
 
 template <int M>

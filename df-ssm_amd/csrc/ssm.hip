@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void ssm_prep_kernel(SsmPrepArgs a, int M) {
     gated_prologue<NJ>(a, j % DFSSM_LORA_R, j / DFSSM_LORA_R, tag);
   }
   lds_barrier();  // every wave has read the count (and used its tag) before it is advanced
-  if (threadIdx.x == 0) st_dev(cnt, epoch + 1u);
+  if (threadIdx.x == 0) *cnt = epoch + 1u;  // read by the next launch only: a plain store suffices
 }
 
 bool ssm_prep_supported(int M, int K, int P) { return M >= 1 && K <= kSpMaxK && K % 512 == 0 && P % 16 == 0; }
