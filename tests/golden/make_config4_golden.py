@@ -1,24 +1,27 @@
-"""Write tests/golden/oracle_2p7b_64layer_b4.npz: the oracle's (oracle/oracle.py OracleModel) greedy
-decode of the full config-4 model -- the 2.7B shape with all 64 layers and the 50288-token
-vocabulary, weights make_weights(config_2p7b(), seed 0), the model bench.py measures -- at batch 4,
-so that the GPU path at full depth (64 layers of launch tags, the prefill's wide GEMMs over
->= 256-row chunks at d_model 2560) is checked against it without running the oracle on the GPU box
-(one run takes ~90 s on this container's CPU).
+"""Write the oracle's (oracle/oracle.py OracleModel) greedy decode of the full config-4 model --
+the 2.7B shape with all 64 layers and the 50288-token vocabulary, weights
+make_weights(config_2p7b(), seed 0), the model bench.py measures -- so that the GPU path at full
+depth (64 layers of launch tags, the prefill's wide GEMMs over >= 256-row chunks at d_model 2560)
+is checked against it without running the oracle on the GPU box:
+  tests/golden/oracle_2p7b_64layer_b4.npz    batch 4, a 129-token prompt (~90 s on 8 CPUs)
+  tests/golden/oracle_2p7b_64layer_b64.npz   batch 64 (the benchmark's batch), a 17-token prompt
+                                             (~10 min on 8 CPUs)
 
-Protocol: prompt = make_prompts(4, 50288, 129); the oracle consumes it step by step and then decodes
-greedily, generate(prompt, 4) (129 + 3 steps); then one more step on the last generated token, whose
+Protocol: prompt = make_prompts(B, 50288, T); the oracle consumes it step by step and then decodes
+greedily, generate(prompt, 4) (T + 3 steps); then one more step on the last generated token, whose
 logits and resulting state are hashed.
 
 Contents:
-  prompt       (4, 129) int64
-  tokens       (4, 4) int64   the 4 greedy tokens
-  next_token   (4,) int64     the greedy token after the extra step
-  logits_sha256  ()  str      SHA-256 of the extra step's (4, 50288) fp16 logits, C order
-  state_sha256   ()  str      SHA-256 of the fp32 SSM state after it, (64, 4, 80, 64, 128) C order
-  conv_sha256    ()  str      SHA-256 of the fp16 conv state after it, (64, 4, 5376, 3) C order
-  logits_head  (4, 8) fp16    logits[:, :8] (a readable excerpt)
+  prompt       (B, T) int64
+  tokens       (B, 4) int64   the 4 greedy tokens
+  next_token   (B,) int64     the greedy token after the extra step
+  logits_sha256  ()  str      SHA-256 of the extra step's (B, 50288) fp16 logits, C order
+  state_sha256   ()  str      SHA-256 of the fp32 SSM state after it, (64, B, 80, 64, 128) C order
+  conv_sha256    ()  str      SHA-256 of the fp16 conv state after it, (64, B, 5376, 3) C order
+  logits_head  (B, 8) fp16    logits[:, :8] (a readable excerpt)
 
-    python tests/golden/make_config4_golden.py
+    python tests/golden/make_config4_golden.py            # batch 4
+    python tests/golden/make_config4_golden.py --batch 64 # batch 64
 """
 import hashlib
 import os
@@ -35,8 +38,8 @@ sys.path.insert(0, REPO)
 from dfssm.synth import config_2p7b, make_prompts, make_weights  # noqa: E402
 from oracle import oracle as O  # noqa: E402
 
-OUT = os.path.join(HERE, "oracle_2p7b_64layer_b4.npz")
-B, T, N_NEW = 4, 129, 4
+N_NEW = 4
+PROMPT_TOKENS = {4: 129, 64: 17}
 
 
 def sha(a: np.ndarray) -> str:
@@ -44,6 +47,12 @@ def sha(a: np.ndarray) -> str:
 
 
 def main():
+    import argparse
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--batch", type=int, default=4, choices=sorted(PROMPT_TOKENS))
+    B = ap.parse_args().batch
+    T = PROMPT_TOKENS[B]
+    OUT = os.path.join(HERE, f"oracle_2p7b_64layer_b{B}.npz")
     t0 = time.time()
     w = make_weights(config_2p7b(), seed=0)
     prompt = make_prompts(B, w.cfg.vocab_size, T)

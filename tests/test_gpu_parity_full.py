@@ -233,13 +233,15 @@ def test_generate_wide_prefill_vs_oracle(case):
     gpu.check_errors()
 
 
-def test_config4_full_depth_vs_oracle_fixture():
-    """The whole config-4 model (2.7B shape, 64 layers, vocabulary 50288; bench.py's weights) at
-    batch 4 against the oracle's run committed in tests/golden/oracle_2p7b_64layer_b4.npz
-    (tests/golden/make_config4_golden.py): a 129-token prompt prefilled in two chunks of 64 tokens
-    (256 rows each: the wide kernels and a chunk boundary), 4 greedy tokens, then one more step:
-    tokens identical, and the SHA-256 of its fp16 logits, of the fp32 SSM state and of the conv
-    state equal to the oracle's."""
+@pytest.mark.parametrize("B,chunk_rows", [(4, 256), (64, 512)])
+def test_config4_full_depth_vs_oracle_fixture(B, chunk_rows):
+    """The whole config-4 model (2.7B shape, 64 layers, vocabulary 50288; bench.py's weights)
+    against the oracle's runs committed in tests/golden/oracle_2p7b_64layer_b{4,64}.npz
+    (tests/golden/make_config4_golden.py): at batch 4 a 129-token prompt prefilled in two chunks of
+    64 tokens, at batch 64 (the benchmark's batch) a 17-token prompt in two chunks of 8 tokens
+    (256 and 512 rows per chunk: the wide kernels and a chunk boundary), 4 greedy tokens, then one
+    more step: tokens identical, and the SHA-256 of its fp16 logits, of the fp32 SSM state and of
+    the conv state equal to the oracle's."""
     import hashlib
     import os
     from dfssm.synth import config_2p7b
@@ -247,12 +249,12 @@ def test_config4_full_depth_vs_oracle_fixture():
     def sha(a):
         return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
-    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oracle_2p7b_64layer_b4.npz"))
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"oracle_2p7b_64layer_b{B}.npz"))
     w = make_weights(config_2p7b(), seed=0)
-    B = g["prompt"].shape[0]
-    print("config 4 full depth (64 layers) vs oracle fixture, batch 4", flush=True)
+    assert g["prompt"].shape[0] == B
+    print(f"config 4 full depth (64 layers) vs oracle fixture, batch {B}", flush=True)
     gpu = DFSSMModel.from_weights(w, device=DEV, batch_size=B)
-    gpu.PREFILL_MAX_ROWS = 256
+    gpu.PREFILL_MAX_ROWS = chunk_rows
     got = gpu.generate(n_tokens=g["tokens"].shape[1], prompt=torch.from_numpy(g["prompt"]), return_tokens=True,
                        verbose=False)
     np.testing.assert_array_equal(got.cpu().numpy(), g["tokens"])
