@@ -133,9 +133,11 @@ struct FusedLds {
 // Every field is a raw load (each in its own register), made unconditionally from clamped
 // indices and used only in the epilogue: loads complete in issue order, so converting or
 // packing a loaded value here (or a load inside a branch, whose join waits for all loads) would
-// make the workgroup wait for the weight stream before its prologue starts.
+// make the workgroup wait for the weight stream before its prologue starts. The epilogue makes
+// the fields opaque before it converts them, so that the compiler cannot move the conversions
+// up to the loads.
 struct EpiRow {
-  uint32_t cw01, cw23;
+  u32x2 cw;  // conv weights 0 | 1 << 16, 2 | 3 << 16: one 64-bit load, kept as one register pair
   float bias, alog;          // dt rows: dt_bias and A_log of the head (A = -exp(A_log) later)
   int la;                    // LoRA A[n][s]
   uint32_t ws, as, cs01, cs2, cb, xres;  // cs01: conv state words 0 | 1 << 16, one (unaligned) load
@@ -180,10 +182,12 @@ __device__ __forceinline__ void load_pin(PIn<M>& pi, const uint16_t* act, int K,
 __device__ __forceinline__ void load_bits(u32x4 (&wb)[kFMaxCPW], const uint32_t* bits, int grp, int K) {
   const int lane = tix() & 63, wave = tix() >> 6, CH = K / 128;
   const u32x4* b = (const u32x4*)bits + (size_t)grp * CH * 64 + lane;
+  // chunks past the row's end are left unset (the GEMV skips them): with a zero default the
+  // compiler may copy a loaded value at the branch join, waiting there for every load
 #pragma unroll
   for (int j = 0; j < kFMaxCPW; ++j) {
     const int c = wave + kFW * j;
-    wb[j] = c < CH ? ld_nt(b + (size_t)c * 64) : u32x4{0u, 0u, 0u, 0u};
+    if (c < CH) wb[j] = ld_nt(b + (size_t)c * 64);
   }
 }
 
@@ -196,9 +200,9 @@ __device__ __forceinline__ void load_bits_rg(u32x2 (&wb)[kCR<RG>], const uint32_
   const u32x4* b = (const u32x4*)bits + (size_t)(grp / (64 / RG)) * CH * 64 + (grp % (64 / RG)) * RG + lane % RG;
 #pragma unroll
   for (int j = 0; j < kCR<RG>; ++j) {
-    const int cu = (64 / RG) * wave + lane / RG + (kFT / RG) * j;
-    wb[j] = cu < 2 * CH ? __builtin_nontemporal_load((const u32x2*)(b + (size_t)(cu >> 1) * 64) + (cu & 1))
-                        : u32x2{0u, 0u};
+    // unconditional, from a clamped half-chunk (the GEMV skips cu >= 2 CH): no branch join
+    const int cu = (64 / RG) * wave + lane / RG + (kFT / RG) * j, cc = cu < 2 * CH ? cu : 2 * CH - 1;
+    wb[j] = __builtin_nontemporal_load((const u32x2*)(b + (size_t)(cc >> 1) * 64) + (cc & 1));
   }
 }
 
@@ -222,14 +226,15 @@ __device__ __forceinline__ EpiRow load_epi(const FusedArgs& a, int grp) {
     __builtin_memcpy(&e.cs01, cs, 4);
     e.cs2 = cs[2];
     const uint32_t* wc = (const uint32_t*)(a.conv_w + (size_t)ch * 4);
-    e.cw01 = wc[0]; e.cw23 = wc[1];
+    e.cw = *(const u32x2*)wc;
     e.cb = a.conv_b[ch];
     e.bias = a.dt_bias[dtr];
     e.alog = a.A_log[dtr];
     e.xres = 0u;
   } else {
     e.xres = a.x[(size_t)m * a.D + n];
-    e.cs01 = e.cs2 = e.cw01 = e.cw23 = e.cb = 0u;
+    e.cs01 = e.cs2 = e.cb = 0u;
+    e.cw = u32x2{0u, 0u};
     e.bias = e.alog = 0.0f;
   }
   return e;
@@ -564,7 +569,12 @@ __device__ __forceinline__ void lora_finish(FusedLds<M>& L, const uint32_t* hsrc
 // finalizes sequence m. IN: z rows store the gate z sigma(z), x/B/C rows conv + SiLU, dt rows
 // softplus dt and exp(dt A) (as tagged fp32 words); OUT: the residual add into x.
 template <int M, bool IN, int RG = 64>
-__device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er, int grp, uint32_t tag) {
+__device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& er_in, int grp, uint32_t tag) {
+  // the inputs, opaque from here on: the compiler otherwise hoists their conversions to right
+  // after the loads at the kernel start and waits there for them
+  EpiRow er = er_in;
+  asm volatile("" : "+v"(er.cw), "+v"(er.bias), "+v"(er.alog), "+v"(er.la), "+v"(er.ws),
+               "+v"(er.as), "+v"(er.cs01), "+v"(er.cs2), "+v"(er.cb), "+v"(er.xres));
   ConvPend cp{nullptr, 0, 0, 0};
   const int tid = tix(), s = tid & 15, j = tid >> 4;
   const int N = IN ? a.IPO : a.D;
@@ -596,10 +606,10 @@ __device__ ConvPend epilogue(FusedLds<M>& L, const FusedArgs& a, const EpiRow& e
       const uint16_t xo = f2h(out);
       cp = ConvPend{a.conv + ((size_t)m * a.C + ch) * 3, (uint16_t)(er.cs01 >> 16), (uint16_t)er.cs2, xo};
       const float xv = h2f(xo);
-      float o = h2f((uint16_t)er.cs01) * h2f((uint16_t)er.cw01);
-      o = o + h2f((uint16_t)(er.cs01 >> 16)) * h2f((uint16_t)(er.cw01 >> 16));
-      o = o + h2f((uint16_t)er.cs2) * h2f((uint16_t)er.cw23);
-      o = o + xv * h2f((uint16_t)(er.cw23 >> 16));
+      float o = h2f((uint16_t)er.cs01) * h2f((uint16_t)er.cw[0]);
+      o = o + h2f((uint16_t)(er.cs01 >> 16)) * h2f((uint16_t)(er.cw[0] >> 16));
+      o = o + h2f((uint16_t)er.cs2) * h2f((uint16_t)er.cw[1]);
+      o = o + xv * h2f((uint16_t)(er.cw[1] >> 16));
       o = o + h2f((uint16_t)er.cb);
       const float sig = 1.0f / (1.0f + dev_expf(-o));
       out = o * sig;
@@ -753,8 +763,11 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   const uint32_t* hC_mine = hC + (wg % kXRep) * kHStride;
 
   // ---- loads that do not depend on the activations ----
+  // Set and used on the phase-A path only: no default value, which the compiler would merge with
+  // the loaded values at the branch join (folding the epilogue's conversions into the join, right
+  // after the loads, and waiting there for them).
   u32x4 wa[kFMaxCPW];
-  EpiRow ea = {};
+  EpiRow ea;
   PIn<M> pa;
   if (wg < gA) {  // x first: the prologue needs it before the weights
     load_pin<M, false>(pa, a.x, a.D, a.ln_w);
@@ -767,6 +780,10 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   const f32x2 h0 = __builtin_nontemporal_load((const f32x2*)state_row(a, item_of(a, wg < items ? wg : items - 1)));
 
   // ---- phase A: in_proj (workgroups < gA), LoRA ranks (gA .. gA + 15) ----
+  // The launch's tag, derived once on every path (after its first polls' loads on the GEMV path):
+  // a tag derived after the paths join made the compiler wait for the epoch load there, on the
+  // path that had already waited for it too, i.e. for phase A's device-scope stores.
+  uint32_t tag;
   if (wg < gA) {
     {
       u32x4 xn[M];
@@ -777,35 +794,26 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
     }
     lds_barrier();  // q published
     TL(1);
-    for (int grp = wg; grp < gA; grp += G) {
-      if (grp != wg) {
-        load_bits(wa, a.in_bits, grp, a.D);
-        ea = load_epi<M, true>(a, grp);
-      }
+    {  // one 64-row group per workgroup (the plan keeps gA + 16 <= G)
       const uint32_t hv = lora_issue(hA_mine, M);
       gemv_partials<M>(L, wa, a.D);
       TL(2);
-      const uint32_t tag = tag_now();
+      tag = tag_now();
       lora_finish<M>(L, hA_mine, hv, tag, a.err);
       lds_barrier();
       TL(3);
-      store_conv(epilogue<M, true>(L, a, ea, grp, tag));
+      store_conv(epilogue<M, true>(L, a, ea, wg, tag));
       TL(4);
       lds_barrier();
     }
   } else if (wg < gA + DFSSM_LORA_R) {
-    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag_now(), a.err, 0u);
+    tag = tag_now();
+    lora_rank<M, false>(L, a.x, nullptr, a.D, a.ln_w, a.in_lBq, wg - gA, hA, tag, a.err, 0u);
     TL(4);
+  } else {
+    tag = tag_now();
   }
   // ---- phase B: SSM + gate ----
-  u32x4 wc[RC < 64 ? 1 : kFMaxCPW];
-  u32x2 wcr[kCR<32>];
-  EpiRow ec = {};
-  if (wg < gC) {  // phase-C weights, loaded while phase B runs
-    if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, wg, a.DI);
-    else load_bits(wc, a.out_bits, wg, a.DI);
-    ec = load_epi<M, false, RC>(a, wg);
-  }
   const int nk = wg < items ? (items - 1 - wg) / G + 1 : 0;  // <= kItemsOf<M>
   if (nk > 0) {
     f32x2 hk[kItemsOf<M>];
@@ -819,9 +827,16 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
         dk[k] = a.Dp[t.head];
       }
     }
-    const uint32_t tag = tag_now();
     TL(5);
-    for (int k = 0; k < nk; ++k) poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
+    int k = 0;
+    do poll_item<M>(L, a, k, item_of(a, wg + k * G), tag);
+    while (++k < nk);
+    // Every wave waits here for its own loads and stores (the polling waves already have): the
+    // compiler's accounting then holds nothing pending past phase B, and no later register reuse
+    // waits on the state rows of items this workgroup does not own (loaded only when it does),
+    // which would also wait for phase B's device-scope stores. The barrier below waits for the
+    // polling waves, which see phase A's stores acknowledged first.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     lds_barrier();
     TL(6);
 #pragma unroll
@@ -832,25 +847,31 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
   TL(7);
   if (wg < gC) {
     lds_barrier();  // LDS reuse after phase A
+    // The weights, issued once this workgroup's SSM items are done: loads and stores complete in
+    // issue order, so a load issued before a poll holds back the poll's result (issued at phase B's
+    // start, their HBM round trip delayed the items' inputs). The gated output g arrives a poll
+    // round trip after the last item, about as long as these loads take. The epilogue inputs
+    // follow the polls of g: with them here, the compiler's wait before the polls (at most 10
+    // memory operations in flight) also waited for the SSM's state stores.
+    u32x4 wc[RC < 64 ? 1 : kFMaxCPW];
+    u32x2 wcr[kCR<32>];
+    if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, wg, a.DI);
+    else load_bits(wc, a.out_bits, wg, a.DI);
     PIn<M> pc;
+    EpiRow ec;
     load_pin<M, true>(pc, nullptr, a.DI, a.norm_w);
-    const uint32_t tag = tag_now();
     TL(8);
     {
       u32x4 xn[M];
       float mx[M];
       norm_rows<M, true>(L, pc, a.gT + (size_t)(wg % kGRep) * kGStride, a.DI, tag, a.err, xn, mx);
+      ec = load_epi<M, false, RC>(a, wg);
       TL(15);
       quantize_rows<M, 21>(L, xn, mx, a.DI);
     }
     lds_barrier();  // q published
     TL(9);
-    for (int grp = wg; grp < gC; grp += G) {
-      if (grp != wg) {
-        if constexpr (RC < 64) load_bits_rg<RC>(wcr, a.out_bits, grp, a.DI);
-        else load_bits(wc, a.out_bits, grp, a.DI);
-        ec = load_epi<M, false, RC>(a, grp);
-      }
+    {  // one RC-row group per workgroup (the plan keeps gC + 16 <= G)
       const uint32_t hv = lora_issue(hC_mine, M);
       if constexpr (RC < 64) gemv_partials_rg<M, RC>(L, wcr, a.DI);
       else gemv_partials<M>(L, wc, a.DI);
@@ -858,14 +879,14 @@ __global__ __launch_bounds__(kFT) void layer_fused_kernel(FusedArgs a) {
       lora_finish<M>(L, hC_mine, hv, tag, a.err);
       lds_barrier();
       TL(11);
-      (void)epilogue<M, false, RC>(L, a, ec, grp, tag);
+      (void)epilogue<M, false, RC>(L, a, ec, wg, tag);
       TL(12);
       lds_barrier();
     }
   } else if (wg < gC + DFSSM_LORA_R) {
     lds_barrier();
     lora_rank<M, true>(L, nullptr, a.gT + (size_t)(wg % kGRep) * kGStride, a.DI, a.norm_w, a.out_lBq, wg - gC, hC,
-                       tag_now(), a.err, tag_now());
+                       tag, a.err, tag);
     TL(12);
   }
   lds_barrier();  // every wave has read the launch count
