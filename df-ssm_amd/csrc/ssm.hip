@@ -23,8 +23,16 @@ namespace dfssm {
 
 // One (sequence m, head, 16-row block) of the step. TAGGED: g goes to gT as tagged words
 // (tag << 16) | fp16 with device-scope stores, and no sum(g^2) slot is written.
+// The tag of a launch whose workgroup launch count is `epoch`, derived where it is used: the empty
+// asm keeps the compiler from deriving it at the kernel start, where it waited for the count's
+// device-scope round trip (~1 us) before issuing any other load.
+__device__ __forceinline__ uint32_t tag_of(uint32_t epoch) {
+  asm volatile("" : "+v"(epoch));
+  return (epoch + 1u) & 0xffffu;
+}
+
 template <bool GATE, bool TAGGED>
-__device__ __forceinline__ void ssm_rows(const SsmArgs& a, int bx, int m, uint32_t* gT, uint32_t tag) {
+__device__ __forceinline__ void ssm_rows(const SsmArgs& a, int bx, int m, uint32_t* gT, uint32_t epoch) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int pblocks = a.P / 16;
   const int head = bx / pblocks;
@@ -94,6 +102,7 @@ __device__ __forceinline__ void ssm_rows(const SsmArgs& a, int bx, int m, uint32
     }
     if (TAGGED) {
       uint32_t* gp = gT + (size_t)m * DI + head * a.P + p;
+      const uint32_t tag = tag_of(epoch);
       st_dev(gp, (tag << 16) | f2h(o0));
       st_dev(gp + 8, (tag << 16) | f2h(o1));
     } else {
@@ -150,7 +159,7 @@ __device__ __forceinline__ bool sp_tag_ok(uint64_t v, uint32_t tag) {
 
 // Sixteen prologue workgroups per row, one LoRA rank rr each.
 template <int NJ>
-__device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int m, uint32_t tag) {
+__device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int m, uint32_t epoch) {
   __shared__ __attribute__((aligned(16))) uint32_t xn2[kSpMaxK / 2];  // g, then xn, as fp16 pairs
   __shared__ double red_d[4], red_h[4];
   __shared__ float red_f[4];
@@ -160,17 +169,20 @@ __device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int
   // (columns 2u, 2u + 1): every wave-wide load below is contiguous, and the loads of one thread are
   // 512 bytes apart (immediate offsets of one address). Norm weights, LoRA-B bytes and scale
   // first (loaded after the wait, they cost a cache round trip at the end of the launch), then
-  // the tagged g words.
-  const int8_t* lb = a.lB ? a.lB + (size_t)rr * K : nullptr;
+  // the tagged g words. All of them unconditional and raw until the polls are done: a select or a
+  // conversion of a loaded value before the poll loop made the workgroup wait for these loads
+  // before its first poll (without LoRA the bytes come from the norm weights, scaled by zero).
+  const int8_t* lb = a.lB ? a.lB + (size_t)rr * K : (const int8_t*)a.norm_w;
+  const uint16_t* lbs = a.lB ? a.lBs + rr : (const uint16_t*)a.norm_w;
   float2 wv[NJ];
   uint32_t bv[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int u = 64 * (NJ * w + j) + lane;
     wv[j] = *(const float2*)(a.norm_w + 2 * u);
-    bv[j] = lb ? *(const uint16_t*)(lb + 2 * u) : 0u;
+    bv[j] = *(const uint16_t*)(lb + 2 * u);
   }
-  const float bs = a.lB ? h2f(a.lBs[rr]) : 0.0f;
+  const uint16_t bs_raw = *lbs;
   const uint64_t* gp = (const uint64_t*)(a.gT + (size_t)m * K) + 64 * NJ * w + lane;
   // every round reloads all NJ words (each round's values are new definitions, so the registers
   // of one copy suffice; the extra loads of a round are a few KiB)
@@ -179,6 +191,7 @@ __device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int
   for (uint32_t it = 0;; ++it) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) gv[j] = ld_dev(gp + 64 * j);
+    const uint32_t tag = tag_of(epoch);  // after the loads: waits for the launch count only
     bool good = true;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) good = good && sp_tag_ok(gv[j], tag);
@@ -189,6 +202,7 @@ __device__ __forceinline__ void gated_prologue(const SsmPrepArgs& a, int rr, int
     }
     __builtin_amdgcn_s_sleep(1);
   }
+  const float bs = a.lB ? h2f(bs_raw) : 0.0f;
   // g pairs to this thread's own LDS slots (read back, then overwritten with xn, by this thread
   // alone), so the g registers are free before the norm pass
   double part = 0.0;
@@ -249,14 +263,13 @@ template <int NJ>
 __global__ __launch_bounds__(256) void ssm_prep_kernel(SsmPrepArgs a, int M) {
   const int nsb = a.s.H * (a.s.P / 16), bx = blockIdx.x;
   uint32_t* cnt = a.launches + bx;
-  const uint32_t epoch = ld_dev(cnt);
-  const uint32_t tag = (epoch + 1u) & 0xffffu;
+  const uint32_t epoch = ld_dev(cnt);  // the tag (tag_of) is derived where it is used
   if (bx < nsb * M) {
     const int m = bx / nsb;
-    ssm_rows<true, true>(a.s, bx - m * nsb, m, a.gT, tag);
+    ssm_rows<true, true>(a.s, bx - m * nsb, m, a.gT, epoch);
   } else {
     const int j = bx - nsb * M;
-    gated_prologue<NJ>(a, j % DFSSM_LORA_R, j / DFSSM_LORA_R, tag);
+    gated_prologue<NJ>(a, j % DFSSM_LORA_R, j / DFSSM_LORA_R, epoch);
   }
   lds_barrier();  // every wave has read the count (and used its tag) before it is advanced
   if (threadIdx.x == 0) *cnt = epoch + 1u;  // read by the next launch only: a plain store suffices
