@@ -26,6 +26,14 @@ __device__ __forceinline__ void st_dev(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The tag of a launch whose workgroup launch count is `epoch`, derived where it is used: the empty
+// asm keeps the compiler from deriving it at the kernel start, where it waited for the count's
+// device-scope round trip (~1 us) before issuing any other load.
+__device__ __forceinline__ uint32_t tag_of(uint32_t epoch) {
+  asm volatile("" : "+v"(epoch));
+  return (epoch + 1u) & 0xffffu;
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(f16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }  // RNE
 __device__ __forceinline__ float r16(float f) { return (float)(f16)f; }  // round through fp16

@@ -61,34 +61,38 @@ constexpr int kProPF = 4;   // 16-byte prefetch vectors per thread of the next l
 __device__ __forceinline__ bool pro_tag_ok(uint64_t v, uint32_t tag) {
   return ((uint32_t)v >> 16) == tag && ((uint32_t)(v >> 32) >> 16) == tag;
 }
-__device__ __forceinline__ void gemm_in_prologue(const GemmPro& p, int D, int m, int k, uint32_t tag, uint32_t* xn2) {
+__device__ __forceinline__ void gemm_in_prologue(const GemmPro& p, int D, int m, int k, uint32_t epoch, uint32_t* xn2) {
   __shared__ double pr_d[16];
   __shared__ float pr_f[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int np = D / 2, nbq = D / 32;  // column pairs; 8-column blocks per quarter
   const int rr = kProPW * k + (w >> 2), c0 = (w & 3) * (D / 4);
   // norm weights of this thread's pairs u = tid + 1024 j and the LoRA-B bytes of rank rr over the
-  // wave's quarter first, then x
+  // wave's quarter first, then x. Unconditional (clamped pairs and blocks, unused past the end;
+  // without LoRA the bytes come from the norm weights, scaled by zero) and raw until the polls are
+  // done: a select or a conversion of a loaded value before the poll loop made the workgroup wait
+  // for these loads before its first poll.
   float2 wv[kProPJ];
 #pragma unroll
   for (int j = 0; j < kProPJ; ++j) {
     const int u = tid + 1024 * j;
-    wv[j] = u < np ? *(const float2*)(p.norm_w + 2 * u) : make_float2(0.0f, 0.0f);
+    wv[j] = *(const float2*)(p.norm_w + 2 * (u < np ? u : np - 1));
   }
-  const int8_t* lb = p.lB ? p.lB + (size_t)rr * D + c0 : nullptr;
+  const int8_t* lb = p.lB ? p.lB + (size_t)rr * D + c0 : (const int8_t*)p.norm_w;
   uint2 bq[kProBI];
 #pragma unroll
   for (int i = 0; i < kProBI; ++i) {
     const int b = 64 * i + lane;
-    bq[i] = (lb && b < nbq) ? *(const uint2*)(lb + 8 * b) : uint2{0u, 0u};
+    bq[i] = *(const uint2*)(lb + 8 * (b < nbq ? b : nbq - 1));
   }
-  const float bs = p.lB ? h2f(p.lBs[rr]) : 0.0f;
+  const uint16_t bs_raw = *(p.lB ? p.lBs + rr : (const uint16_t*)p.norm_w);
   const uint64_t* xp = (const uint64_t*)(p.xT + (size_t)m * D) + tid;
   uint64_t xv[kProPJ];
 #pragma nounroll
   for (uint32_t it = 0;; ++it) {
 #pragma unroll
     for (int j = 0; j < kProPJ; ++j) xv[j] = tid + 1024 * j < np ? ld_dev(xp + 1024 * j) : 0ull;
+    const uint32_t tag = tag_of(epoch);  // after the loads: waits for the launch count only
     bool good = true;
 #pragma unroll
     for (int j = 0; j < kProPJ; ++j) good = good && (tid + 1024 * j >= np || pro_tag_ok(xv[j], tag));
@@ -99,6 +103,7 @@ __device__ __forceinline__ void gemm_in_prologue(const GemmPro& p, int D, int m,
     }
     __builtin_amdgcn_s_sleep(1);
   }
+  const float bs = p.lB ? h2f(bs_raw) : 0.0f;
   double part = 0.0;
 #pragma unroll
   for (int j = 0; j < kProPJ; ++j) {
@@ -183,15 +188,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const GemmPro& p) {
   uint32_t epoch = 0;
   if constexpr (PRO) {
     cnt = p.launches + (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+    // Every thread, from a per-lane (vector) address, on both paths: loaded by thread 0 alone,
+    // the value was moved at the branch join right after the load, and the workgroup waited there
+    // for the count's device-scope round trip before loading its tile (a uniform address becomes a
+    // scalar load, which the first LDS access would wait for); one load for both paths also keeps
+    // the GEMM path from reusing its register while it is pending (a wait amid the tile's loads).
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    epoch = ld_dev(cnt + z);
     if ((int)blockIdx.y >= p.gy) {  // prologue workgroups
       const int pi = ((int)blockIdx.y - p.gy) * (int)gridDim.x + (int)blockIdx.x;
-      const uint32_t ep = ld_dev(cnt);
-      if (pi < kProPW * a.M) gemm_in_prologue(p, a.N, pi / kProPW, pi % kProPW, (ep + 1u) & 0xffffu, (uint32_t*)qs);
+      if (pi < kProPW * a.M) gemm_in_prologue(p, a.N, pi / kProPW, pi % kProPW, epoch, (uint32_t*)qs);
       lds_barrier();  // every wave has used its tag before the count is advanced
-      if (tid == 0) *cnt = ep + 1u;  // read by the next launch only: a plain store suffices
+      if (tid == 0) *cnt = epoch + 1u;  // read by the next launch only: a plain store suffices
       return;
     }
-    if (tid == 0) epoch = ld_dev(cnt);
   }
   const int rt = wave % RT, kq = wave / RT, j = lane >> 4;
   const int g = blockIdx.x;

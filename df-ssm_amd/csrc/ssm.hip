@@ -23,14 +23,6 @@ namespace dfssm {
 
 // One (sequence m, head, 16-row block) of the step. TAGGED: g goes to gT as tagged words
 // (tag << 16) | fp16 with device-scope stores, and no sum(g^2) slot is written.
-// The tag of a launch whose workgroup launch count is `epoch`, derived where it is used: the empty
-// asm keeps the compiler from deriving it at the kernel start, where it waited for the count's
-// device-scope round trip (~1 us) before issuing any other load.
-__device__ __forceinline__ uint32_t tag_of(uint32_t epoch) {
-  asm volatile("" : "+v"(epoch));
-  return (epoch + 1u) & 0xffffu;
-}
-
 template <bool GATE, bool TAGGED>
 __device__ __forceinline__ void ssm_rows(const SsmArgs& a, int bx, int m, uint32_t* gT, uint32_t epoch) {
   const int tid = threadIdx.x, lane = tid & 63;
